@@ -1,0 +1,254 @@
+"""Benchmark: C2C complex64 GB/s and % of HBM peak, N = 2^10..2^20, plus the
+p50 latency at N=2048 B=1 (BASELINE.json metric), on one MI355X.
+
+One step = one forward C2C complex64 transform (through the public plan API:
+``plan_fft`` with the device profile -> ``execute_fft_plan``) of every size
+N = 2^10 .. 2^20 at B = max(64, 2^25 / N) rows -- 256 MiB in and 256 MiB out
+per size, larger than the 256 MB Infinity Cache.  Inputs are synthetic
+(iid N(0,1) real/imag parts from a fixed device-side seed) and resident in
+HBM before the timed region.  ``value`` = algorithmic bytes of all K steps
+(16*N*B per transform) / timed wall time, in GB/s.
+
+Also reported (on the same JSON line):
+* ``roofline``: the dominant kernel (largest share of a step), its algorithmic
+  bytes per launch over its mean launch duration (HIP events on the stream the
+  kernel runs on), against 8 TB/s; ``traffic`` from the committed rocprofv3
+  PMC summary (profiles/pmc_traffic.json) when present, else null;
+* ``per_size``: GB/s, fraction of peak and GFLOP/s (5 N log2 N per transform)
+  per N, from HIP events;
+* ``latency_n2048_b1``: the reference protocol (warmup 5, 5 x 32 trials,
+  device sync per trial, pooled p50, scripts/issue10_wp3_holdout.py:176-190)
+  for execute_fft_plan, plus the kernel-only event p50;
+* ``config2``: latency and GB/s of BASELINE config 2 (N in {1024, 2048}, B in
+  {16, 64});
+* ``cpu_baseline``: the reference's own CPU FFT (butterfly::fft_dit built
+  into oracle/_ref; the C restatement when that build is absent) on one core,
+  on a bounded sample -- one transform of each N = 2^10..2^20 -- median of 3.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_GBPS = 8000.0
+SIZES = [1 << k for k in range(10, 21)]
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def batch_for(n: int) -> int:
+    return max(64, (1 << 25) // n)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU: every box here has one MI355X; "
+                                   "the batch shards across GPUs with no exchange (see DESIGN.md), "
+                                   "but multi-GPU runs are not part of this benchmark",
+                          "n_gpus": args.gpus}))
+        return 2
+
+    import numpy as np
+    import torch
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    from kunlunxin_fft_amd import native
+    from kunlunxin_fft_amd.entry import _resolve
+
+    if not torch.cuda.is_available():
+        log("bench.py needs a ROCm GPU")
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(0)
+    prof = pkg.DeviceProfile.load().hash()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(102026)
+
+    # ---- inputs resident in HBM, plans resolved once (plan reuse)
+    work = []
+    for n in SIZES:
+        b = batch_for(n)
+        x = torch.randn((b, n), dtype=torch.complex64, device=dev, generator=gen) * math.sqrt(2.0)
+        plan = pkg.plan_fft("dit", n, batch=b, profile_hash=prof)
+        work.append((n, b, x, plan))
+        log(f"size N={n} B={b} executed={plan.executed} fallback={plan.fallback}")
+    torch.cuda.synchronize()
+
+    def step():
+        for _, _, x, plan in work:
+            pkg.execute_fft_plan(plan, x)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    step_bytes = sum(16 * n * b for n, b, _, _ in work)
+    wall = t1 - t0
+    value = step_bytes * args.steps / wall / 1e9
+    ms_per_step = wall / args.steps * 1e3
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, {value:.1f} GB/s")
+
+    # ---- per size: event time of one execute, and per-launch durations
+    per_size = []
+    kernels = {}  # (flow, n, launch index) -> [ms]
+    stream = torch.cuda.current_stream(dev)
+    for n, b, x, plan in work:
+        nplan, (shape, dt) = _resolve(plan, 0)
+        out = torch.empty(shape, dtype=dt, device=dev)
+        evs = []
+        for _ in range(10):
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record(stream)
+            nplan.execute(x.data_ptr(), out.data_ptr(), stream.cuda_stream)
+            e.record(stream)
+            evs.append((s, e))
+        torch.cuda.synchronize()
+        ms = statistics.median(s.elapsed_time(e) for s, e in evs)
+        launches = []
+        for _ in range(5):
+            launches.append(nplan.execute_timed(x.data_ptr(), out.data_ptr(), stream.cuda_stream))
+        per_launch = [statistics.median(col) for col in zip(*launches)]
+        for i, t in enumerate(per_launch):
+            kernels[(nplan.flow_name, n, b, i, len(per_launch))] = t
+        gbps = 16 * n * b / (ms * 1e-3) / 1e9
+        per_size.append({
+            "n": n, "batch": b, "executed": plan.executed, "flow": nplan.flow_name,
+            "fallback": plan.fallback, "launches": len(per_launch),
+            "ms": round(ms, 5), "gbps": round(gbps, 1), "frac_hbm": round(gbps / PEAK_GBPS, 4),
+            "gflops": round(5 * n * math.log2(n) * b / (ms * 1e-3) / 1e9, 1),
+            "launch_ms": [round(t, 5) for t in per_launch],
+            "split": [int(nplan.info.n1), int(nplan.info.n2)] if nplan.info.n1 else None,
+        })
+        log(f"N={n:>8} B={b:>6} {nplan.flow_name:>10} {ms:8.4f} ms {gbps:8.1f} GB/s "
+            f"({gbps / PEAK_GBPS:.1%}) launches={['%.4f' % t for t in per_launch]}")
+
+    # ---- dominant kernel: the launch with the largest share of a step
+    (dflow, dn, db, di, dk), dms = max(kernels.items(), key=lambda kv: kv[1])
+    d_bytes = 16 * dn * db  # every pass of every flow reads and writes all B*N elements once
+    d_ach = d_bytes / (dms * 1e-3) / 1e9
+    kname = {"lds-fused": "lds_fft_kernel", "four-step": "fourstep_pass_kernel"}.get(dflow, dflow)
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    key = f"{dflow}:N={dn}:B={db}:launch={di}"
+    if os.path.exists(tpath):
+        try:
+            traffic = json.load(open(tpath)).get(key)
+        except (OSError, ValueError):
+            traffic = None
+    roofline = {"bound": "hbm", "achieved": round(d_ach, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                "frac": round(d_ach / PEAK_GBPS, 4), "traffic": traffic,
+                "kernel": f"{kname} ({dflow}, N={dn}, B={db}, launch {di + 1}/{dk})",
+                "algorithmic_bytes_per_launch": d_bytes, "mean_launch_ms": round(dms, 5)}
+
+    # ---- latency at N=2048 B=1 (reference protocol) and config 2
+    def latency(n, b):
+        rng = np.random.default_rng(102026 + 10 * n + b)
+        h = (rng.standard_normal((b, n)) + 1j * rng.standard_normal((b, n))).astype(np.complex64)
+        x = torch.from_numpy(h[0] if b == 1 else h).to(dev)
+        plan = pkg.plan_fft("dit", n, batch=b, profile_hash=prof)
+        for _ in range(5):
+            pkg.execute_fft_plan(plan, x)
+        torch.cuda.synchronize()
+        wall = []
+        for _ in range(5):
+            for _ in range(32):
+                a = time.perf_counter()
+                pkg.execute_fft_plan(plan, x)
+                torch.cuda.synchronize()
+                wall.append((time.perf_counter() - a) * 1e3)
+        nplan, (shape, dt) = _resolve(plan, 0)
+        out = torch.empty(shape, dtype=dt, device=dev)
+        evs = []
+        for _ in range(100):
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record(stream)
+            nplan.execute(x.data_ptr(), out.data_ptr(), stream.cuda_stream)
+            e.record(stream)
+            evs.append((s, e))
+        torch.cuda.synchronize()
+        ev = statistics.median(s.elapsed_time(e) for s, e in evs)
+        p50 = statistics.median(wall)
+        return {"n": n, "batch": b, "executed": plan.executed, "api_wall_p50_ms": round(p50, 5),
+                "kernel_event_p50_ms": round(ev, 5),
+                "api_gbps": round(16 * n * b / (p50 * 1e-3) / 1e9, 3)}
+
+    lat = latency(2048, 1)
+    log(f"latency N=2048 B=1: {lat}")
+    cfg2 = [latency(n, b) for n in (1024, 2048) for b in (16, 64)]
+    for c in cfg2:
+        log(f"config2: {c}")
+
+    # ---- CPU baseline (reference CPU path, 1 core, bounded sample)
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle  # the reference CPU path / its restatement, timed as the baseline
+
+        rng = np.random.default_rng(7)
+        tot_s, tot_bytes, kinds = 0.0, 0, set()
+        for n in SIZES:
+            h = rng.standard_normal(n) + 1j * rng.standard_normal(n)
+            s, kind = oracle.time_cpu_fft(h, threads=1, reps=3)
+            kinds.add(kind)
+            tot_s += s
+            tot_bytes += 16 * n
+        cpu = {"value": round(tot_bytes / tot_s / 1e9, 4), "unit": "GB/s", "cores": 1,
+               "kind": "reference" if kinds == {"reference"} else "port",
+               "sample": "one transform of each N = 2^10..2^20 (11 transforms, complex<double>, "
+                         "butterfly::fft_dit with its per-stage twiddle rebuild), median of 3, "
+                         f"{tot_s:.2f} s per pass; host has {os.cpu_count()} CPUs",
+               "gpu_over_cpu": round(value / (tot_bytes / tot_s / 1e9), 1)}
+        log(f"cpu baseline: {cpu}")
+
+    line = {
+        "metric": "C2C complex64 GB/s & % HBM peak, N=2^10-2^20; p50 latency N=2048 B=1",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "complex64 (fp32)",
+        "data": "synthetic: iid N(0,1) real/imag parts, fixed device seed, resident in HBM",
+        "config": {"workload": "forward C2C complex64 via plan_fft/execute_fft_plan, "
+                               "N=2^10..2^20, B=max(64, 2^25/N) per N (256 MiB in + 256 MiB out "
+                               "per N); one step = all 11 sizes",
+                   "frac_hbm_of_value": round(value / PEAK_GBPS, 4)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "latency_n2048_b1": lat,
+        "config2": cfg2,
+        "per_size": per_size,
+    }
+    print(json.dumps(line), flush=True)
+    out_dir = os.path.join(ROOT, "gpurun_out")
+    if os.path.isdir(out_dir):
+        with open(os.path.join(out_dir, "bench_detail.json"), "w") as f:
+            json.dump(line, f, indent=1)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

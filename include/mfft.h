@@ -1,0 +1,168 @@
+/*
+ * mfft.h -- C ABI of the MI355X (gfx950) FFT operator library.
+ *
+ * The reference (TruNcat3/kunlunxin-fft) has no C ABI: its boundary is the
+ * Python plan API in src/xpu/entry.py.  Each entry point below replaces one
+ * piece of what that API does underneath, so that a host binding (the
+ * package's Python ctypes layer, or any C/C++/FFI caller) can keep the
+ * reference's plan/execute semantics:
+ *
+ *   mfft_plan_create   <- plan_fft(...) resolution + the runner's per-call
+ *                         twiddle build (entry.py:292-426, runner.py:93-97,
+ *                         1650-1658) and the 4-step plan caches
+ *                         (adapter_hybrid.py:60-108, entry.py:228-233)
+ *   mfft_execute       <- execute_fft_plan(plan, x) (entry.py:501-628) with
+ *                         the inverse conjugation, norm epilogue
+ *                         (entry.py:617-628, 656-668) and the dedicated real
+ *                         flows (entry.py:555-587) fused into the kernels
+ *   mfft_plan_destroy  <- dropping the plan / its cache entry (entry.py:631-653)
+ *   mfft_bit_reverse_permute
+ *                      <- runner.bit_reverse_permute (runner.py:1542-1552)
+ *   mfft_device_props  <- the device facts DeviceProfile / env fingerprint
+ *                         read (config.py:55-95, envcheck.py:62-88)
+ *   mfft_last_error    <- the exception message of the Python API; error
+ *                         classes map to ValueError / TypeError / RuntimeError
+ *                         (validate.py:19-68, context.py:52-56)
+ *
+ * Data layout: interleaved complex64 (float re, float im) for complex
+ * buffers, float32 for real ones, rows of a batch contiguous:
+ *   c2c  in [batch][n] complex64      -> out [batch][n] complex64
+ *   r2c  in [batch][n] float32        -> out [batch][n/2+1] complex64
+ *   c2r  in [batch][n/2+1] complex64  -> out [batch][n] float32
+ * (c2r ignores the imaginary parts of bins 0 and n/2, as torch.fft does).
+ *
+ * Ownership and threading: a plan owns its device twiddle tables and any
+ * workspace; mfft_execute allocates nothing and never synchronises the host.
+ * It enqueues on `stream` (a hipStream_t; NULL = the default stream) of the
+ * device that was current at plan creation, which must be current at
+ * execute.  `in` and `out` must not overlap; `in` is never written.
+ * Executes of one plan that overlap in time (two streams or two host threads)
+ * share the plan's workspace and race: serialise them, or create one plan per
+ * stream.
+ */
+#ifndef MFFT_H_
+#define MFFT_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MFFT_ABI_VERSION 1
+
+/* return codes (0 = success); the Python layer maps them to exceptions */
+enum {
+    MFFT_OK = 0,
+    MFFT_ERR_VALUE = 1,       /* bad size, enum, pointer, overlap -> ValueError */
+    MFFT_ERR_TYPE = 2,        /* reserved for dtype errors       -> TypeError  */
+    MFFT_ERR_RUNTIME = 3,     /* HIP failure, wrong device       -> RuntimeError */
+    MFFT_ERR_UNSUPPORTED = 4  /* flow cannot run this shape      -> ValueError */
+};
+
+/* transform_type: src/xpu/config.py:34 TRANSFORM_TYPES */
+enum { MFFT_C2C = 0, MFFT_R2C = 1, MFFT_C2R = 2 };
+/* transform_direction: config.py:35 */
+enum { MFFT_FORWARD = 0, MFFT_INVERSE = 1 };
+/* norm: config.py:36 NORMALIZATIONS, scales of entry.py:81-102 */
+enum { MFFT_NORM_NONE = 0, MFFT_NORM_FORWARD = 1, MFFT_NORM_BACKWARD = 2, MFFT_NORM_ORTHO = 3 };
+
+/* Kernel families (flow ids).  The first four keep the reference's global
+ * stage flows (one launch per stage, M0 / M5 of src/xpu/runner.py); the others
+ * are the MI355X flows that replace M1/M2/M3 and the hybrid 4-step. */
+enum {
+    MFFT_FLOW_AUTO = 0,        /* LDS_FUSED when the core fits one workgroup, else FOUR_STEP */
+    MFFT_FLOW_RADIX2_DIT = 1,  /* M0 fft_dit: bit reversal folded into stage 0 (runner.py:118-162) */
+    MFFT_FLOW_RADIX2_DIF = 2,  /* M0 fft_dif: bit reversal folded into the last stage (runner.py:165-206) */
+    MFFT_FLOW_RADIX4_DIT = 3,  /* M5 fft_dit_radix4: digit reversal folded into stage 0 (runner.py:1399-1470) */
+    MFFT_FLOW_RADIX4_DIF = 4,  /* M5 fft_dif_radix4 (runner.py:1473-1540) */
+    MFFT_FLOW_LDS_FUSED = 5,   /* one pass: whole transform resident in LDS/registers (core n <= 8192) */
+    MFFT_FLOW_FOUR_STEP = 6    /* two passes: column FFTs + twiddle, then row FFTs (core n >= 256) */
+};
+
+/* Flow parameters (params[i], all optional, 0 = library default):
+ *   RADIX2_* / RADIX4_*: params[0] = threads per block (64..1024, power of two)
+ *   LDS_FUSED:           params[0] = elements per thread (4, 8 or 16)
+ *   FOUR_STEP:           params[0] = n1 (column FFT length; n2 = core_n/n1),
+ *                        params[1] = batch rows per chunk (both passes run
+ *                                    chunk by chunk; 0 = whole batch) */
+#define MFFT_MAX_PARAMS 4
+
+typedef struct mfft_plan mfft_plan;
+
+typedef struct {
+    int64_t n, batch, core_n;     /* core_n: complex core length (n, or n/2 for r2c/c2r) */
+    int32_t transform_type, transform_direction, norm;
+    int32_t flow;                 /* resolved flow id (never MFFT_FLOW_AUTO) */
+    int32_t device;
+    int32_t launches;             /* kernel launches per mfft_execute */
+    int32_t elems_per_thread;     /* LDS_FUSED: elements per thread */
+    int32_t threads_per_block;
+    int64_t n1, n2, chunk_rows;   /* FOUR_STEP split */
+    int64_t workspace_bytes;      /* device scratch held by the plan */
+    int64_t table_bytes;          /* device twiddle tables held by the plan */
+    double scale;                 /* output scale applied in the final store */
+} mfft_plan_info;
+
+typedef struct {
+    char name[256];               /* hipDeviceProp_t::name */
+    char gcn_arch_name[256];      /* e.g. "gfx950:sramecc+:xnack-" */
+    int32_t multiprocessor_count; /* CUs */
+    int32_t warp_size;            /* 64 on CDNA */
+    int64_t shared_mem_per_block; /* LDS bytes a workgroup may use */
+    int64_t shared_mem_per_multiprocessor;
+    int64_t total_global_mem;
+    int32_t clock_rate_khz;
+    int32_t memory_clock_rate_khz;
+    int32_t memory_bus_width;
+    int32_t l2_cache_size;
+    int32_t driver_version;       /* hipDriverGetVersion */
+    int32_t runtime_version;      /* hipRuntimeGetVersion */
+    int32_t abi_version;          /* MFFT_ABI_VERSION */
+} mfft_device_props;
+
+/* Create a plan on the current device.  Validates everything before any
+ * allocation: n a power of two (c2c 1..2^20, r2c/c2r 2..2^20), batch >= 1,
+ * enums in range, r2c forward-only and c2r inverse-only (entry.py:157-172),
+ * and that `flow` can run the shape.  Uploads the twiddle tables and
+ * allocates the workspace (the only allocations the library makes). */
+int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_type,
+                     int transform_direction, int norm, int flow,
+                     const int32_t* params, int nparams);
+
+/* Enqueue one transform of all `batch` rows.  No allocation, no host sync. */
+int mfft_execute(const mfft_plan* plan, const void* in, void* out, void* stream);
+
+/* mfft_execute with a HIP event recorded on `stream` before the first and
+ * after every kernel launch (the profiling counterpart of the reference's
+ * phase ledger, src/xpu/ledger.py:262-296).  Waits for the stream, then
+ * writes the duration of each launch in milliseconds to launch_ms[0..k) with
+ * k = min(launches, cap) and stores k in *n_launches.  Same work and results
+ * as mfft_execute; creates and destroys its events (no device memory). */
+int mfft_execute_timed(const mfft_plan* plan, const void* in, void* out, void* stream,
+                       float* launch_ms, int cap, int* n_launches);
+
+/* Release the plan's device memory (synchronises its device first). NULL is a no-op. */
+int mfft_plan_destroy(mfft_plan* plan);
+
+/* Describe a plan (resolved flow, launch count, memory held). */
+int mfft_plan_query(const mfft_plan* plan, mfft_plan_info* info);
+
+/* out[r][bit_reverse(i)] = in[r][i] over `batch` rows of n complex64
+ * (runner.bit_reverse_permute, runner.py:1542-1552); n a power of two. */
+int mfft_bit_reverse_permute(const void* in, void* out, int64_t n, int64_t batch, void* stream);
+
+/* Device facts for the profile / environment fingerprint. */
+int mfft_device_props_get(int device, mfft_device_props* out);
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* mfft_last_error(void);
+
+/* MFFT_ABI_VERSION of the loaded library. */
+int mfft_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MFFT_H_ */

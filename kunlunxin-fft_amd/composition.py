@@ -1,0 +1,101 @@
+"""Exact-shape composition registry (reference src/xpu/composition.py).
+
+On the P800 the registry promoted one vendor-core 4-step composition
+(N=2048, B=16).  On MI355X the 4-step is a first-class kernel family chosen
+by the selector table itself, so no composition table ships: the lookup
+exists to keep the plan API's contract and fails closed -- it returns None
+unless a valid, profile- and environment-bound table is supplied.
+"""
+from __future__ import annotations
+
+import json
+import os
+
+from .config import CONFIG_DIR, ConfigError
+
+TABLE_PATH = os.path.join(CONFIG_DIR, "composition_table.json")
+KIND = "composition-promotion"
+TABLE_REQUIRED_KEYS = ("kind", "profile_hash", "env_hash", "precision", "guard_pct", "entries")
+ENTRY_REQUIRED_KEYS = ("N", "batch", "direction", "flow_id", "flow_realization",
+                       "processing_unit", "candidate_ms", "incumbent_ms", "guard_pct", "reason")
+
+
+def guard_pct_of(candidate_ms: float, incumbent_ms: float) -> float:
+    """Percent by which the candidate beats the incumbent (positive = faster)."""
+    return (incumbent_ms - candidate_ms) / incumbent_ms * 100.0
+
+
+def table_violations(table: dict) -> list[str]:
+    bad = [f"missing table key {k!r}" for k in TABLE_REQUIRED_KEYS if table.get(k) in (None, "")]
+    if bad:
+        return bad
+    if table["kind"] != KIND:
+        bad.append(f"kind {table['kind']!r} != {KIND!r}")
+    if not isinstance(table["entries"], list):
+        return bad + ["entries not a list"]
+    seen = set()
+    for i, e in enumerate(table["entries"]):
+        miss = [k for k in ENTRY_REQUIRED_KEYS if e.get(k) in (None, "")]
+        if miss:
+            bad.append(f"entry {i}: missing {miss}")
+            continue
+        key = (e["N"], e["batch"], e["direction"])
+        if key in seen:
+            bad.append(f"duplicate exact-shape key {key}")
+        seen.add(key)
+        g = guard_pct_of(float(e["candidate_ms"]), float(e["incumbent_ms"]))
+        if abs(g - float(e["guard_pct"])) > 1e-6:
+            bad.append(f"entry {key}: guard_pct does not match its medians")
+        if g < float(table["guard_pct"]):
+            bad.append(f"entry {key}: guard {g:.3f}% below {table['guard_pct']}%")
+    return bad
+
+
+def load_composition_table(path: str = TABLE_PATH):
+    """None when no table exists; ConfigError when one exists but is invalid."""
+    try:
+        with open(path) as f:
+            table = json.load(f)
+    except FileNotFoundError:
+        return None
+    except json.JSONDecodeError as e:
+        raise ConfigError(f"composition table unreadable: {path}: {e}") from None
+    if not isinstance(table, dict):
+        raise ConfigError(f"composition table is not an object: {path}")
+    v = table_violations(table)
+    if v:
+        raise ConfigError("composition table violates its contract: " + "; ".join(v[:8]))
+    return table
+
+
+def composition_select(direction: str, n: int, batch: int = 1, precision: str = "fp32",
+                       profile_hash: str | None = None, env_hash: str | None = "auto",
+                       table: dict | None = None, transform_type: str = "c2c",
+                       transform_direction: str = "forward",
+                       normalization: str = "backward"):
+    """Exact-shape composition entry, or None (fail closed on any mismatch)."""
+    if direction != "dit":
+        return None
+    if (transform_type, transform_direction, normalization) != ("c2c", "forward", "backward"):
+        return None
+    if table is None:
+        table = load_composition_table()
+        if table is None:
+            return None
+    if precision != table.get("precision"):
+        return None
+    if not profile_hash or profile_hash != table.get("profile_hash"):
+        return None
+    bound = table.get("env_hash") or ""
+    if not bound:
+        return None
+    if env_hash == "auto":
+        from .envcheck import current_env_hash
+
+        env_hash = current_env_hash()
+    if env_hash is None or env_hash != bound:
+        return None
+    for e in table.get("entries", ()):
+        if (e["N"], e["batch"], e["direction"]) == (n, batch, direction):
+            return e
+    return None

@@ -1,0 +1,164 @@
+"""Configuration loading (host-only: no torch import).
+
+Mirrors the reference's ``src/xpu/config.py`` contract -- ``ConfigError``,
+the semantic-key taxonomy, a ``DeviceProfile`` whose ``hash()`` binds a
+selector table to a device, and a ``DesignSpace`` that every table entry's
+parameters must come from -- with MI355X facts in place of the P800 ones.
+
+* ``DeviceProfile.hash()`` is sha256 of the sorted-key JSON of the profile,
+  first 16 hex digits (config.py:94-95 of the reference).
+* The JSON files live in this package's ``config/`` directory.
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+from dataclasses import asdict, dataclass
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+CONFIG_DIR = os.path.join(_PKG, "config")
+
+
+class ConfigError(ValueError):
+    """Raised when a config file is missing, unreadable, or fails its schema
+    (reference config.py:24-25)."""
+
+
+# Semantic key taxonomy (reference config.py:34-36).
+TRANSFORM_TYPES = ("c2c", "r2c", "c2r")
+TRANSFORM_DIRECTIONS = ("forward", "inverse")
+NORMALIZATIONS = ("none", "forward", "backward", "ortho")
+
+
+def _read_json(name: str) -> dict:
+    path = os.path.join(CONFIG_DIR, name)
+    if not os.path.exists(path):
+        raise ConfigError(f"missing config file: {path}")
+    with open(path) as f:
+        try:
+            return json.load(f)
+        except json.JSONDecodeError as e:
+            raise ConfigError(f"{path} is not valid JSON: {e}") from e
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ConfigError(msg)
+
+
+def _pow2_list(v) -> bool:
+    return (isinstance(v, list) and bool(v)
+            and all(isinstance(t, int) and t > 0 and (t & (t - 1)) == 0 for t in v))
+
+
+@dataclass(frozen=True)
+class DeviceProfile:
+    """Validated MI355X hardware profile (config/device.json).
+
+    Static facts only; the live runtime/driver binding is the separate
+    environment fingerprint (``envcheck``), as in the reference.
+    """
+
+    device: str
+    board: str
+    gfx_arch: str
+    compute_units: int
+    xcds: int
+    wavefront_size: int
+    lds_bytes_per_cu: int
+    hbm_gib: int
+    hbm_peak_gbps: int
+    device_code_path: str
+    torch_device_key: str
+    baseline: str
+    max_n: int
+
+    @staticmethod
+    def load() -> "DeviceProfile":
+        d = _read_json("device.json")
+        for key in ("device", "board", "gfx_arch", "device_code_path", "torch_device_key", "baseline"):
+            _require(isinstance(d.get(key), str) and d[key],
+                     f"device.json: {key} must be a non-empty string")
+        for key in ("compute_units", "xcds", "wavefront_size", "lds_bytes_per_cu", "hbm_gib",
+                    "hbm_peak_gbps", "max_n"):
+            _require(isinstance(d.get(key), int) and d[key] > 0,
+                     f"device.json: {key} must be a positive int")
+        return DeviceProfile(**{k: d[k] for k in DeviceProfile.__dataclass_fields__})
+
+    def hash(self) -> str:
+        return hashlib.sha256(json.dumps(asdict(self), sort_keys=True).encode()).hexdigest()[:16]
+
+
+@dataclass(frozen=True)
+class DesignSpace:
+    """The published MI355X candidate space (config/butterfly_space.json).
+
+    Every selector-table entry's parameters must be drawn from these lists;
+    the table loader refuses a table that names anything else (reference
+    selector.py:140-248 contract, rebuilt for the HIP kernels).
+    """
+
+    space_id: str
+    target: str
+    radix: tuple
+    stage_blocks: tuple
+    lds_elems: tuple
+    lds_max_n: int
+    fourstep_n1: tuple
+    fourstep_chunk_rows: tuple
+    fourstep_min_n: int
+    batch_candidates: tuple
+    batch_variants: tuple
+    layout_in: str
+    layout_out: str
+
+    @staticmethod
+    def load() -> "DesignSpace":
+        d = _read_json("butterfly_space.json")
+        _require(isinstance(d.get("space_id"), str) and d["space_id"], "butterfly_space.json: space_id required")
+        _require(isinstance(d.get("target"), str) and d["target"], "butterfly_space.json: target required")
+        p = d.get("P", {})
+        _require(_pow2_list(p.get("radix")), "butterfly_space.json: P.radix must be powers of two")
+        st = p.get("global_stage", {})
+        _require(_pow2_list(st.get("blocks")), "butterfly_space.json: P.global_stage.blocks must be powers of two")
+        lds = p.get("lds_fused", {})
+        _require(_pow2_list(lds.get("elems")), "butterfly_space.json: P.lds_fused.elems must be powers of two")
+        _require(isinstance(lds.get("max_n"), int) and lds["max_n"] > 0, "butterfly_space.json: P.lds_fused.max_n required")
+        fs = p.get("four_step", {})
+        _require(_pow2_list(fs.get("n1")), "butterfly_space.json: P.four_step.n1 must be powers of two")
+        ch = fs.get("chunk_rows")
+        _require(isinstance(ch, list) and ch and all(isinstance(c, int) and c >= 0 for c in ch),
+                 "butterfly_space.json: P.four_step.chunk_rows must be non-negative ints")
+        _require(isinstance(fs.get("min_n"), int) and fs["min_n"] > 0, "butterfly_space.json: P.four_step.min_n required")
+        b = p.get("batch_expansion", {})
+        _require(_pow2_list(b.get("candidates")), "butterfly_space.json: P.batch_expansion.candidates must be powers of two")
+        variants = b.get("variants", [])
+        _require(isinstance(variants, list) and all(v in ("spread", "folded") for v in variants),
+                 "butterfly_space.json: P.batch_expansion.variants must be 'spread'/'folded'")
+        lay = d.get("L", {})
+        _require(isinstance(lay.get("in"), list) and lay["in"], "butterfly_space.json: L.in required")
+        _require(isinstance(lay.get("out"), list) and lay["out"], "butterfly_space.json: L.out required")
+        return DesignSpace(
+            space_id=d["space_id"], target=d["target"], radix=tuple(p["radix"]),
+            stage_blocks=tuple(st["blocks"]), lds_elems=tuple(lds["elems"]), lds_max_n=lds["max_n"],
+            fourstep_n1=tuple(fs["n1"]), fourstep_chunk_rows=tuple(ch), fourstep_min_n=fs["min_n"],
+            batch_candidates=tuple(b["candidates"]), batch_variants=tuple(variants),
+            layout_in=lay["in"][0], layout_out=lay["out"][0],
+        )
+
+
+@dataclass(frozen=True)
+class SizeMatrix:
+    """Length lists of the correctness and benchmark matrices (config/sizes.json)."""
+
+    correctness_sizes: tuple
+    bench_sizes: tuple
+    batches: tuple
+
+    @staticmethod
+    def load() -> "SizeMatrix":
+        d = _read_json("sizes.json")
+        for key in ("correctness_sizes", "bench_sizes", "batches"):
+            _require(_pow2_list(d.get(key)), f"sizes.json: {key} must be a non-empty list of powers of two")
+        return SizeMatrix(tuple(d["correctness_sizes"]), tuple(d["bench_sizes"]), tuple(d["batches"]))

@@ -1,0 +1,37 @@
+"""Device guard around every launch (reference src/xpu/context.py:43-66).
+
+``device_context(device)`` makes the tensor's GPU current for the duration of
+a launch; the native plan is bound to the device that was current when it
+was created.  A missing GPU stack is a RuntimeError, never a silent no-op.
+"""
+from __future__ import annotations
+
+import contextlib
+
+
+def device_ready() -> bool:
+    try:
+        import torch
+
+        return bool(torch.cuda.is_available())
+    except Exception:  # noqa: BLE001
+        return False
+
+
+@contextlib.contextmanager
+def device_context(device):
+    import torch
+
+    if not torch.cuda.is_available():
+        raise RuntimeError("no ROCm GPU available: the FFT kernels run on the GPU only")
+    index = device.index if hasattr(device, "index") else int(device)
+    if index is None:
+        index = torch.cuda.current_device()
+    with torch.cuda.device(index):
+        yield index
+
+
+def device_name(index: int = 0) -> str:
+    import torch
+
+    return torch.cuda.get_device_name(index)

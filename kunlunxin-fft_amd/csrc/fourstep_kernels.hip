@@ -1,0 +1,215 @@
+// fourstep_kernels.hip -- two-pass (Bailey 4-step) FFT for core lengths
+// 2^8 .. 2^20, the MI355X form of the reference's hybrid path
+// (src/xpu/adapter_hybrid.py:224-270, scripts/issue10_wp3_perf.py:428-461).
+//
+// N = N1*N2, n = n1*N2 + n2, k = k1 + N1*k2:
+//   X[k1 + N1*k2] = sum_n2 W_N2^(n2*k2) * [ W_N^(n2*k1) * sum_n1 x[n1*N2+n2] W_N1^(n1*k1) ]
+// Pass 1 (column pass): for each n2, an N1-point FFT down the column
+//   x[n1*N2 + n2] (row stride N2), times W_N^(n2*k1), stored transposed as
+//   Z[n2*N1 + k1] -- one contiguous run of N1 per column, so the store is
+//   unit-stride.  The twiddle and the layout hand-off are fused into this
+//   store (the reference's k_twiddle_fused idea, issue10_wp3_perf.py:214-242).
+// Pass 2 (row pass): for each k1, an N2-point FFT over Z[k1 + N1*n2] (stride
+//   N1), stored to X[k1 + N1*k2] -- the same addresses it read, so pass 2 runs
+//   in place on the output buffer and the plan needs no workspace.
+// Both passes are one kernel template: a block owns C adjacent columns (lanes
+// run along the columns, so every row access is a C*8-byte contiguous run),
+// keeps them in LDS, and runs the same Stockham passes as the single-pass
+// kernel on each column.  Inverse = conjugated roots; the norm scale is applied
+// by pass 2's store.  The big twiddle W_N^e (e < N) is the product of two
+// small tables, W_N^(e mod 2^h) * W_N^(2^h * (e >> h)).
+#include "mfft_device.hpp"
+#include "mfft_internal.hpp"
+
+namespace mfft {
+namespace {
+
+__device__ __forceinline__ int pad(int i) { return i + (i >> 4); }
+
+template <int LOGL, int LOGE, int LOGC>
+struct ColCfg {
+    static constexpr int L = 1 << LOGL;
+    static constexpr int E = 1 << LOGE;
+    static constexpr int C = 1 << LOGC;
+    static constexpr int T = L / E;  // threads per column
+    static constexpr int WG = C * T;
+    static constexpr int P = (LOGL + LOGE - 1) / LOGE;
+    static constexpr int PITCH = L + (L >> 4) + 1;
+    static constexpr int logr(int p) { return p < P - 1 ? LOGE : LOGL - LOGE * (P - 1); }
+    static constexpr int lns(int p) { return LOGE * p; }
+};
+
+// KIND 0: pass 1 (column FFT of length L = N1 over S = N2 columns, twiddle,
+//         transposed store).  KIND 1: pass 2 (in place, L = N2, S = N1 columns).
+template <int LOGL, int LOGE, int LOGC, int DIR, int KIND>
+__global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_pass_kernel(
+    const float2* src, float2* dst, const float2* __restrict__ tw,
+    const float2* __restrict__ tw_lo, const float2* __restrict__ tw_hi, int tw_h, int logn,
+    int log_s, float scale) {
+    using C = ColCfg<LOGL, LOGE, LOGC>;
+    constexpr int L = C::L, E = C::E, T = C::T, P = C::P, NC = C::C;
+    __shared__ float2 lds[NC * C::PITCH];
+
+    const int tid = threadIdx.x;
+    const int c = tid & (NC - 1);
+    const int j = tid >> LOGC;
+    const int groups = (1 << log_s) >> LOGC;  // column groups per transform
+    const int64_t row = blockIdx.x / groups;
+    const int c0 = (blockIdx.x - (int)(row * groups)) << LOGC;
+    const int64_t base = row << logn;
+    const float2* s = src + base + c0 + c;
+    float2* lt = lds + c * C::PITCH;
+
+    float2 v[E];
+    {
+        constexpr int R0 = 1 << C::logr(0);
+        constexpr int NB0 = E / R0;
+        static_for<0, NB0>([&](auto m) {
+            static_for<0, R0>([&](auto q) {
+                const int i = j + m.value * T + q.value * (L / R0);
+                v[m.value * R0 + q.value] = s[(int64_t)i << log_s];
+            });
+        });
+    }
+    // KIND 1 runs in place (src == dst): every element of this block's columns
+    // is in registers before the first barrier, all stores come after it, and
+    // no other block touches these columns.
+
+    static_for<0, P>([&](auto pp) {
+        constexpr int p = pp.value;
+        constexpr int LR = C::logr(p);
+        constexpr int R = 1 << LR;
+        constexpr int NB = E / R;
+        constexpr int LNS = C::lns(p);
+        constexpr int NS = 1 << LNS;
+        if constexpr (p > 0) {
+            static_for<0, NB>([&](auto m) {
+                static_for<0, R>([&](auto q) {
+                    const int i = j + m.value * T + q.value * (L / R);
+                    v[m.value * R + q.value] = lt[pad(i)];
+                });
+            });
+        }
+        static_for<0, NB>([&](auto m) {
+            if constexpr (NS > 1) {
+                const int b = j + m.value * T;
+                const int k = b & (NS - 1);
+                constexpr int LST = LOGL - LNS - LR;
+                static_for<1, R>([&](auto q) {
+                    const float2 w = tw[(q.value * k) << LST];
+                    v[m.value * R + q.value] = cmul_tw<DIR>(v[m.value * R + q.value], w);
+                });
+            }
+            dft<R, DIR, m.value * R, 1>(v);
+        });
+        if constexpr (p < P - 1 || KIND == 0) {
+            if constexpr (p > 0) __syncthreads();
+            static_for<0, NB>([&](auto m) {
+                const int b = j + m.value * T;
+                const int base_o = ((b >> LNS) << (LNS + LR)) + (b & (NS - 1));
+                static_for<0, R>([&](auto q) { lt[pad(base_o + q.value * NS)] = v[m.value * R + q.value]; });
+            });
+            __syncthreads();
+        }
+    });
+
+    if constexpr (KIND == 0) {
+        // transposed, twiddled store: lanes run along k1 inside one column
+        const int hmask = (1 << tw_h) - 1;
+        static_for<0, E>([&](auto r) {
+            const int e = tid + r.value * C::WG;
+            const int cc = e >> LOGL;
+            const int k1 = e & (L - 1);
+            const int n2 = c0 + cc;
+            const uint32_t ex = (uint32_t)n2 * (uint32_t)k1;  // < N
+            const float2 w = cmul(tw_lo[ex & hmask], tw_hi[ex >> tw_h]);
+            const float2 val = cmul_tw<DIR>(lds[cc * C::PITCH + pad(k1)], w);
+            dst[base + ((int64_t)n2 << LOGL) + k1] = val;
+        });
+    } else {
+        constexpr int LR = C::logr(P - 1);
+        constexpr int R = 1 << LR;
+        constexpr int NB = E / R;
+        constexpr int NS = L / R;
+        float2* d = dst + base + c0 + c;
+        static_for<0, NB>([&](auto m) {
+            const int b = j + m.value * T;
+            static_for<0, R>([&](auto q) {
+                d[(int64_t)(b + q.value * NS) << log_s] = cscale(v[m.value * R + q.value], scale);
+            });
+        });
+    }
+}
+
+// column-group width and elements per thread for a pass of length 2^logl
+constexpr int col_loge(int logl) { return logl >= 8 ? 4 : (logl >= 6 ? 3 : 2); }
+constexpr int col_logc(int logl) { return logl >= 9 ? 3 : 4; }
+
+template <int LOGL, int DIR, int KIND>
+hipError_t launch_pass(const float2* src, float2* dst, const mfft_plan* p, int64_t rows,
+                       int log_s, float scale, hipStream_t stream) {
+    constexpr int LOGE = col_loge(LOGL);
+    constexpr int LOGC = col_logc(LOGL);
+    using C = ColCfg<LOGL, LOGE, LOGC>;
+    const int logn = ilog2((int)p->core_n);
+    const int64_t groups = ((int64_t)1 << log_s) >> LOGC;
+    const int64_t blocks = rows * groups;
+    const float2* tw = KIND == 0 ? p->tw_n1 : p->tw_n2;
+    fourstep_pass_kernel<LOGL, LOGE, LOGC, DIR, KIND><<<(unsigned)blocks, C::WG, 0, stream>>>(
+        src, dst, tw, p->tw_lo, p->tw_hi, p->tw_h, logn, log_s, scale);
+    mark(stream);
+    return hipGetLastError();
+}
+
+template <int DIR, int KIND>
+hipError_t dispatch_len(int logl, const float2* src, float2* dst, const mfft_plan* p, int64_t rows,
+                        int log_s, float scale, hipStream_t stream) {
+    switch (logl) {
+        case 4: return launch_pass<4, DIR, KIND>(src, dst, p, rows, log_s, scale, stream);
+        case 5: return launch_pass<5, DIR, KIND>(src, dst, p, rows, log_s, scale, stream);
+        case 6: return launch_pass<6, DIR, KIND>(src, dst, p, rows, log_s, scale, stream);
+        case 7: return launch_pass<7, DIR, KIND>(src, dst, p, rows, log_s, scale, stream);
+        case 8: return launch_pass<8, DIR, KIND>(src, dst, p, rows, log_s, scale, stream);
+        case 9: return launch_pass<9, DIR, KIND>(src, dst, p, rows, log_s, scale, stream);
+        case 10: return launch_pass<10, DIR, KIND>(src, dst, p, rows, log_s, scale, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+bool fourstep_supported(int log2n1, int log2n2) {
+    // each pass length in [16, 1024]; the other factor must hold a full column group
+    if (log2n1 < 4 || log2n1 > 10 || log2n2 < 4 || log2n2 > 10) return false;
+    return log2n2 >= col_logc(log2n1) && log2n1 >= col_logc(log2n2);
+}
+
+void fourstep_default_split(int log2n, int* log2n1, int* log2n2) {
+    *log2n1 = log2n / 2;
+    *log2n2 = log2n - *log2n1;
+}
+
+hipError_t launch_fourstep(int dir, const float2* src, float2* dst, const mfft_plan* p, int64_t rows,
+                           float scale, hipStream_t stream, int* launches) {
+    const int l1 = ilog2((int)p->n1), l2 = ilog2((int)p->n2);
+    const int64_t chunk = p->chunk_rows > 0 ? p->chunk_rows : rows;
+    const int64_t n = p->core_n;
+    int count = 0;
+    for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
+        const int64_t rc = rows - r0 < chunk ? rows - r0 : chunk;
+        const float2* s = src + r0 * n;
+        float2* d = dst + r0 * n;
+        hipError_t e;
+        e = dir < 0 ? dispatch_len<-1, 0>(l1, s, d, p, rc, l2, 1.0f, stream)
+                    : dispatch_len<1, 0>(l1, s, d, p, rc, l2, 1.0f, stream);
+        if (e != hipSuccess) return e;
+        e = dir < 0 ? dispatch_len<-1, 1>(l2, d, d, p, rc, l1, scale, stream)
+                    : dispatch_len<1, 1>(l2, d, d, p, rc, l1, scale, stream);
+        if (e != hipSuccess) return e;
+        count += 2;
+    }
+    if (launches) *launches = count;
+    return hipSuccess;
+}
+
+}  // namespace mfft

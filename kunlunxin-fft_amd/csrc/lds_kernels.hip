@@ -1,0 +1,258 @@
+// lds_kernels.hip -- single-pass LDS-resident FFT for core lengths 1..8192.
+//
+// One HBM read and one HBM write per element: every transform stays inside
+// one workgroup from its first load to its last store.  This is the MI355X
+// replacement for the reference's M1 (stages fused in global memory with
+// barriers, kernels.py:426-484), M2 (first log2(T) stages as a dense matmul,
+// kernels.py:487-532) and M3 (tail stages as XOR-gather maps, kernels.py:
+// 925-990): all log2(N) stages run here, with no global round trip between
+// them.
+//
+// Algorithm: Stockham auto-sort (natural order in and out, no bit reversal
+// pass).  Pass p with radix R and accumulated span NS handles butterflies
+// b in [0, L/R): inputs b + q*L/R, twiddles W_{NS*R}^(q*(b % NS)), an
+// in-register radix-R DFT, outputs (b/NS)*NS*R + b%NS + q*NS.  Each thread
+// owns E = L/T elements (T threads per transform), i.e. E/R butterflies per
+// pass.  Pass 0 reads HBM directly and the last pass writes HBM directly --
+// both are unit-stride across lanes -- and the passes in between exchange
+// through LDS.  LDS addresses carry one pad slot per 16 elements and an odd
+// per-transform pitch, which spreads the stride-R Stockham writes over banks.
+//
+// Modes fused into the same kernel (src/xpu/entry.py:555-587 semantics):
+//   0  c2c: core + norm scale in the final store (inverse = conjugated roots)
+//   1  r2c: the real input viewed as n/2 complex (x[2k] + i x[2k+1]) is the
+//      core input for free; the stitch of kernels.py:1127-1177 runs from LDS
+//      and writes the n/2+1 bins with the scale
+//   2  c2r: the pre-twiddle of kernels.py:1180-1229 is applied while loading
+//      the n/2+1 bins; the inverse core writes the n real samples as n/2
+//      complex pairs with scale 2*norm_scale
+#include "mfft_device.hpp"
+#include "mfft_internal.hpp"
+
+namespace mfft {
+namespace {
+
+template <int LOGL, int LOGE>
+struct LdsCfg {
+    static constexpr int L = 1 << LOGL;
+    static constexpr int LE = LOGE < LOGL ? LOGE : LOGL;  // log2 elements per thread
+    static constexpr int E = 1 << LE;
+    static constexpr int T = L / E;                        // threads per transform
+    static constexpr int WG = T >= 256 ? T : 256;          // threads per block
+    static constexpr int TPB = WG / T;                     // transforms per block
+    static constexpr int P = (LOGL == 0) ? 1 : (LOGL + LE - 1) / LE;  // passes
+    static constexpr int PITCH = L + (L >> 4) + 1;
+    static constexpr int LDS_ELEMS = TPB * PITCH;
+    static constexpr int logr(int p) { return p < P - 1 ? LE : LOGL - LE * (P - 1); }
+    static constexpr int lns(int p) { return LE * p; }
+};
+
+__device__ __forceinline__ int pad(int i) { return i + (i >> 4); }
+
+template <int LOGL, int LOGE, int DIR, int MODE>
+__global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG)) void lds_fft_kernel(
+    const void* __restrict__ src_v, void* __restrict__ dst_v, const float2* __restrict__ tw,
+    const float2* __restrict__ tw_real, int64_t rows, float scale) {
+    using C = LdsCfg<LOGL, LOGE>;
+    constexpr int L = C::L, E = C::E, T = C::T, P = C::P;
+    constexpr bool NEED_LDS = (P > 1) || (MODE == 1);
+    __shared__ float2 lds[NEED_LDS ? C::LDS_ELEMS : 1];
+
+    const int tid = threadIdx.x;
+    const int tl = tid / T;
+    const int j = tid & (T - 1);
+    const int64_t row = (int64_t)blockIdx.x * C::TPB + tl;
+    const bool active = row < rows;
+    float2* lt = lds + (NEED_LDS ? tl * C::PITCH : 0);
+
+    float2 v[E];
+
+    // ---- pass-0 operands straight from HBM
+    {
+        constexpr int R0 = 1 << C::logr(0);
+        constexpr int NB0 = E / R0;
+        if constexpr (MODE == 2) {
+            const float2* xb = (const float2*)src_v + row * (L + 1);
+            static_for<0, NB0>([&](auto m) {
+                static_for<0, R0>([&](auto q) {
+                    const int i = j + m.value * T + q.value * (L / R0);
+                    float2 z = make_float2(0.0f, 0.0f);
+                    if (active) {
+                        float2 xk = xb[i];
+                        float2 xj = xb[L - i];
+                        if (i == 0) {
+                            xk.y = 0.0f;
+                            xj.y = 0.0f;
+                        }
+                        const float ar = 0.5f * (xk.x + xj.x), ai = 0.5f * (xk.y - xj.y);
+                        const float cr = 0.5f * (xk.x - xj.x), ci = 0.5f * (xk.y + xj.y);
+                        const float2 t = tw_real[i];
+                        const float wr = t.x, wi = -t.y;
+                        z = make_float2(ar - (wr * ci + wi * cr), ai + (wr * cr - wi * ci));
+                    }
+                    v[m.value * R0 + q.value] = z;
+                });
+            });
+        } else {
+            const float2* src = (const float2*)src_v + row * L;
+            static_for<0, NB0>([&](auto m) {
+                static_for<0, R0>([&](auto q) {
+                    const int i = j + m.value * T + q.value * (L / R0);
+                    v[m.value * R0 + q.value] = active ? src[i] : make_float2(0.0f, 0.0f);
+                });
+            });
+        }
+    }
+
+    // ---- Stockham passes
+    static_for<0, P>([&](auto pp) {
+        constexpr int p = pp.value;
+        constexpr int LR = C::logr(p);
+        constexpr int R = 1 << LR;
+        constexpr int NB = E / R;
+        constexpr int LNS = C::lns(p);
+        constexpr int NS = 1 << LNS;
+        if constexpr (p > 0) {
+            static_for<0, NB>([&](auto m) {
+                static_for<0, R>([&](auto q) {
+                    const int i = j + m.value * T + q.value * (L / R);
+                    v[m.value * R + q.value] = lt[pad(i)];
+                });
+            });
+        }
+        static_for<0, NB>([&](auto m) {
+            if constexpr (NS > 1) {
+                const int b = j + m.value * T;
+                const int k = b & (NS - 1);
+                constexpr int LST = LOGL - LNS - LR;  // log2(L / (NS*R))
+                static_for<1, R>([&](auto q) {
+                    const float2 w = tw[(q.value * k) << LST];
+                    v[m.value * R + q.value] = cmul_tw<DIR>(v[m.value * R + q.value], w);
+                });
+            }
+            dft<R, DIR, m.value * R, 1>(v);
+        });
+        if constexpr (p < P - 1 || MODE == 1) {
+            if constexpr (p > 0) __syncthreads();  // every thread has read this pass's inputs
+            static_for<0, NB>([&](auto m) {
+                const int b = j + m.value * T;
+                const int base = ((b >> LNS) << (LNS + LR)) + (b & (NS - 1));
+                static_for<0, R>([&](auto q) { lt[pad(base + q.value * NS)] = v[m.value * R + q.value]; });
+            });
+            __syncthreads();
+        }
+    });
+
+    // ---- epilogue
+    if constexpr (MODE == 1) {
+        // r2c stitch out of LDS: bins k in [0, L], X[k] = a - i*w*c
+        float2* xo = (float2*)dst_v + row * (L + 1);
+        if (active) {
+            auto stitch = [&](int k) {
+                const float2 zk = lt[pad(k & (L - 1))];
+                const float2 zj = lt[pad((L - k) & (L - 1))];
+                const float ar = 0.5f * (zk.x + zj.x), ai = 0.5f * (zk.y - zj.y);
+                const float cr = 0.5f * (zk.x - zj.x), ci = 0.5f * (zk.y + zj.y);
+                const float2 w = tw_real[k];
+                const float xr = ar + (w.x * ci + w.y * cr);
+                float xi = ai - (w.x * cr - w.y * ci);
+                if (k == 0 || k == L) xi = 0.0f;
+                xo[k] = make_float2(xr * scale, xi * scale);
+            };
+            static_for<0, E>([&](auto m) { stitch(j + m.value * T); });
+            if (j == 0) stitch(L);
+        }
+    } else {
+        constexpr int LR = C::logr(P - 1);
+        constexpr int R = 1 << LR;
+        constexpr int NB = E / R;
+        constexpr int NS = L / R;
+        float2* dst = (float2*)dst_v + row * L;
+        if (active) {
+            static_for<0, NB>([&](auto m) {
+                const int b = j + m.value * T;
+                static_for<0, R>([&](auto q) { dst[b + q.value * NS] = cscale(v[m.value * R + q.value], scale); });
+            });
+        }
+    }
+}
+
+template <int LOGL, int LOGE, int DIR, int MODE>
+hipError_t launch_one(const void* src, void* dst, const float2* tw, const float2* tw_real,
+                      int64_t rows, float scale, hipStream_t stream) {
+    using C = LdsCfg<LOGL, LOGE>;
+    const int64_t blocks = (rows + C::TPB - 1) / C::TPB;
+    if (blocks <= 0) return hipSuccess;
+    lds_fft_kernel<LOGL, LOGE, DIR, MODE><<<(unsigned)blocks, C::WG, 0, stream>>>(src, dst, tw, tw_real, rows, scale);
+    mark(stream);
+    return hipGetLastError();
+}
+
+template <int LOGL, int LOGE>
+hipError_t dispatch_mode(int mode, int dir, const void* src, void* dst, const float2* tw,
+                         const float2* tw_real, int64_t rows, float scale, hipStream_t stream) {
+    if (mode == 0) {
+        return dir < 0 ? launch_one<LOGL, LOGE, -1, 0>(src, dst, tw, tw_real, rows, scale, stream)
+                       : launch_one<LOGL, LOGE, 1, 0>(src, dst, tw, tw_real, rows, scale, stream);
+    }
+    if (mode == 1) return launch_one<LOGL, LOGE, -1, 1>(src, dst, tw, tw_real, rows, scale, stream);
+    return launch_one<LOGL, LOGE, 1, 2>(src, dst, tw, tw_real, rows, scale, stream);
+}
+
+template <int LOGL>
+hipError_t dispatch_elems(int loge, int mode, int dir, const void* src, void* dst, const float2* tw,
+                          const float2* tw_real, int64_t rows, float scale, hipStream_t stream) {
+    switch (loge) {
+        case 2: return dispatch_mode<LOGL, 2>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 3: return dispatch_mode<LOGL, 3>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        default: return dispatch_mode<LOGL, 4>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+    }
+}
+
+}  // namespace
+
+bool lds_supported(int log2l, int elems) {
+    if (log2l < 0 || log2l > kMaxLdsLog2) return false;
+    if (elems != 0 && elems != 4 && elems != 8 && elems != 16) return false;
+    // a 8192-point transform needs 16 elements per thread (512 threads, 69 KiB LDS)
+    if (log2l == 13 && elems != 0 && elems != 16) return false;
+    return true;
+}
+
+int lds_default_elems(int log2l) {
+    if (log2l <= 4) return 16;  // one thread holds the whole transform (min(L, 16))
+    if (log2l <= 6) return 8;
+    return 16;
+}
+
+int lds_threads_per_block(int log2l, int elems) {
+    int le = ilog2(elems);
+    if (le > log2l) le = log2l;
+    const int t = 1 << (log2l - le);
+    return t >= 256 ? t : 256;
+}
+
+hipError_t launch_lds(int mode, int dir, int log2l, int elems, const void* src, void* dst,
+                      const float2* tw, const float2* tw_real, int64_t rows, float scale,
+                      hipStream_t stream) {
+    const int loge = ilog2(elems);
+    switch (log2l) {
+        case 0: return dispatch_elems<0>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 1: return dispatch_elems<1>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 2: return dispatch_elems<2>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 3: return dispatch_elems<3>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 4: return dispatch_elems<4>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 5: return dispatch_elems<5>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 6: return dispatch_elems<6>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 7: return dispatch_elems<7>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 8: return dispatch_elems<8>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 9: return dispatch_elems<9>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 10: return dispatch_elems<10>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 11: return dispatch_elems<11>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 12: return dispatch_elems<12>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 13: return dispatch_mode<13, 4>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace mfft

@@ -1,0 +1,489 @@
+// mfft_api.hip -- the C ABI of include/mfft.h: plan creation (validation,
+// twiddle tables, workspace), execution (kernel launches only) and queries.
+//
+// Validation mirrors the reference's contracts and happens before any device
+// allocation: power-of-two lengths (validate.py:13-16 log2_exact), the
+// direction lock of real transforms (entry.py:157-172), known enums
+// (entry.py:136-156).  Twiddles are computed on the host in double and
+// rounded once to float (the reference builds them per call in float32,
+// runner.py:93-97; here they are built once per plan).
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "mfft_device.hpp"
+#include "mfft_internal.hpp"
+
+namespace mfft {
+thread_local LaunchTimer* g_timer = nullptr;
+}
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(MFFT_ERR_RUNTIME, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+int log2_exact(int64_t n) {
+    if (n <= 0 || (n & (n - 1)) != 0) return -1;
+    int b = 0;
+    while (((int64_t)1 << b) != n) ++b;
+    return b;
+}
+
+double norm_scale(int64_t n, int dir, int norm) {
+    // entry.py:81-102
+    if (norm == MFFT_NORM_ORTHO) return 1.0 / std::sqrt((double)n);
+    if ((norm == MFFT_NORM_FORWARD && dir == MFFT_FORWARD) ||
+        (norm == MFFT_NORM_BACKWARD && dir == MFFT_INVERSE))
+        return 1.0 / (double)n;
+    return 1.0;
+}
+
+// forward roots exp(-2*pi*i*m/len) for m in [0, count), rounded from double
+std::vector<float2> roots(int64_t len, int64_t count, int64_t step) {
+    std::vector<float2> w((size_t)count);
+    const long double two_pi = 6.283185307179586476925286766559005768L;
+    for (int64_t m = 0; m < count; ++m) {
+        const int64_t e = (m * step) % len;
+        // exact values on the axes keep symmetric roots symmetric
+        if (e == 0) { w[m] = make_float2(1.0f, 0.0f); continue; }
+        if (4 * e == len) { w[m] = make_float2(0.0f, -1.0f); continue; }
+        if (2 * e == len) { w[m] = make_float2(-1.0f, 0.0f); continue; }
+        if (4 * e == 3 * len) { w[m] = make_float2(0.0f, 1.0f); continue; }
+        const long double a = -two_pi * (long double)e / (long double)len;
+        w[m] = make_float2((float)cosl(a), (float)sinl(a));
+    }
+    return w;
+}
+
+int upload(float2** dptr, const std::vector<float2>& h, int64_t* bytes) {
+    const size_t nb = h.size() * sizeof(float2);
+    hipError_t e = hipMalloc((void**)dptr, nb > 0 ? nb : sizeof(float2));
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(twiddle table)");
+    if (nb) {
+        e = hipMemcpy(*dptr, h.data(), nb, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return hip_fail(e, "hipMemcpy(twiddle table)");
+    }
+    *bytes += (int64_t)nb;
+    return MFFT_OK;
+}
+
+void release(mfft_plan* p) {
+    float2** bufs[] = {&p->tw, &p->tw_n1, &p->tw_n2, &p->tw_lo, &p->tw_hi, &p->tw_real, &p->ws_a, &p->ws_b};
+    for (float2** b : bufs) {
+        if (*b) (void)hipFree(*b);
+        *b = nullptr;
+    }
+}
+
+bool is_stage_flow(int f) {
+    return f == MFFT_FLOW_RADIX2_DIT || f == MFFT_FLOW_RADIX2_DIF || f == MFFT_FLOW_RADIX4_DIT ||
+           f == MFFT_FLOW_RADIX4_DIF;
+}
+
+// Enqueue the complex core of length p->core_n over `rows` rows.
+int run_core(const mfft_plan* p, const float2* src, float2* dst, int dir, float scale,
+             hipStream_t stream) {
+    hipError_t e = hipSuccess;
+    int launches = 0;
+    switch (p->flow) {
+        case MFFT_FLOW_RADIX2_DIT:
+        case MFFT_FLOW_RADIX2_DIF:
+            e = mfft::launch_radix2(p->flow == MFFT_FLOW_RADIX2_DIF, dir, src, dst, p->ws_b, p->tw,
+                                    p->core_n, p->batch, scale, p->block, stream, &launches);
+            break;
+        case MFFT_FLOW_RADIX4_DIT:
+        case MFFT_FLOW_RADIX4_DIF:
+            e = mfft::launch_radix4(p->flow == MFFT_FLOW_RADIX4_DIF, dir, src, dst, p->ws_b, p->tw,
+                                    p->core_n, p->batch, scale, p->block, stream, &launches);
+            break;
+        case MFFT_FLOW_LDS_FUSED:
+            e = mfft::launch_lds(0, dir, mfft::ilog2((int)p->core_n), p->elems, src, dst, p->tw, nullptr,
+                                 p->batch, scale, stream);
+            break;
+        case MFFT_FLOW_FOUR_STEP:
+            e = mfft::launch_fourstep(dir, src, dst, p, p->batch, scale, stream, &launches);
+            break;
+        default:
+            return fail(MFFT_ERR_VALUE, "internal: unknown flow %d", p->flow);
+    }
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    return MFFT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mfft_abi_version(void) { return MFFT_ABI_VERSION; }
+
+const char* mfft_last_error(void) { return g_err.c_str(); }
+
+int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_type,
+                     int transform_direction, int norm, int flow, const int32_t* params, int nparams) {
+    g_err.clear();
+    if (!out) return fail(MFFT_ERR_VALUE, "out must not be NULL");
+    *out = nullptr;
+    if (transform_type < MFFT_C2C || transform_type > MFFT_C2R)
+        return fail(MFFT_ERR_VALUE, "unsupported transform_type %d", transform_type);
+    if (transform_direction != MFFT_FORWARD && transform_direction != MFFT_INVERSE)
+        return fail(MFFT_ERR_VALUE, "unsupported transform_direction %d", transform_direction);
+    if (norm < MFFT_NORM_NONE || norm > MFFT_NORM_ORTHO) return fail(MFFT_ERR_VALUE, "unsupported norm %d", norm);
+    if (transform_type == MFFT_R2C && transform_direction != MFFT_FORWARD)
+        return fail(MFFT_ERR_VALUE, "r2c is a forward transform");
+    if (transform_type == MFFT_C2R && transform_direction != MFFT_INVERSE)
+        return fail(MFFT_ERR_VALUE, "c2r is an inverse transform");
+    const int logn = log2_exact(n);
+    if (logn < 0) return fail(MFFT_ERR_VALUE, "size must be a positive power of two, got %lld", (long long)n);
+    if (logn > mfft::kMaxLog2N)
+        return fail(MFFT_ERR_VALUE, "n=%lld exceeds the supported maximum 2^%d", (long long)n, mfft::kMaxLog2N);
+    if (transform_type != MFFT_C2C && n < 2)
+        return fail(MFFT_ERR_VALUE, "real transforms need n >= 2, got %lld", (long long)n);
+    if (batch < 1) return fail(MFFT_ERR_VALUE, "batch must be >= 1, got %lld", (long long)batch);
+    if (nparams < 0 || nparams > MFFT_MAX_PARAMS || (nparams > 0 && !params))
+        return fail(MFFT_ERR_VALUE, "bad params (nparams=%d)", nparams);
+    int32_t prm[MFFT_MAX_PARAMS] = {0, 0, 0, 0};
+    for (int i = 0; i < nparams; ++i) prm[i] = params[i];
+    for (int i = 0; i < MFFT_MAX_PARAMS; ++i)
+        if (prm[i] < 0) return fail(MFFT_ERR_VALUE, "params[%d]=%d must be >= 0", i, prm[i]);
+
+    const bool real = transform_type != MFFT_C2C;
+    const int64_t core_n = real ? n / 2 : n;
+    const int logc = log2_exact(core_n);
+    const int dir = transform_direction == MFFT_FORWARD ? -1 : 1;
+
+    // ---- resolve and check the flow
+    if (flow == MFFT_FLOW_AUTO) flow = logc <= mfft::kMaxLdsLog2 ? MFFT_FLOW_LDS_FUSED : MFFT_FLOW_FOUR_STEP;
+    int block = 256, elems = 0;
+    int64_t n1 = 0, n2 = 0, chunk = 0;
+    switch (flow) {
+        case MFFT_FLOW_RADIX2_DIT:
+        case MFFT_FLOW_RADIX2_DIF:
+        case MFFT_FLOW_RADIX4_DIT:
+        case MFFT_FLOW_RADIX4_DIF: {
+            const int min_log = (flow == MFFT_FLOW_RADIX4_DIT || flow == MFFT_FLOW_RADIX4_DIF) ? 2 : 1;
+            if (logc < min_log)
+                return fail(MFFT_ERR_UNSUPPORTED, "flow %d needs a core length >= %d, got %lld", flow,
+                            1 << min_log, (long long)core_n);
+            if (prm[0]) {
+                const int lb = log2_exact(prm[0]);
+                if (lb < 6 || lb > 10)
+                    return fail(MFFT_ERR_VALUE, "threads per block %d must be a power of two in [64, 1024]", prm[0]);
+                block = prm[0];
+            }
+            break;
+        }
+        case MFFT_FLOW_LDS_FUSED:
+            if (!mfft::lds_supported(logc, prm[0]))
+                return fail(MFFT_ERR_UNSUPPORTED,
+                            "LDS_FUSED runs core lengths up to 2^%d with 4, 8 or 16 elements per thread "
+                            "(got core length %lld, elements %d)",
+                            mfft::kMaxLdsLog2, (long long)core_n, prm[0]);
+            elems = prm[0] ? prm[0] : mfft::lds_default_elems(logc);
+            if (logc == 13) elems = 16;
+            block = mfft::lds_threads_per_block(logc, elems);
+            break;
+        case MFFT_FLOW_FOUR_STEP: {
+            int l1, l2;
+            mfft::fourstep_default_split(logc, &l1, &l2);
+            if (prm[0]) {
+                l1 = log2_exact(prm[0]);
+                if (l1 < 0) return fail(MFFT_ERR_VALUE, "n1=%d must be a power of two", prm[0]);
+                l2 = logc - l1;
+            }
+            if (logc < mfft::kMinFourStepLog2 || !mfft::fourstep_supported(l1, l2))
+                return fail(MFFT_ERR_UNSUPPORTED,
+                            "FOUR_STEP needs core length 2^8..2^20 split into n1, n2 in [16, 1024] "
+                            "(got core length %lld, n1=2^%d)",
+                            (long long)core_n, l1);
+            n1 = (int64_t)1 << l1;
+            n2 = (int64_t)1 << l2;
+            chunk = prm[1] > 0 ? prm[1] : 0;
+            break;
+        }
+        default:
+            return fail(MFFT_ERR_VALUE, "unknown flow id %d", flow);
+    }
+
+    int dev = 0;
+    hipError_t he = hipGetDevice(&dev);
+    if (he != hipSuccess) return hip_fail(he, "hipGetDevice");
+
+    mfft_plan* p = new (std::nothrow) mfft_plan();
+    if (!p) return fail(MFFT_ERR_RUNTIME, "out of host memory");
+    p->n = n;
+    p->batch = batch;
+    p->core_n = core_n;
+    p->transform_type = transform_type;
+    p->transform_direction = transform_direction;
+    p->norm = norm;
+    p->flow = flow;
+    p->device = dev;
+    p->block = block;
+    p->elems = elems;
+    p->n1 = n1;
+    p->n2 = n2;
+    p->chunk_rows = chunk;
+    p->r2c_fused = transform_type == MFFT_R2C && flow == MFFT_FLOW_LDS_FUSED;
+    p->c2r_fused = transform_type == MFFT_C2R && flow == MFFT_FLOW_LDS_FUSED;
+    // c2r: the half-length inverse core carries a factor 2 (entry.py:583-587)
+    const double sc = norm_scale(n, transform_direction, norm) * (transform_type == MFFT_C2R ? 2.0 : 1.0);
+    p->scale = (float)sc;
+
+    int rc = MFFT_OK;
+    // ---- twiddle tables
+    if (flow == MFFT_FLOW_FOUR_STEP) {
+        const int lc = logc;
+        p->tw_h = (lc + 1) / 2;
+        if (rc == MFFT_OK) rc = upload(&p->tw_n1, roots(n1, n1, 1), &p->table_bytes);
+        if (rc == MFFT_OK) rc = upload(&p->tw_n2, roots(n2, n2, 1), &p->table_bytes);
+        if (rc == MFFT_OK) rc = upload(&p->tw_lo, roots(core_n, (int64_t)1 << p->tw_h, 1), &p->table_bytes);
+        if (rc == MFFT_OK)
+            rc = upload(&p->tw_hi, roots(core_n, core_n >> p->tw_h, (int64_t)1 << p->tw_h), &p->table_bytes);
+    } else {
+        rc = upload(&p->tw, roots(core_n, core_n, 1), &p->table_bytes);
+    }
+    if (rc == MFFT_OK && real) {
+        // exp(-2*pi*i*k/n), k in [0, n/2]  (runner.py:1650-1658 range)
+        rc = upload(&p->tw_real, roots(n, n / 2 + 1, 1), &p->table_bytes);
+    }
+
+    // ---- workspace
+    const size_t core_bytes = (size_t)batch * (size_t)core_n * sizeof(float2);
+    const bool need_a = real && !(p->r2c_fused || p->c2r_fused);
+    const bool need_b = is_stage_flow(flow);
+    if (rc == MFFT_OK && need_a) {
+        he = hipMalloc((void**)&p->ws_a, core_bytes);
+        if (he != hipSuccess) rc = hip_fail(he, "hipMalloc(workspace)");
+        else p->ws_bytes += (int64_t)core_bytes;
+    }
+    if (rc == MFFT_OK && need_b) {
+        he = hipMalloc((void**)&p->ws_b, core_bytes);
+        if (he != hipSuccess) rc = hip_fail(he, "hipMalloc(workspace)");
+        else p->ws_bytes += (int64_t)core_bytes;
+    }
+
+    // ---- launch count (per execute)
+    int core_launches = 0;
+    switch (flow) {
+        case MFFT_FLOW_RADIX2_DIT:
+        case MFFT_FLOW_RADIX2_DIF: core_launches = logc; break;
+        case MFFT_FLOW_RADIX4_DIT:
+        case MFFT_FLOW_RADIX4_DIF: core_launches = logc / 2 + (logc & 1); break;
+        case MFFT_FLOW_LDS_FUSED: core_launches = 1; break;
+        case MFFT_FLOW_FOUR_STEP: {
+            const int64_t ch = chunk > 0 ? chunk : batch;
+            core_launches = (int)(2 * ((batch + ch - 1) / ch));
+            break;
+        }
+    }
+    p->launches = core_launches + (need_a ? 1 : 0);
+
+    if (rc == MFFT_OK) {
+        he = hipDeviceSynchronize();  // table uploads complete before the first execute
+        if (he != hipSuccess) rc = hip_fail(he, "hipDeviceSynchronize");
+    }
+    if (rc != MFFT_OK) {
+        release(p);
+        delete p;
+        return rc;
+    }
+    (void)dir;
+    *out = p;
+    return MFFT_OK;
+}
+
+int mfft_execute(const mfft_plan* p, const void* in, void* out, void* stream_v) {
+    g_err.clear();
+    if (!p) return fail(MFFT_ERR_VALUE, "plan must not be NULL");
+    if (!in || !out) return fail(MFFT_ERR_VALUE, "in and out must not be NULL");
+    const size_t in_bytes = (size_t)p->batch *
+        (p->transform_type == MFFT_R2C ? (size_t)p->n * 4
+         : p->transform_type == MFFT_C2R ? (size_t)(p->n / 2 + 1) * 8 : (size_t)p->n * 8);
+    const size_t out_bytes = (size_t)p->batch *
+        (p->transform_type == MFFT_R2C ? (size_t)(p->n / 2 + 1) * 8
+         : p->transform_type == MFFT_C2R ? (size_t)p->n * 4 : (size_t)p->n * 8);
+    const char* ib = (const char*)in;
+    const char* ob = (const char*)out;
+    if (ib < ob + out_bytes && ob < ib + in_bytes)
+        return fail(MFFT_ERR_VALUE, "in and out must not overlap");
+    if ((((uintptr_t)in) & 7) && p->transform_type != MFFT_R2C)
+        return fail(MFFT_ERR_VALUE, "complex input must be 8-byte aligned");
+    if ((((uintptr_t)in) & 7) && p->transform_type == MFFT_R2C)
+        return fail(MFFT_ERR_VALUE, "r2c input must be 8-byte aligned (pairs are read as complex)");
+    if (((uintptr_t)out) & 7) return fail(MFFT_ERR_VALUE, "output must be 8-byte aligned");
+    int dev = -1;
+    hipError_t he = hipGetDevice(&dev);
+    if (he != hipSuccess) return hip_fail(he, "hipGetDevice");
+    if (dev != p->device)
+        return fail(MFFT_ERR_RUNTIME, "plan was created on device %d but device %d is current", p->device, dev);
+    hipStream_t stream = (hipStream_t)stream_v;
+    const int dir = p->transform_direction == MFFT_FORWARD ? -1 : 1;
+
+    if (p->transform_type == MFFT_C2C)
+        return run_core(p, (const float2*)in, (float2*)out, dir, p->scale, stream);
+
+    const int logc = mfft::ilog2((int)p->core_n);
+    if (p->transform_type == MFFT_R2C) {
+        if (p->r2c_fused) {
+            he = mfft::launch_lds(1, -1, logc, p->elems, in, out, p->tw, p->tw_real, p->batch, p->scale, stream);
+            return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
+        }
+        int rc = run_core(p, (const float2*)in, p->ws_a, -1, 1.0f, stream);
+        if (rc != MFFT_OK) return rc;
+        he = mfft::launch_r2c_stitch(p->ws_a, (float2*)out, p->tw_real, p->n, p->batch, p->scale, stream);
+        return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
+    }
+    // c2r
+    if (p->c2r_fused) {
+        he = mfft::launch_lds(2, 1, logc, p->elems, in, out, p->tw, p->tw_real, p->batch, p->scale, stream);
+        return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
+    }
+    he = mfft::launch_c2r_pre((const float2*)in, p->ws_a, p->tw_real, p->n, p->batch, stream);
+    if (he != hipSuccess) return hip_fail(he, "kernel launch");
+    return run_core(p, p->ws_a, (float2*)out, 1, p->scale, stream);
+}
+
+int mfft_execute_timed(const mfft_plan* p, const void* in, void* out, void* stream_v,
+                       float* launch_ms, int cap, int* n_launches) {
+    g_err.clear();
+    if (!launch_ms || !n_launches || cap < 1 || cap > 4096)
+        return fail(MFFT_ERR_VALUE, "launch_ms/n_launches must be valid and 1 <= cap <= 4096");
+    *n_launches = 0;
+    if (!p) return fail(MFFT_ERR_VALUE, "plan must not be NULL");
+    std::vector<hipEvent_t> ev((size_t)cap + 1, nullptr);
+    int rc = MFFT_OK;
+    for (auto& e : ev) {
+        hipError_t he = hipEventCreate(&e);
+        if (he != hipSuccess) {
+            rc = hip_fail(he, "hipEventCreate");
+            break;
+        }
+    }
+    hipStream_t stream = (hipStream_t)stream_v;
+    mfft::LaunchTimer timer{ev.data(), cap, 0};
+    if (rc == MFFT_OK) {
+        hipError_t he = hipEventRecord(ev[0], stream);
+        if (he != hipSuccess) rc = hip_fail(he, "hipEventRecord");
+    }
+    if (rc == MFFT_OK) {
+        mfft::g_timer = &timer;
+        rc = mfft_execute(p, in, out, stream_v);
+        mfft::g_timer = nullptr;
+    }
+    if (rc == MFFT_OK && timer.count > 0) {
+        hipError_t he = hipEventSynchronize(ev[timer.count]);
+        if (he != hipSuccess) rc = hip_fail(he, "hipEventSynchronize");
+        for (int i = 0; rc == MFFT_OK && i < timer.count; ++i) {
+            float ms = 0.0f;
+            he = hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+            if (he != hipSuccess) rc = hip_fail(he, "hipEventElapsedTime");
+            launch_ms[i] = ms;
+        }
+        if (rc == MFFT_OK) *n_launches = timer.count;
+    }
+    for (auto& e : ev)
+        if (e) (void)hipEventDestroy(e);
+    return rc;
+}
+
+int mfft_plan_destroy(mfft_plan* p) {
+    g_err.clear();
+    if (!p) return MFFT_OK;
+    int cur = -1;
+    (void)hipGetDevice(&cur);
+    if (cur != p->device) (void)hipSetDevice(p->device);
+    hipError_t e = hipDeviceSynchronize();
+    release(p);
+    if (cur >= 0 && cur != p->device) (void)hipSetDevice(cur);
+    delete p;
+    return e == hipSuccess ? MFFT_OK : hip_fail(e, "hipDeviceSynchronize");
+}
+
+int mfft_plan_query(const mfft_plan* p, mfft_plan_info* info) {
+    g_err.clear();
+    if (!p || !info) return fail(MFFT_ERR_VALUE, "plan and info must not be NULL");
+    std::memset(info, 0, sizeof(*info));
+    info->n = p->n;
+    info->batch = p->batch;
+    info->core_n = p->core_n;
+    info->transform_type = p->transform_type;
+    info->transform_direction = p->transform_direction;
+    info->norm = p->norm;
+    info->flow = p->flow;
+    info->device = p->device;
+    info->launches = p->launches;
+    info->elems_per_thread = p->elems;
+    info->threads_per_block = p->block;
+    info->n1 = p->n1;
+    info->n2 = p->n2;
+    info->chunk_rows = p->chunk_rows;
+    info->workspace_bytes = p->ws_bytes;
+    info->table_bytes = p->table_bytes;
+    info->scale = (double)p->scale;
+    return MFFT_OK;
+}
+
+int mfft_bit_reverse_permute(const void* in, void* out, int64_t n, int64_t batch, void* stream) {
+    g_err.clear();
+    if (!in || !out) return fail(MFFT_ERR_VALUE, "in and out must not be NULL");
+    const int logn = log2_exact(n);
+    if (logn < 0 || logn > mfft::kMaxLog2N)
+        return fail(MFFT_ERR_VALUE, "size must be a power of two in [1, 2^%d], got %lld", mfft::kMaxLog2N, (long long)n);
+    if (batch < 1) return fail(MFFT_ERR_VALUE, "batch must be >= 1");
+    const size_t bytes = (size_t)n * (size_t)batch * 8;
+    if ((const char*)in < (const char*)out + bytes && (const char*)out < (const char*)in + bytes)
+        return fail(MFFT_ERR_VALUE, "in and out must not overlap");
+    hipError_t e = mfft::launch_bitrev((const float2*)in, (float2*)out, n, batch, (hipStream_t)stream);
+    return e == hipSuccess ? MFFT_OK : hip_fail(e, "kernel launch");
+}
+
+int mfft_device_props_get(int device, mfft_device_props* out) {
+    g_err.clear();
+    if (!out) return fail(MFFT_ERR_VALUE, "out must not be NULL");
+    std::memset(out, 0, sizeof(*out));
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    if (device < 0 || device >= count)
+        return fail(MFFT_ERR_VALUE, "device %d out of range (%d devices)", device, count);
+    hipDeviceProp_t pr;
+    e = hipGetDeviceProperties(&pr, device);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    std::snprintf(out->name, sizeof(out->name), "%s", pr.name);
+    std::snprintf(out->gcn_arch_name, sizeof(out->gcn_arch_name), "%s", pr.gcnArchName);
+    out->multiprocessor_count = pr.multiProcessorCount;
+    out->warp_size = pr.warpSize;
+    out->shared_mem_per_block = (int64_t)pr.sharedMemPerBlock;
+    out->shared_mem_per_multiprocessor = (int64_t)pr.maxSharedMemoryPerMultiProcessor;
+    out->total_global_mem = (int64_t)pr.totalGlobalMem;
+    out->clock_rate_khz = pr.clockRate;
+    out->memory_clock_rate_khz = pr.memoryClockRate;
+    out->memory_bus_width = pr.memoryBusWidth;
+    out->l2_cache_size = pr.l2CacheSize;
+    int v = 0;
+    if (hipDriverGetVersion(&v) == hipSuccess) out->driver_version = v;
+    v = 0;
+    if (hipRuntimeGetVersion(&v) == hipSuccess) out->runtime_version = v;
+    out->abi_version = MFFT_ABI_VERSION;
+    return MFFT_OK;
+}
+
+}  // extern "C"

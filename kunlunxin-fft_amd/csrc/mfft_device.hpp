@@ -1,0 +1,147 @@
+// mfft_device.hpp -- device building blocks shared by every gfx950 kernel:
+// interleaved complex64 arithmetic, compile-time roots of unity, and the
+// in-register radix-R DFT used as the butterfly of every Stockham pass.
+//
+// Sign convention: DIR = -1 is the forward transform (exp(-2*pi*i*j*k/N),
+// src/xpu/runner.py:93-97), DIR = +1 the unnormalised inverse.  Twiddle
+// tables in device memory always hold the forward roots; the inverse uses
+// their conjugates, folded into the complex product at no cost.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <type_traits>
+
+namespace mfft {
+
+template <int I>
+using ic = std::integral_constant<int, I>;
+
+// Calls f(ic<B>{}), f(ic<B+1>{}), ..., f(ic<E-1>{}) -- a loop whose index is
+// a compile-time constant, so register arrays are indexed statically.
+template <int B, int E, typename F>
+__host__ __device__ __forceinline__ constexpr void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(ic<B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v >> 1); }
+
+constexpr int brev_bits(int x, int bits) {
+    int r = 0;
+    for (int i = 0; i < bits; ++i) {
+        r = (r << 1) | (x & 1);
+        x >>= 1;
+    }
+    return r;
+}
+
+// ---- compile-time cos/sin of 2*pi*j/R (Taylor series on [-pi, pi]) -------
+constexpr double kPi = 3.14159265358979323846264338327950288;
+
+constexpr double taylor_sin(double x) {
+    double term = x, sum = x;
+    for (int i = 1; i < 24; ++i) {
+        term *= -x * x / ((2.0 * i) * (2.0 * i + 1.0));
+        sum += term;
+    }
+    return sum;
+}
+
+constexpr double taylor_cos(double x) {
+    double term = 1.0, sum = 1.0;
+    for (int i = 1; i < 24; ++i) {
+        term *= -x * x / ((2.0 * i - 1.0) * (2.0 * i));
+        sum += term;
+    }
+    return sum;
+}
+
+// angle 2*pi*j/R reduced to (-pi, pi]
+constexpr double root_angle(int j, int R) {
+    int jj = ((j % R) + R) % R;
+    double a = 2.0 * kPi * (double)jj / (double)R;
+    return a > kPi ? a - 2.0 * kPi : a;
+}
+
+// ---- complex64 helpers ------------------------------------------------------
+__device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
+__device__ __forceinline__ float2 csub(float2 a, float2 b) { return make_float2(a.x - b.x, a.y - b.y); }
+__device__ __forceinline__ float2 cmul(float2 a, float2 b) {
+    return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+}
+__device__ __forceinline__ float2 cscale(float2 a, float s) { return make_float2(a.x * s, a.y * s); }
+__device__ __forceinline__ float2 cconj(float2 a) { return make_float2(a.x, -a.y); }
+
+// a * w (DIR = -1) or a * conj(w) (DIR = +1), w a forward-table root
+template <int DIR>
+__device__ __forceinline__ float2 cmul_tw(float2 a, float2 w) {
+    if constexpr (DIR < 0) {
+        return make_float2(a.x * w.x - a.y * w.y, a.x * w.y + a.y * w.x);
+    } else {
+        return make_float2(a.x * w.x + a.y * w.y, a.y * w.x - a.x * w.y);
+    }
+}
+
+// a * exp(DIR * 2*pi*i*J/R) with exact rotations for multiples of pi/2 and
+// the symmetric pi/4 constants; everything resolved at compile time.
+template <int R, int J, int DIR>
+__device__ __forceinline__ float2 rot(float2 a) {
+    constexpr int j = ((J % R) + R) % R;
+    if constexpr (j == 0) {
+        return a;
+    } else if constexpr (2 * j == R) {
+        return make_float2(-a.x, -a.y);
+    } else if constexpr (4 * j == R) {  // exp(DIR*i*pi/2) = DIR*i
+        return DIR < 0 ? make_float2(a.y, -a.x) : make_float2(-a.y, a.x);
+    } else if constexpr (4 * j == 3 * R) {  // exp(DIR*i*3pi/2) = -DIR*i
+        return DIR < 0 ? make_float2(-a.y, a.x) : make_float2(a.y, -a.x);
+    } else if constexpr (8 * j == R || 8 * j == 3 * R || 8 * j == 5 * R || 8 * j == 7 * R) {
+        constexpr float h = 0.70710678118654752440f;
+        constexpr float c = (8 * j == R || 8 * j == 7 * R) ? h : -h;
+        constexpr float s0 = (8 * j == R || 8 * j == 3 * R) ? h : -h;  // sin(2*pi*j/R)
+        constexpr float s = DIR < 0 ? -s0 : s0;
+        return make_float2(c * (a.x) - s * (a.y), c * (a.y) + s * (a.x));
+    } else {
+        constexpr double ang = root_angle(j, R);
+        constexpr float c = (float)taylor_cos(ang);
+        constexpr float s = (float)(DIR < 0 ? -taylor_sin(ang) : taylor_sin(ang));
+        return make_float2(a.x * c - a.y * s, a.x * s + a.y * c);
+    }
+}
+
+// In-register DFT of length R over v[OFF + q*STR], q in [0, R), natural order
+// in and out.  A radix-2 decimation-in-frequency network with compile-time
+// twiddles, followed by the bit-reversal reorder (pure register renaming).
+template <int R, int DIR, int OFF, int STR, int E>
+__device__ __forceinline__ void dft(float2 (&v)[E]) {
+    static_assert(R >= 1 && (R & (R - 1)) == 0, "radix must be a power of two");
+    constexpr int LOGR = ilog2(R);
+    if constexpr (R > 1) {
+        static_for<0, LOGR>([&](auto s) {
+            constexpr int h = R >> (s.value + 1);
+            static_for<0, R / 2>([&](auto p) {
+                constexpr int blk = (p.value / h) * 2 * h;
+                constexpr int jj = p.value % h;
+                constexpr int i0 = OFF + (blk + jj) * STR;
+                constexpr int i1 = OFF + (blk + jj + h) * STR;
+                const float2 a = v[i0];
+                const float2 b = v[i1];
+                v[i0] = cadd(a, b);
+                v[i1] = rot<2 * h, jj, DIR>(csub(a, b));
+            });
+        });
+        float2 t[R];
+        static_for<0, R>([&](auto q) { t[q.value] = v[OFF + brev_bits(q.value, LOGR) * STR]; });
+        static_for<0, R>([&](auto q) { v[OFF + q.value * STR] = t[q.value]; });
+    }
+}
+
+// 32-bit bit reversal of the low `bits` bits (bits in [1, 31]).
+__device__ __forceinline__ uint32_t brev_low(uint32_t x, int bits) {
+    return __brev(x) >> (32 - bits);
+}
+
+}  // namespace mfft

@@ -1,0 +1,92 @@
+// mfft_internal.hpp -- host-side plan record and the launchers each kernel
+// source file provides.  Every launcher only enqueues on `stream` and returns
+// hipGetLastError()'s verdict through the caller.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mfft.h"
+
+struct mfft_plan {
+    int64_t n = 0, batch = 0;
+    int64_t core_n = 0;  // complex core length
+    int transform_type = MFFT_C2C, transform_direction = MFFT_FORWARD, norm = MFFT_NORM_BACKWARD;
+    int flow = MFFT_FLOW_AUTO;
+    int device = 0;
+    float scale = 1.0f;  // applied by the final store of the core (c2c, c2r) or the stitch (r2c)
+    int block = 256;     // stage flows: threads per block
+    int elems = 16;      // LDS_FUSED: elements per thread
+    int launches = 0;
+    int64_t n1 = 0, n2 = 0, chunk_rows = 0;
+    bool r2c_fused = false, c2r_fused = false;
+
+    // device memory owned by the plan
+    float2* tw = nullptr;       // W_core^m, m in [0, core_n)   (stage + LDS flows)
+    float2* tw_n1 = nullptr;    // W_n1^m                        (four-step pass 1)
+    float2* tw_n2 = nullptr;    // W_n2^m                        (four-step pass 2)
+    float2* tw_lo = nullptr;    // W_core^m, m < 2^h             (four-step twiddle, low digit)
+    float2* tw_hi = nullptr;    // W_core^(m*2^h)                (four-step twiddle, high digit)
+    int tw_h = 0;
+    float2* tw_real = nullptr;  // exp(-2*pi*i*k/n), k in [0, n/2]  (r2c stitch / c2r pre)
+    float2* ws_a = nullptr;     // core-sized scratch (real flows: core output / input)
+    float2* ws_b = nullptr;     // core-sized scratch (stage-flow ping-pong)
+    int64_t ws_bytes = 0, table_bytes = 0;
+};
+
+namespace mfft {
+
+// Optional per-launch event recording (mfft_execute_timed): every launcher
+// calls mark(stream) right after each kernel launch.  Off (nullptr) otherwise.
+struct LaunchTimer {
+    hipEvent_t* ev;  // cap + 1 events; ev[0] is recorded before the first launch
+    int cap;
+    int count;       // launches marked so far
+};
+extern thread_local LaunchTimer* g_timer;
+inline void mark(hipStream_t s) {
+    LaunchTimer* t = g_timer;
+    if (t && t->count < t->cap) {
+        (void)hipEventRecord(t->ev[t->count + 1], s);
+        ++t->count;
+    }
+}
+
+constexpr int kMaxLog2N = 20;        // reference range: 8 .. 2^20 (docs/user-guide/transforms.md)
+constexpr int kMaxLdsLog2 = 13;      // single-pass LDS kernel: core length <= 8192
+constexpr int kMinFourStepLog2 = 8;  // four-step needs n1, n2 >= 16
+
+// ---- stage_kernels.hip: reference global-stage flows, real epilogues ------
+// Radix-2 / radix-4 global-stage core over `rows` rows of length n:
+// reads `src` (never written), writes `dst`, ping-pongs through `scratch`.
+hipError_t launch_radix2(bool dif, int dir, const float2* src, float2* dst, float2* scratch,
+                         const float2* tw, int64_t n, int64_t rows, float scale, int block,
+                         hipStream_t stream, int* launches);
+hipError_t launch_radix4(bool dif, int dir, const float2* src, float2* dst, float2* scratch,
+                         const float2* tw, int64_t n, int64_t rows, float scale, int block,
+                         hipStream_t stream, int* launches);
+hipError_t launch_bitrev(const float2* src, float2* dst, int64_t n, int64_t rows, hipStream_t stream);
+// R2C stitch: z [rows][n/2] (unnormalised N/2 FFT of packed pairs) -> x [rows][n/2+1]
+hipError_t launch_r2c_stitch(const float2* z, float2* x, const float2* tw_real, int64_t n,
+                             int64_t rows, float scale, hipStream_t stream);
+// C2R pre-twiddle: x [rows][n/2+1] -> z [rows][n/2], the inverse core's input
+hipError_t launch_c2r_pre(const float2* x, float2* z, const float2* tw_real, int64_t n,
+                          int64_t rows, hipStream_t stream);
+
+// ---- lds_kernels.hip: single-pass LDS-resident Stockham kernel ------------
+// mode 0: c2c core; 1: r2c (core forward + fused stitch); 2: c2r (fused
+// pre-twiddle + inverse core).  `log2l` is the core length's log2.
+bool lds_supported(int log2l, int elems);
+int lds_default_elems(int log2l);
+int lds_threads_per_block(int log2l, int elems);
+hipError_t launch_lds(int mode, int dir, int log2l, int elems, const void* src, void* dst,
+                      const float2* tw, const float2* tw_real, int64_t rows, float scale,
+                      hipStream_t stream);
+
+// ---- fourstep_kernels.hip: two-pass column/row FFT -----------------------
+bool fourstep_supported(int log2n1, int log2n2);
+void fourstep_default_split(int log2n, int* log2n1, int* log2n2);
+hipError_t launch_fourstep(int dir, const float2* src, float2* dst, const mfft_plan* p,
+                           int64_t rows, float scale, hipStream_t stream, int* launches);
+
+}  // namespace mfft

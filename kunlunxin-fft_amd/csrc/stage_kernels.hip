@@ -1,0 +1,327 @@
+// stage_kernels.hip -- the reference's global-stage flows on gfx950, plus the
+// standalone real-transform prologue/epilogue kernels.
+//
+// These keep the index maps of the reference's M0 / M5 flows (one launch and
+// one HBM round trip per stage), because they are the selector's baseline and
+// its closed fallback:
+//   radix-2 DIT stage  src/xpu/kernels.py:100-163  (j = k % n, i = (k/n)*2n + j,
+//                      b = X[i+n]*W[j*M], Y[i] = a+b, Y[i+n] = a-b, M = N/2n;
+//                      bit reversal folded into stage 0's loads)
+//   radix-2 DIF stage  kernels.py:166-236  ((a+b, (a-b)*W); bit or mixed digit
+//                      reversal folded into the last stage's stores)
+//   radix-4 DIT/DIF    kernels.py:239-423  (span 4n, twiddles W^(d*j*M), d=1..3;
+//                      mixed radix-4/2 digit reversal of kernels.py:41-78)
+// Differences on purpose: data are interleaved complex64 (one 8-byte load per
+// element instead of two planar ones), the batch is folded into a 1-D grid,
+// the twiddle table holds all N roots (so W^(3jM) needs no conjugate fold), and
+// the inverse / norm epilogue is fused into the stages (conjugated roots and a
+// scaled final store) instead of two extra passes.
+#include "mfft_device.hpp"
+#include "mfft_internal.hpp"
+
+namespace mfft {
+namespace {
+
+// mixed radix-4/2 digit reversal for DIT input (kernels.py:41-56 semantics):
+// radix-4 digits low to high, an odd top bit lands in bit 0.
+__device__ __forceinline__ uint32_t dit_digit_reverse(uint32_t x, int bits) {
+    uint32_t rev = 0;
+    for (int q = 0; q < bits / 2; ++q) rev |= ((x >> (2 * q)) & 3u) << (bits - 2 * q - 2);
+    if (bits & 1) rev |= (x >> (bits - 1)) & 1u;
+    return rev;
+}
+
+// DIF output digit reversal (kernels.py:59-78 semantics): with odd bits the
+// 1-bit digit sits at the bottom of the index and takes the top weight.
+__device__ __forceinline__ uint32_t dif_digit_reverse(uint32_t x, int bits) {
+    if ((bits & 1) == 0) return dit_digit_reverse(x, bits);
+    uint32_t rev = (x & 1u) << (bits - 1);
+    for (int q = 1; q <= bits / 2; ++q) rev |= ((x >> (2 * q - 1)) & 3u) << (bits - 1 - 2 * q);
+    return rev;
+}
+
+// REV: 0 = natural, 1 = bit reversal, 2 = mixed DIF digit reversal
+template <int REV>
+__device__ __forceinline__ uint32_t permute_out(uint32_t i, int bits) {
+    if constexpr (REV == 1) return brev_low(i, bits);
+    else if constexpr (REV == 2) return dif_digit_reverse(i, bits);
+    else return i;
+}
+
+template <int DIR, bool BITREV_IN>
+__global__ void r2_dit_stage(const float2* __restrict__ x, float2* __restrict__ y,
+                             const float2* __restrict__ tw, int64_t total, int logn, int log_ns,
+                             float scale) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= total) return;
+    const int64_t row = g >> (logn - 1);
+    const uint32_t k = (uint32_t)(g & (((int64_t)1 << (logn - 1)) - 1));
+    const uint32_t ns = 1u << log_ns;
+    const uint32_t j = k & (ns - 1);
+    const uint32_t i = ((k >> log_ns) << (log_ns + 1)) + j;
+    uint32_t sa = i, sb = i + ns;
+    if constexpr (BITREV_IN) {
+        sa = brev_low(sa, logn);
+        sb = brev_low(sb, logn);
+    }
+    const float2* xr = x + (row << logn);
+    float2* yr = y + (row << logn);
+    const float2 a = xr[sa];
+    const float2 b = cmul_tw<DIR>(xr[sb], tw[(size_t)j << (logn - 1 - log_ns)]);
+    yr[i] = cscale(cadd(a, b), scale);
+    yr[i + ns] = cscale(csub(a, b), scale);
+}
+
+template <int DIR, int REV_OUT>
+__global__ void r2_dif_stage(const float2* __restrict__ x, float2* __restrict__ y,
+                             const float2* __restrict__ tw, int64_t total, int logn, int log_ns,
+                             float scale) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= total) return;
+    const int64_t row = g >> (logn - 1);
+    const uint32_t k = (uint32_t)(g & (((int64_t)1 << (logn - 1)) - 1));
+    const uint32_t ns = 1u << log_ns;
+    const uint32_t j = k & (ns - 1);
+    const uint32_t i = ((k >> log_ns) << (log_ns + 1)) + j;
+    const float2* xr = x + (row << logn);
+    float2* yr = y + (row << logn);
+    const float2 a = xr[i];
+    const float2 b = xr[i + ns];
+    const float2 d = cmul_tw<DIR>(csub(a, b), tw[(size_t)j << (logn - 1 - log_ns)]);
+    yr[permute_out<REV_OUT>(i, logn)] = cscale(cadd(a, b), scale);
+    yr[permute_out<REV_OUT>(i + ns, logn)] = cscale(d, scale);
+}
+
+template <int DIR, bool DIGREV_IN>
+__global__ void r4_dit_stage(const float2* __restrict__ x, float2* __restrict__ y,
+                             const float2* __restrict__ tw, int64_t total, int logn, int log_ns,
+                             float scale) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= total) return;
+    const int64_t row = g >> (logn - 2);
+    const uint32_t off = (uint32_t)(g & (((int64_t)1 << (logn - 2)) - 1));
+    const uint32_t ns = 1u << log_ns;
+    const uint32_t j = off & (ns - 1);
+    const uint32_t i = ((off >> log_ns) << (log_ns + 2)) + j;
+    const float2* xr = x + (row << logn);
+    float2* yr = y + (row << logn);
+    const uint32_t jm = j << (logn - 2 - log_ns);  // j*M, M = N/(4n)
+    float2 v[4];
+    static_for<0, 4>([&](auto d) {
+        uint32_t s = i + d.value * ns;
+        if constexpr (DIGREV_IN) s = dit_digit_reverse(s, logn);
+        v[d.value] = xr[s];
+        if constexpr (d.value > 0) v[d.value] = cmul_tw<DIR>(v[d.value], tw[d.value * jm]);
+    });
+    dft<4, DIR, 0, 1>(v);
+    static_for<0, 4>([&](auto d) { yr[i + d.value * ns] = cscale(v[d.value], scale); });
+}
+
+template <int DIR, bool DIGREV_OUT>
+__global__ void r4_dif_stage(const float2* __restrict__ x, float2* __restrict__ y,
+                             const float2* __restrict__ tw, int64_t total, int logn, int log_ns,
+                             float scale) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= total) return;
+    const int64_t row = g >> (logn - 2);
+    const uint32_t off = (uint32_t)(g & (((int64_t)1 << (logn - 2)) - 1));
+    const uint32_t ns = 1u << log_ns;
+    const uint32_t j = off & (ns - 1);
+    const uint32_t i = ((off >> log_ns) << (log_ns + 2)) + j;
+    const float2* xr = x + (row << logn);
+    float2* yr = y + (row << logn);
+    const uint32_t jm = j << (logn - 2 - log_ns);
+    float2 v[4];
+    static_for<0, 4>([&](auto d) { v[d.value] = xr[i + d.value * ns]; });
+    dft<4, DIR, 0, 1>(v);
+    static_for<0, 4>([&](auto d) {
+        float2 o = v[d.value];
+        if constexpr (d.value > 0) o = cmul_tw<DIR>(o, tw[d.value * jm]);
+        uint32_t s = i + d.value * ns;
+        if constexpr (DIGREV_OUT) s = dif_digit_reverse(s, logn);
+        yr[s] = cscale(o, scale);
+    });
+}
+
+__global__ void bitrev_kernel(const float2* __restrict__ x, float2* __restrict__ y, int64_t total,
+                              int logn) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= total) return;
+    const int64_t row = g >> logn;
+    const uint32_t i = (uint32_t)(g & (((int64_t)1 << logn) - 1));
+    const uint32_t r = logn > 0 ? brev_low(i, logn) : 0u;
+    y[(row << logn) + r] = x[g];
+}
+
+// R2C stitch (kernels.py:1127-1177 formula): X[k] = a - i*w*c with
+// a = (Z[k] + conj Z[j])/2, c = (Z[k] - conj Z[j])/2, j = (np-k) % np,
+// w = exp(-2*pi*i*k/n); imaginary parts of bins 0 and np are exactly 0.
+__global__ void r2c_stitch_kernel(const float2* __restrict__ z, float2* __restrict__ x,
+                                  const float2* __restrict__ tw_real, int64_t total, int64_t np,
+                                  float scale) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= total) return;
+    const int64_t row = g / (np + 1);
+    const int64_t k = g - row * (np + 1);
+    const float2* zr = z + row * np;
+    const float2 zk = zr[k & (np - 1)];
+    const float2 zj = zr[(np - k) & (np - 1)];
+    const float ar = 0.5f * (zk.x + zj.x), ai = 0.5f * (zk.y - zj.y);
+    const float cr = 0.5f * (zk.x - zj.x), ci = 0.5f * (zk.y + zj.y);
+    const float2 w = tw_real[k];
+    float xr = ar + (w.x * ci + w.y * cr);
+    float xi = ai - (w.x * cr - w.y * ci);
+    if (k == 0 || k == np) xi = 0.0f;
+    x[g] = make_float2(xr * scale, xi * scale);
+}
+
+// C2R pre-twiddle (kernels.py:1180-1229 formula): Z[k] = a + i*w'*c with
+// a = (X[k] + conj X[j])/2, c = (X[k] - conj X[j])/2, j = np-k,
+// w' = exp(+2*pi*i*k/n); imaginary parts of bins 0 and np are ignored.
+__global__ void c2r_pre_kernel(const float2* __restrict__ x, float2* __restrict__ z,
+                               const float2* __restrict__ tw_real, int64_t total, int64_t np) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= total) return;
+    const int64_t row = g / np;
+    const int64_t k = g - row * np;
+    const float2* xr = x + row * (np + 1);
+    float2 xk = xr[k];
+    float2 xj = xr[np - k];
+    if (k == 0) {
+        xk.y = 0.0f;
+        xj.y = 0.0f;
+    }
+    const float ar = 0.5f * (xk.x + xj.x), ai = 0.5f * (xk.y - xj.y);
+    const float cr = 0.5f * (xk.x - xj.x), ci = 0.5f * (xk.y + xj.y);
+    const float2 t = tw_real[k];
+    const float wr = t.x, wi = -t.y;
+    z[g] = make_float2(ar - (wr * ci + wi * cr), ai + (wr * cr - wi * ci));
+}
+
+inline unsigned grid_for(int64_t total, int block) { return (unsigned)((total + block - 1) / block); }
+
+}  // namespace
+
+hipError_t launch_radix2(bool dif, int dir, const float2* src, float2* dst, float2* scratch,
+                         const float2* tw, int64_t n, int64_t rows, float scale, int block,
+                         hipStream_t stream, int* launches) {
+    const int logn = ilog2((int)n);
+    const int64_t total = rows * (n >> 1);
+    const unsigned grid = grid_for(total, block);
+    const float2* cur = src;
+    int count = 0;
+    for (int s = 0; s < logn; ++s) {
+        float2* out = ((logn - 1 - s) % 2 == 0) ? dst : scratch;
+        const bool last = s == logn - 1;
+        const float sc = last ? scale : 1.0f;
+        if (!dif) {
+            const int log_ns = s;  // half-spans 1, 2, ..., N/2
+            if (dir < 0) {
+                if (s == 0) r2_dit_stage<-1, true><<<grid, block, 0, stream>>>(cur, out, tw, total, logn, log_ns, sc);
+                else r2_dit_stage<-1, false><<<grid, block, 0, stream>>>(cur, out, tw, total, logn, log_ns, sc);
+            } else {
+                if (s == 0) r2_dit_stage<1, true><<<grid, block, 0, stream>>>(cur, out, tw, total, logn, log_ns, sc);
+                else r2_dit_stage<1, false><<<grid, block, 0, stream>>>(cur, out, tw, total, logn, log_ns, sc);
+            }
+        } else {
+            const int log_ns = logn - 1 - s;  // half-spans N/2, ..., 1
+            if (dir < 0) {
+                if (last) r2_dif_stage<-1, 1><<<grid, block, 0, stream>>>(cur, out, tw, total, logn, log_ns, sc);
+                else r2_dif_stage<-1, 0><<<grid, block, 0, stream>>>(cur, out, tw, total, logn, log_ns, sc);
+            } else {
+                if (last) r2_dif_stage<1, 1><<<grid, block, 0, stream>>>(cur, out, tw, total, logn, log_ns, sc);
+                else r2_dif_stage<1, 0><<<grid, block, 0, stream>>>(cur, out, tw, total, logn, log_ns, sc);
+            }
+        }
+        mark(stream);
+        ++count;
+        cur = out;
+    }
+    if (launches) *launches = count;
+    return hipGetLastError();
+}
+
+hipError_t launch_radix4(bool dif, int dir, const float2* src, float2* dst, float2* scratch,
+                         const float2* tw, int64_t n, int64_t rows, float scale, int block,
+                         hipStream_t stream, int* launches) {
+    const int logn = ilog2((int)n);
+    const int n4 = logn / 2;          // radix-4 stages
+    const bool tail = (logn & 1) != 0;  // one radix-2 stage when log2 N is odd
+    const int stages = n4 + (tail ? 1 : 0);
+    const int64_t total4 = rows * (n >> 2);
+    const int64_t total2 = rows * (n >> 1);
+    const unsigned grid4 = grid_for(total4, block);
+    const unsigned grid2 = grid_for(total2, block);
+    const float2* cur = src;
+    for (int s = 0; s < stages; ++s) {
+        float2* out = ((stages - 1 - s) % 2 == 0) ? dst : scratch;
+        const bool last = s == stages - 1;
+        const float sc = last ? scale : 1.0f;
+        if (!dif) {
+            // runner.py:1367-1383: spans 4, 16, ..., then a radix-2 span-N tail
+            if (s < n4) {
+                const int log_ns = 2 * s;
+                const bool first = s == 0;
+                if (dir < 0) {
+                    if (first) r4_dit_stage<-1, true><<<grid4, block, 0, stream>>>(cur, out, tw, total4, logn, log_ns, sc);
+                    else r4_dit_stage<-1, false><<<grid4, block, 0, stream>>>(cur, out, tw, total4, logn, log_ns, sc);
+                } else {
+                    if (first) r4_dit_stage<1, true><<<grid4, block, 0, stream>>>(cur, out, tw, total4, logn, log_ns, sc);
+                    else r4_dit_stage<1, false><<<grid4, block, 0, stream>>>(cur, out, tw, total4, logn, log_ns, sc);
+                }
+            } else {
+                if (dir < 0) r2_dit_stage<-1, false><<<grid2, block, 0, stream>>>(cur, out, tw, total2, logn, logn - 1, sc);
+                else r2_dit_stage<1, false><<<grid2, block, 0, stream>>>(cur, out, tw, total2, logn, logn - 1, sc);
+            }
+        } else {
+            // runner.py:1386-1396: radix-4 groups N, N/4, ..., then a group-2 tail
+            if (s < n4) {
+                const int log_ns = logn - 2 - 2 * s;
+                const bool digrev = last;  // no tail: the last radix-4 stage permutes
+                if (dir < 0) {
+                    if (digrev) r4_dif_stage<-1, true><<<grid4, block, 0, stream>>>(cur, out, tw, total4, logn, log_ns, sc);
+                    else r4_dif_stage<-1, false><<<grid4, block, 0, stream>>>(cur, out, tw, total4, logn, log_ns, sc);
+                } else {
+                    if (digrev) r4_dif_stage<1, true><<<grid4, block, 0, stream>>>(cur, out, tw, total4, logn, log_ns, sc);
+                    else r4_dif_stage<1, false><<<grid4, block, 0, stream>>>(cur, out, tw, total4, logn, log_ns, sc);
+                }
+            } else {
+                if (dir < 0) r2_dif_stage<-1, 2><<<grid2, block, 0, stream>>>(cur, out, tw, total2, logn, 0, sc);
+                else r2_dif_stage<1, 2><<<grid2, block, 0, stream>>>(cur, out, tw, total2, logn, 0, sc);
+            }
+        }
+        mark(stream);
+        cur = out;
+    }
+    if (launches) *launches = stages;
+    return hipGetLastError();
+}
+
+hipError_t launch_bitrev(const float2* src, float2* dst, int64_t n, int64_t rows, hipStream_t stream) {
+    const int logn = ilog2((int)n);
+    const int64_t total = rows * n;
+    if (total == 0) return hipSuccess;
+    bitrev_kernel<<<grid_for(total, 256), 256, 0, stream>>>(src, dst, total, logn);
+    mark(stream);
+    return hipGetLastError();
+}
+
+hipError_t launch_r2c_stitch(const float2* z, float2* x, const float2* tw_real, int64_t n,
+                             int64_t rows, float scale, hipStream_t stream) {
+    const int64_t np = n >> 1;
+    const int64_t total = rows * (np + 1);
+    r2c_stitch_kernel<<<grid_for(total, 256), 256, 0, stream>>>(z, x, tw_real, total, np, scale);
+    mark(stream);
+    return hipGetLastError();
+}
+
+hipError_t launch_c2r_pre(const float2* x, float2* z, const float2* tw_real, int64_t n,
+                          int64_t rows, hipStream_t stream) {
+    const int64_t np = n >> 1;
+    const int64_t total = rows * np;
+    c2r_pre_kernel<<<grid_for(total, 256), 256, 0, stream>>>(x, z, tw_real, total, np);
+    mark(stream);
+    return hipGetLastError();
+}
+
+}  // namespace mfft

@@ -1,0 +1,390 @@
+"""Selector -> execution entry: the drop-in plan API (reference src/xpu/entry.py).
+
+Same contract as the reference:
+
+1. validate semantics (direction in {dit, dif}, precision fp32,
+   transform_type in {c2c, r2c, c2r}, transform_direction in {forward,
+   inverse}, norm in {none, forward, backward, ortho}; r2c is forward-only
+   and c2r inverse-only) and raise ``ValueError`` before any table query;
+2. look up the frozen MI355X table (``selector``), after the composition
+   registry (``composition``, which ships empty and fails closed);
+3. resolve the runner name (``executed``), or fall back to M0 with the
+   reason when the table abstains or names no lowering;
+4. ``execute_fft_plan`` checks the input's shape/dtype against the plan,
+   then runs the runner's native plan -- one kernel launch for the LDS and
+   real flows, two per chunk for the four-step, one per stage for M0/M5.
+
+What is different underneath, on purpose: the inverse conjugation, the norm
+epilogue (entry.py:617-628, 656-668) and the R2C/C2R pack/stitch/pre-twiddle
+(entry.py:555-587) are fused into the kernels instead of being separate
+passes.  R2C/C2R always run the dedicated half-length flow (N/2-point complex
+core), marked ``params["real_compat"] = REAL_FLOW_MARK``; the reference's
+full-length compatibility path is not built (it computes the same values
+with twice the core work).
+
+This module imports no torch at module scope, so planning is host-only.
+"""
+from __future__ import annotations
+
+import math
+import weakref
+from dataclasses import dataclass, field
+
+from .composition import composition_select
+from .config import NORMALIZATIONS, TRANSFORM_DIRECTIONS, TRANSFORM_TYPES
+from .selector import Selection, find_entry, load_table, select
+
+DEFAULT_BLOCK = 256
+SUPPORTED_DIRECTIONS = ("dit", "dif")
+SUPPORTED_PRECISIONS = ("fp32",)
+SUPPORTED_TRANSFORMS = TRANSFORM_TYPES
+SUPPORTED_TRANSFORM_DIRECTIONS = TRANSFORM_DIRECTIONS
+SUPPORTED_NORMS = NORMALIZATIONS
+REAL_COMPAT_MARK = "packed-c2c-compat"
+REAL_FLOW_MARK = "dedicated-half-spectrum"
+REAL_FLOW_IDS = {"r2c": "dedicated-r2c-pack-v1", "c2r": "dedicated-c2r-hermitian-v1"}
+MAX_N = 1 << 20
+_SUPPORTED_DTYPES = {"fp32": "complex64"}
+
+
+def norm_scale(n: int, transform_direction: str, norm: str) -> float:
+    """Epilogue scale for one (direction, norm) pair -- torch.fft semantics.
+
+    ================== ============ ============
+    norm               forward      inverse
+    ================== ============ ============
+    ``none``           1            1
+    ``forward``        1/N          1
+    ``backward``       1            1/N
+    ``ortho``          1/sqrt(N)    1/sqrt(N)
+    ================== ============ ============
+    """
+    if transform_direction not in SUPPORTED_TRANSFORM_DIRECTIONS:
+        raise ValueError(f"bad transform_direction {transform_direction!r}")
+    if norm not in SUPPORTED_NORMS:
+        raise ValueError(f"bad norm {norm!r}")
+    if norm == "ortho":
+        return 1.0 / math.sqrt(n)
+    if (norm, transform_direction) in (("forward", "forward"), ("backward", "inverse")):
+        return 1.0 / n
+    return 1.0
+
+
+@dataclass(frozen=True)
+class ExecutionPlan:
+    """What will actually run for one shape under the frozen table
+    (reference entry.py:105-128, same fields)."""
+
+    n: int
+    batch: int
+    direction: str
+    precision: str
+    selection_source: str  # "table" | "abstain" | "composition"
+    reason: str
+    fallback: bool          # True when M0 runs instead of a table winner
+    executed: str           # runner name actually used
+    block: int | None = None
+    flow_id: str | None = None
+    flow_realization: str | None = None
+    processing_unit: str | None = None
+    params: dict = field(default_factory=dict)
+    transform_type: str = "c2c"
+    transform_direction: str = "forward"
+    norm: str = "backward"
+
+    def as_report(self) -> "ExecutionReport":
+        return ExecutionReport(**self.__dict__)
+
+
+@dataclass(frozen=True)
+class ExecutionReport(ExecutionPlan):
+    """ExecutionPlan plus the observation that the plan was carried out."""
+
+
+def _validate_semantics(direction: str, precision: str, transform_type: str = "c2c",
+                        transform_direction: str = "forward", norm: str = "backward") -> None:
+    """Reject unsupported semantics before any table query or launch."""
+    if direction not in SUPPORTED_DIRECTIONS:
+        raise ValueError(f"unsupported direction {direction!r}; supported: {SUPPORTED_DIRECTIONS} "
+                         "(the decomposition, not the transform direction)")
+    if precision not in SUPPORTED_PRECISIONS:
+        raise ValueError(f"unsupported precision {precision!r}; supported: {SUPPORTED_PRECISIONS}")
+    if transform_type not in SUPPORTED_TRANSFORMS:
+        raise ValueError(f"unsupported transform_type {transform_type!r}; supported: "
+                         f"{SUPPORTED_TRANSFORMS}; unknown transforms never fall back to another one")
+    if transform_direction not in SUPPORTED_TRANSFORM_DIRECTIONS:
+        raise ValueError(f"unsupported transform_direction {transform_direction!r}; supported: "
+                         f"{SUPPORTED_TRANSFORM_DIRECTIONS}")
+    if norm not in SUPPORTED_NORMS:
+        raise ValueError(f"unsupported norm {norm!r}; supported: {SUPPORTED_NORMS}")
+    if transform_type == "r2c" and transform_direction != "forward":
+        raise ValueError(f"r2c is a forward transform; got transform_direction={transform_direction!r}")
+    if transform_type == "c2r" and transform_direction != "inverse":
+        raise ValueError(f"c2r is an inverse transform; got transform_direction={transform_direction!r}")
+
+
+def _validate_shape(n: int, batch: int, transform_type: str) -> None:
+    if not isinstance(n, int) or n <= 0 or (n & (n - 1)):
+        raise ValueError(f"n must be a positive power of two, got {n!r}")
+    if n > MAX_N:
+        raise ValueError(f"n={n} exceeds the supported maximum {MAX_N}")
+    if transform_type in ("r2c", "c2r") and n < 2:
+        raise ValueError(f"real transforms need n >= 2, got {n}")
+    if not isinstance(batch, int) or batch < 1:
+        raise ValueError(f"batch must be a positive int, got {batch!r}")
+
+
+def _m0_name(direction: str, batch: int) -> str:
+    if batch > 1:
+        return "fft_dit_batch" if direction == "dit" else "fft_dif_batch"
+    return "fft_dit" if direction == "dit" else "fft_dif"
+
+
+def _real_params(transform_type: str) -> dict:
+    if transform_type in REAL_FLOW_IDS:
+        return {"real_flow": REAL_FLOW_IDS[transform_type], "real_compat": REAL_FLOW_MARK}
+    return {}
+
+
+def _m0_plan(n, batch, direction, precision, reason, fallback, block=DEFAULT_BLOCK,
+             transform_type="c2c", transform_direction="forward", norm="backward") -> ExecutionPlan:
+    params = {"variant": "folded", "batch": batch} if batch > 1 else {}
+    params.update(_real_params(transform_type))
+    return ExecutionPlan(
+        n=n, batch=batch, direction=direction, precision=precision,
+        selection_source="abstain" if fallback else "table", reason=reason, fallback=fallback,
+        executed=_m0_name(direction, batch), block=block, flow_id="baseline-global-stage",
+        flow_realization="global-stage", processing_unit="radix2-scalar", params=params,
+        transform_type=transform_type, transform_direction=transform_direction, norm=norm,
+    )
+
+
+def _dispatch(sel: Selection):
+    """Runner name for a table Selection, or None when no lowering implements
+    that (realization, unit, direction, batch) combination."""
+    key = (sel.flow_realization, sel.processing_unit, sel.direction)
+    single = sel.batch == 1
+    sfx = "" if single else "_batch"
+    if key[:2] == ("global-stage", "radix2-scalar"):
+        return ("fft_dit" if sel.direction == "dit" else "fft_dif") + sfx
+    if key[:2] == ("global-stage", "radix4-scalar"):
+        return ("fft_dit_radix4" if sel.direction == "dit" else "fft_dif_radix4") + sfx
+    if key[:2] == ("matrix-resident", "dense-dot-fft64"):
+        return ("fft_dit_matrix" if sel.direction == "dit" else "fft_dif_matrix") + sfx
+    if key[:2] == ("lds-resident", "stockham-radix16"):
+        return "fft_lds_fused" + sfx
+    if key[:2] == ("four-step", "stockham-radix16"):
+        return "fft_four_step" + sfx
+    if not single:
+        return None  # batched M1/M3: no lowering (reference entry.py:214-216)
+    if key == ("fused-inplace", "radix2-scalar", "dit"):
+        return "fft_dit_fused"
+    if key[:2] == ("grouped-boundary", "composite-linear-map"):
+        return "fft_dit_grouped" if sel.direction == "dit" else "fft_dif_grouped"
+    return None
+
+
+def _entry_block(table: dict, sel: Selection) -> int:
+    """Incumbent block for the shape when the table records one."""
+    try:
+        e = find_entry(table, sel.n, sel.batch, sel.direction, sel.transform_type,
+                       sel.transform_direction, sel.normalization)
+    except (KeyError, TypeError):
+        e = None
+    if e is None:
+        return DEFAULT_BLOCK
+    return int(e.get("incumbent_block") or DEFAULT_BLOCK)
+
+
+def _composition_plan(comp: dict, n, batch, direction, precision, transform_direction,
+                      norm) -> ExecutionPlan:
+    return ExecutionPlan(
+        n=n, batch=batch, direction=direction, precision=precision,
+        selection_source="composition",
+        reason=f"composition {comp['flow_id']} (exact shape, {comp['guard_pct']:.1f}% guard): "
+               f"{comp['reason']}",
+        fallback=False, executed="run_hybrid", block=None, flow_id=comp["flow_id"],
+        flow_realization=comp["flow_realization"], processing_unit=comp["processing_unit"],
+        params={"flow_kind": "composition", "tile": comp.get("tile", 0)},
+        transform_type="c2c", transform_direction=transform_direction, norm=norm,
+    )
+
+
+def plan_fft(direction: str, n: int, batch: int = 1, precision: str = "fp32",
+             profile_hash: str | None = None, table: dict | None = None,
+             env_hash: str | None = "auto", transform_type: str = "c2c",
+             transform_direction: str | None = None, norm: str = "backward") -> ExecutionPlan:
+    """Resolve the frozen table onto a concrete plan (host-only, no torch).
+
+    ``profile_hash=None`` abstains to M0 (pass ``DeviceProfile.load().hash()``
+    to use the table); ``env_hash="auto"`` re-verifies the table against the
+    live device/runtime fingerprint; an unknown or different environment, or
+    a shape outside the table, falls back to M0 with ``plan.reason`` saying
+    why.  ``transform_direction=None`` means the type's locked direction
+    (forward, or inverse for c2r).
+    """
+    if transform_direction is None:
+        transform_direction = "inverse" if transform_type == "c2r" else "forward"
+    _validate_semantics(direction, precision, transform_type, transform_direction, norm)
+    _validate_shape(n, batch, transform_type)
+    if transform_type == "c2c":
+        comp = composition_select(direction, n, batch=batch, precision=precision,
+                                  profile_hash=profile_hash, env_hash=env_hash,
+                                  transform_type=transform_type,
+                                  transform_direction=transform_direction, normalization=norm)
+        if comp is not None:
+            return _composition_plan(comp, n, batch, direction, precision, transform_direction, norm)
+    table = table if table is not None else load_table()
+    sel = select(direction, n, batch=batch, precision=precision, profile_hash=profile_hash,
+                 table=table, env_hash=env_hash, transform_type=transform_type,
+                 transform_direction=transform_direction, normalization=norm)
+    sem = dict(transform_type=transform_type, transform_direction=transform_direction, norm=norm)
+    if not sel.selected:
+        return _m0_plan(n, batch, direction, precision, sel.reason, True,
+                        block=_entry_block(table, sel), **sem)
+    name = sel.executed or _dispatch(sel)
+    if name is None:
+        return _m0_plan(n, batch, direction, precision,
+                        f"no lowering for {sel.flow_realization}/{sel.processing_unit} "
+                        f"direction={direction} batch={batch}; M0 fallback", True,
+                        block=_entry_block(table, sel), **sem)
+    params = dict(sel.params or {})
+    if sel.entry_tier == "previous-fallback":
+        params["previous_fallback"] = True
+    if params.get("real_flow"):
+        from .semantic import family_allows
+
+        if not family_allows(transform_type, params["real_flow"]):
+            raise ValueError(f"real_flow {params['real_flow']!r} not in the {transform_type} family")
+    params.update(_real_params(transform_type))
+    return ExecutionPlan(
+        n=n, batch=batch, direction=direction, precision=precision, selection_source="table",
+        reason=sel.reason, fallback=False, executed=name, block=sel.block, flow_id=sel.flow_id,
+        flow_realization=sel.flow_realization, processing_unit=sel.processing_unit, params=params,
+        **sem,
+    )
+
+
+def _expected_input_n(plan: ExecutionPlan) -> int:
+    """Last-dim length the plan expects for its transform_type."""
+    return plan.n // 2 + 1 if plan.transform_type == "c2r" else plan.n
+
+
+def _check_plan_input(plan: ExecutionPlan, shape, dtype_name: str) -> None:
+    """Host-testable shape/dtype contract (reference entry.py:467-498):
+    c2c complex64 (N,)/(B,N); r2c float32 (N,)/(B,N); c2r complex64
+    (N/2+1,)/(B,N/2+1).  Batch 1 takes rank-1 only."""
+    want = "float32" if plan.transform_type == "r2c" else _SUPPORTED_DTYPES.get(plan.precision, "complex64")
+    if dtype_name != want:
+        raise TypeError(f"x must be {want} for transform_type={plan.transform_type} "
+                        f"precision={plan.precision}, got {dtype_name}")
+    shape = tuple(int(s) for s in shape)
+    m = _expected_input_n(plan)
+    if plan.batch == 1:
+        if len(shape) != 1 or shape[0] != m:
+            raise ValueError(f"plan expects rank-1 x with N={m} (batch=1, "
+                             f"transform_type={plan.transform_type}); got shape {shape}")
+    elif len(shape) != 2 or shape != (plan.batch, m):
+        raise ValueError(f"plan expects x shape ({plan.batch}, {m}); got shape {shape}")
+
+
+# Per-plan resolved (native plan, output spec), evicted when the plan dies.
+_RESOLVED: dict = {}
+
+
+def _resolve(plan: ExecutionPlan, device_index: int):
+    key = (id(plan), device_index)
+    hit = _RESOLVED.get(key)
+    if hit is not None and hit[0]() is plan:
+        return hit[1], hit[2]
+    from . import runner
+
+    nplan = runner.get_native_plan(plan.executed, plan.n, plan.batch, plan.transform_type,
+                                   plan.transform_direction, plan.norm, plan.block,
+                                   plan.params or {}, device_index)
+    spec = runner.output_spec(plan.transform_type, plan.n, plan.batch)
+    ref = weakref.ref(plan, lambda _r, k=key: _RESOLVED.pop(k, None))
+    _RESOLVED[key] = (ref, nplan, spec)
+    return nplan, spec
+
+
+def execute_fft_plan(plan: ExecutionPlan, x):
+    """Execute a resolved plan without re-querying the table (plan reuse).
+
+    ``x`` must be a contiguous GPU tensor of the plan's shape and dtype; the
+    result is a newly allocated tensor on the same device and stream.
+    """
+    import torch
+
+    from .ledger import phase
+
+    with phase("plan-validate"):
+        if not isinstance(x, torch.Tensor):
+            raise TypeError(f"x must be a torch.Tensor, got {type(x).__name__}")
+        _check_plan_input(plan, tuple(x.shape), str(x.dtype).split(".")[-1])
+        if plan.transform_type not in SUPPORTED_TRANSFORMS:
+            raise ValueError(f"plan transform_type {plan.transform_type!r} not supported")
+        if plan.transform_direction not in SUPPORTED_TRANSFORM_DIRECTIONS:
+            raise ValueError(f"plan transform_direction {plan.transform_direction!r} not supported")
+        if plan.norm not in SUPPORTED_NORMS:
+            raise ValueError(f"plan norm {plan.norm!r} not supported")
+        if plan.params.get("flow_kind") == "composition" and plan.transform_type != "c2c":
+            raise ValueError("composition plans support transform_type='c2c' only")
+        if x.device.type != "cuda":
+            raise ValueError(f"x must be on the GPU (device='cuda'), got {x.device}")
+        if not x.is_contiguous():
+            raise ValueError("x must be contiguous; call .contiguous() first")
+    dev = x.device.index if x.device.index is not None else torch.cuda.current_device()
+    with phase("core-invoke"):
+        nplan, (shape, dt) = _resolve(plan, dev)
+        out = torch.empty(shape, dtype=dt, device=x.device)
+        from .runner import launch
+
+        return launch(nplan, x, out)
+
+
+def run_fft(x, direction: str, *, batch: int | None = None, precision: str = "fp32",
+            profile_hash: str | None = None, table: dict | None = None,
+            transform_type: str = "c2c", transform_direction: str | None = None,
+            norm: str = "backward"):
+    """One-shot plan + execute; returns ``(y, ExecutionReport)``.
+
+    A rank-2 ``(1, N)`` input runs as the batch-1 plan and the output is
+    restored to ``(1, ...)``; for c2r the full length is inferred as
+    ``2*(m-1)`` from the ``m`` half-spectrum bins.
+    """
+    import torch
+
+    if transform_direction is None:
+        transform_direction = "inverse" if transform_type == "c2r" else "forward"
+    _validate_semantics(direction, precision, transform_type, transform_direction, norm)
+    want = torch.float32 if transform_type == "r2c" else getattr(torch, _SUPPORTED_DTYPES[precision])
+    if not isinstance(x, torch.Tensor):
+        raise TypeError(f"x must be a torch.Tensor, got {type(x).__name__}")
+    if x.dtype != want:
+        raise TypeError(f"x must be {want} for transform_type={transform_type} "
+                        f"precision={precision}, got {x.dtype}")
+    squeezed = False
+    if x.dim() == 1:
+        n, b = x.numel(), 1
+    elif x.dim() == 2 and x.shape[0] == 1:
+        x = x[0]
+        n, b = x.numel(), 1
+        squeezed = True
+    elif x.dim() == 2:
+        b, n = int(x.shape[0]), int(x.shape[1])
+    else:
+        raise ValueError(f"x must be rank-1 or rank-2, got dim={x.dim()}")
+    if batch is not None and batch != b:
+        raise ValueError(f"batch={batch} does not match effective batch {b}")
+    if transform_type == "c2r":
+        if n < 2:
+            raise ValueError(f"c2r half-spectrum length {n} too short")
+        n = (n - 1) * 2
+    plan = plan_fft(direction, n, batch=b, precision=precision, profile_hash=profile_hash,
+                    table=table, transform_type=transform_type,
+                    transform_direction=transform_direction, norm=norm)
+    y = execute_fft_plan(plan, x)
+    if squeezed:
+        y = y.unsqueeze(0)
+    return y, plan.as_report()

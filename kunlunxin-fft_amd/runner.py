@@ -1,0 +1,350 @@
+"""Tensor-level runners: the reference's runner names over the native flows.
+
+``execute_fft_plan`` dispatches by ``plan.executed`` exactly like the
+reference (entry.py:549-550: ``getattr(runner, plan.executed)``); here the
+name selects a native flow of ``libmfft.so`` and the plan's parameters:
+
+===========================================  ==============================  =========
+runner name (reference file:line)            native flow                     params
+===========================================  ==============================  =========
+fft_dit, fft_dit_batch (runner.py:118, 781)  RADIX2_DIT (M0, bitrev fold)    block
+fft_dif, fft_dif_batch (runner.py:165, 839)  RADIX2_DIF (M0, bitrev fold)    block
+fft_dit_radix4(_batch) (runner.py:1399,1112) RADIX4_DIT (M5, digit-rev fold) block
+fft_dif_radix4(_batch) (runner.py:1473,1193) RADIX4_DIF (M5)                 block
+fft_lds_fused(_batch)                        LDS_FUSED (single pass)         elems
+fft_four_step(_batch)                        FOUR_STEP (two passes)          n1, chunk_rows
+fft_dit_fused (runner.py:209)                LDS_FUSED / FOUR_STEP (auto)    --
+fft_{dit,dif}_matrix(_batch) (runner.py:379) LDS_FUSED / FOUR_STEP (auto)    --
+fft_{dit,dif}_grouped (runner.py:505)        LDS_FUSED / FOUR_STEP (auto)    --
+run_hybrid (adapter_hybrid.py:224)           FOUR_STEP (n1 = N/tile)         tile
+===========================================  ==============================  =========
+
+The M1/M2/M3 names exist so a plan naming them still runs: on MI355X the
+stages they fuse (in global memory, as a dense matmul, or as XOR-gather
+maps) all run inside one LDS-resident kernel, or the four-step for core
+lengths above 8192.
+
+Every transform semantic -- C2C forward/inverse with its norm, R2C and C2R
+-- is one native plan: the conjugation, the norm scale and the real-FFT
+pack/stitch/pre-twiddle are fused into the kernels, so a call is one
+allocation of the output plus one ``mfft_execute``.  Native plans are cached
+by shape/semantics/flow/device.
+"""
+from __future__ import annotations
+
+import math
+import threading
+import time
+from collections import OrderedDict
+
+import torch
+
+from . import native
+from .context import device_name, device_ready  # noqa: F401  (re-exported)
+from .validate import log2_exact, validate_batch_input, validate_input, validate_tensor
+
+DEFAULT_STAGE_BLOCK = 256
+
+# runner name -> (native flow, parameter kind)
+RUNNER_FLOWS = {
+    "fft_dit": (native.FLOW_RADIX2_DIT, "block"),
+    "fft_dit_batch": (native.FLOW_RADIX2_DIT, "block"),
+    "fft_dif": (native.FLOW_RADIX2_DIF, "block"),
+    "fft_dif_batch": (native.FLOW_RADIX2_DIF, "block"),
+    "fft_dit_radix4": (native.FLOW_RADIX4_DIT, "block"),
+    "fft_dit_radix4_batch": (native.FLOW_RADIX4_DIT, "block"),
+    "fft_dif_radix4": (native.FLOW_RADIX4_DIF, "block"),
+    "fft_dif_radix4_batch": (native.FLOW_RADIX4_DIF, "block"),
+    "fft_lds_fused": (native.FLOW_LDS_FUSED, "lds"),
+    "fft_lds_fused_batch": (native.FLOW_LDS_FUSED, "lds"),
+    "fft_four_step": (native.FLOW_FOUR_STEP, "fourstep"),
+    "fft_four_step_batch": (native.FLOW_FOUR_STEP, "fourstep"),
+    "fft_dit_fused": (native.FLOW_AUTO, "none"),
+    "fft_dit_matrix": (native.FLOW_AUTO, "none"),
+    "fft_dif_matrix": (native.FLOW_AUTO, "none"),
+    "fft_dit_matrix_batch": (native.FLOW_AUTO, "none"),
+    "fft_dif_matrix_batch": (native.FLOW_AUTO, "none"),
+    "fft_dit_grouped": (native.FLOW_AUTO, "none"),
+    "fft_dif_grouped": (native.FLOW_AUTO, "none"),
+    "run_hybrid": (native.FLOW_FOUR_STEP, "hybrid"),
+}
+
+
+def flow_params(executed: str, n: int, transform_type: str, block, params: dict) -> tuple:
+    """(flow id, native params) for one runner name and plan parameters."""
+    if executed not in RUNNER_FLOWS:
+        raise ValueError(f"unknown runner {executed!r}")
+    flow, kind = RUNNER_FLOWS[executed]
+    params = params or {}
+    core = n // 2 if transform_type in ("r2c", "c2r") else n
+    # A legacy table entry measured on the c2c core of length n also answers
+    # r2c/c2r, whose core is n/2: keep its flow where the flow can run that
+    # core, else let the library pick (LDS up to 8192, four-step above).
+    if kind == "lds" and core > 8192:
+        return native.FLOW_AUTO, ()
+    if kind == "fourstep":
+        n1 = int(params.get("n1", 0))
+        if core < 256:
+            return native.FLOW_AUTO, ()
+        if n1 and (core % n1 or not 16 <= core // n1 <= 1024 or not 16 <= n1 <= 1024):
+            n1 = 0
+        return flow, (n1, int(params.get("chunk_rows", 0)))
+    if kind == "block":
+        # a stage flow needs at least one stage (radix-4: one radix-4 stage);
+        # shorter cores (N=1 c2c, N=2 real) run in the single-pass kernel
+        if core < (4 if flow in (native.FLOW_RADIX4_DIT, native.FLOW_RADIX4_DIF) else 2):
+            return native.FLOW_AUTO, ()
+        b = int(block or DEFAULT_STAGE_BLOCK)
+        log2_exact(b)
+        if b < 64 or b > 1024:
+            raise ValueError(f"block must be a power of two in [64, 1024], got {b}")
+        return flow, (b,)
+    if kind == "lds":
+        return flow, (int(params.get("elems", 0)),)
+    if kind == "hybrid":
+        tile = int(params.get("tile", 0))
+        n1 = core // tile if tile and core % tile == 0 else 0
+        return flow, (n1, 0)
+    return flow, ()
+
+
+_NATIVE: "OrderedDict[tuple, native.NativePlan]" = OrderedDict()
+_NATIVE_LOCK = threading.Lock()
+NATIVE_CACHE_SIZE = 32
+
+
+def get_native_plan(executed: str, n: int, batch: int, transform_type: str,
+                    transform_direction: str, norm: str, block, params: dict,
+                    device_index: int) -> native.NativePlan:
+    """Cached native plan for one (runner, shape, semantics, params, device)."""
+    flow, prm = flow_params(executed, n, transform_type, block, params)
+    key = (flow, prm, int(n), int(batch), transform_type, transform_direction, norm, int(device_index))
+    with _NATIVE_LOCK:
+        p = _NATIVE.get(key)
+        if p is not None:
+            _NATIVE.move_to_end(key)
+            return p
+    with torch.cuda.device(device_index):
+        p = native.NativePlan(n, batch, transform_type, transform_direction, norm, flow, prm)
+    with _NATIVE_LOCK:
+        _NATIVE[key] = p
+        while len(_NATIVE) > NATIVE_CACHE_SIZE:
+            _NATIVE.popitem(last=False)
+    return p
+
+
+def clear_native_cache() -> None:
+    with _NATIVE_LOCK:
+        _NATIVE.clear()
+
+
+def output_spec(transform_type: str, n: int, batch: int):
+    """(shape, dtype) of a plan's output; rank-1 for batch 1 (entry.py:488-493)."""
+    if transform_type == "r2c":
+        last, dt = n // 2 + 1, torch.complex64
+    elif transform_type == "c2r":
+        last, dt = n, torch.float32
+    else:
+        last, dt = n, torch.complex64
+    return ((last,) if batch == 1 else (batch, last)), dt
+
+
+def launch(nplan: native.NativePlan, x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """Enqueue one execute on x's device and current stream."""
+    dev = x.device.index if x.device.index is not None else torch.cuda.current_device()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    if torch.cuda.current_device() == dev:
+        nplan.execute(x.data_ptr(), out.data_ptr(), stream)
+    else:
+        with torch.cuda.device(dev):
+            nplan.execute(x.data_ptr(), out.data_ptr(), stream)
+    return out
+
+
+def run(executed: str, x: torch.Tensor, batch: int, n: int, transform_type: str = "c2c",
+        transform_direction: str = "forward", norm: str = "backward", block=None,
+        params: dict | None = None) -> torch.Tensor:
+    """Run one transform of ``x`` through the named runner; returns a new tensor."""
+    dev = x.device.index if x.device.index is not None else torch.cuda.current_device()
+    nplan = get_native_plan(executed, n, batch, transform_type, transform_direction, norm,
+                            block, params or {}, dev)
+    shape, dt = output_spec(transform_type, n, batch)
+    out = torch.empty(shape, dtype=dt, device=x.device)
+    return launch(nplan, x, out)
+
+
+# ---------------- reference runner entry points (forward C2C) ----------------
+
+def _single(name, x, block, params=None):
+    validate_input(x, "x", block=block)
+    return run(name, x, 1, x.numel(), block=block, params=params, norm="backward")
+
+
+def _batched(name, x, block, params=None):
+    validate_batch_input(x, "x", block=block)
+    b, n = int(x.shape[0]), int(x.shape[1])
+    y = run(name, x, b, n, block=block, params=params, norm="backward")
+    return y.reshape(b, n)
+
+
+def fft_dit(x, block: int = DEFAULT_STAGE_BLOCK, twiddle=None):
+    """M0 radix-2 DIT: log2(N) stage launches, bit reversal folded into stage 0."""
+    return _single("fft_dit", x, block)
+
+
+def fft_dif(x, block: int = DEFAULT_STAGE_BLOCK, twiddle=None):
+    """M0 radix-2 DIF: log2(N) stage launches, bit reversal folded into the last."""
+    return _single("fft_dif", x, block)
+
+
+def fft_dit_batch(x, block: int = DEFAULT_STAGE_BLOCK, variant: str = "folded"):
+    """M4: M0 over a (B, N) batch folded into one 1-D grid per stage."""
+    _check_variant(variant)
+    return _batched("fft_dit_batch", x, block)
+
+
+def fft_dif_batch(x, block: int = DEFAULT_STAGE_BLOCK, variant: str = "folded"):
+    _check_variant(variant)
+    return _batched("fft_dif_batch", x, block)
+
+
+def fft_dit_radix4(x, block: int = DEFAULT_STAGE_BLOCK, twiddle=None):
+    """M5 radix-4 DIT (radix-2 tail for odd log2 N), digit reversal folded in."""
+    if x.numel() < 4:
+        raise ValueError(f"radix-4 requires N >= 4, got N={x.numel()}")
+    return _single("fft_dit_radix4", x, block)
+
+
+def fft_dif_radix4(x, block: int = DEFAULT_STAGE_BLOCK, twiddle=None):
+    if x.numel() < 4:
+        raise ValueError(f"radix-4 requires N >= 4, got N={x.numel()}")
+    return _single("fft_dif_radix4", x, block)
+
+
+def fft_dit_radix4_batch(x, block: int = DEFAULT_STAGE_BLOCK, variant: str = "folded"):
+    _check_variant(variant)
+    return _batched("fft_dit_radix4_batch", x, block)
+
+
+def fft_dif_radix4_batch(x, block: int = DEFAULT_STAGE_BLOCK, variant: str = "folded"):
+    _check_variant(variant)
+    return _batched("fft_dif_radix4_batch", x, block)
+
+
+def fft_lds_fused(x, elems: int = 0):
+    """Single-pass LDS-resident Stockham FFT (core length <= 8192)."""
+    return _single("fft_lds_fused", x, None, {"elems": elems})
+
+
+def fft_lds_fused_batch(x, elems: int = 0):
+    return _batched("fft_lds_fused_batch", x, None, {"elems": elems})
+
+
+def fft_four_step(x, n1: int = 0, chunk_rows: int = 0):
+    """Two-pass four-step FFT (column pass + twiddle, in-place row pass)."""
+    return _single("fft_four_step", x, None, {"n1": n1, "chunk_rows": chunk_rows})
+
+
+def fft_four_step_batch(x, n1: int = 0, chunk_rows: int = 0):
+    return _batched("fft_four_step_batch", x, None, {"n1": n1, "chunk_rows": chunk_rows})
+
+
+def fft_dit_fused(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64):
+    """Reference M1 name: all stages fused on chip (LDS kernel)."""
+    return _single("fft_dit_fused", x, None)
+
+
+def fft_dit_matrix(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64, rows: int = 8):
+    """Reference M2 name: runs the LDS / four-step kernels on MI355X."""
+    return _single("fft_dit_matrix", x, None)
+
+
+def fft_dif_matrix(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64, rows: int = 8):
+    return _single("fft_dif_matrix", x, None)
+
+
+def fft_dit_matrix_batch(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64, rows: int = 8,
+                         variant: str = "spread"):
+    return _batched("fft_dit_matrix_batch", x, None)
+
+
+def fft_dif_matrix_batch(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64, rows: int = 8,
+                         variant: str = "spread"):
+    return _batched("fft_dif_matrix_batch", x, None)
+
+
+def fft_dit_grouped(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64, rows: int = 8,
+                    glog: int = 2, maxp: int = 4096, cells: int = 1):
+    """Reference M3 name: runs the LDS / four-step kernels on MI355X."""
+    return _single("fft_dit_grouped", x, None)
+
+
+def fft_dif_grouped(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64, rows: int = 8,
+                    glog: int = 2, maxp: int = 4096, cells: int = 1):
+    return _single("fft_dif_grouped", x, None)
+
+
+def _check_variant(variant: str) -> None:
+    if variant not in ("folded", "spread"):
+        raise ValueError(f"variant must be 'folded' or 'spread', got {variant!r}")
+
+
+def bit_reverse_permute(x):
+    """Y[r][bit_reverse(i)] = X[r][i] (reference runner.py:1542-1552)."""
+    validate_tensor(x, "x", dtype=torch.complex64)
+    n = int(x.shape[-1])
+    log2_exact(n)
+    b = 1 if x.dim() == 1 else int(x.shape[0])
+    out = torch.empty_like(x)
+    dev = x.device.index if x.device.index is not None else torch.cuda.current_device()
+    with torch.cuda.device(dev):
+        native.bit_reverse_permute(x.data_ptr(), out.data_ptr(), n, b,
+                                   torch.cuda.current_stream(dev).cuda_stream)
+    return out
+
+
+def twiddle_tables(n: int, device):
+    """Planar (cos, sin) float32 of exp(-2*pi*i*idx/n), idx in [0, n/2)
+    (reference runner.py:93-97); computed in float64 and rounded once.
+    The native plans build their own tables; this is an inspection helper."""
+    log2_exact(n)
+    idx = torch.arange(n >> 1, dtype=torch.float64)
+    ang = -2.0 * math.pi * idx / n
+    return (torch.cos(ang).to(torch.float32).to(device), torch.sin(ang).to(torch.float32).to(device))
+
+
+def time_call(fn, *args, warmup: int = 5, trials: int = 50, **kwargs) -> float:
+    """Median wall time (ms) of fn(*args) with a device sync per trial."""
+    for _ in range(warmup):
+        fn(*args, **kwargs)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(trials):
+        t0 = time.perf_counter()
+        fn(*args, **kwargs)
+        torch.cuda.synchronize()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def time_call_detailed(fn, *args, warmup: int = 5, trials: int = 50, **kwargs) -> dict:
+    """Wall-time and HIP-event medians (ms) of fn(*args) on the current stream."""
+    for _ in range(warmup):
+        fn(*args, **kwargs)
+    torch.cuda.synchronize()
+    wall, ev = [], []
+    for _ in range(trials):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        s.record()
+        fn(*args, **kwargs)
+        e.record()
+        torch.cuda.synchronize()
+        wall.append((time.perf_counter() - t0) * 1e3)
+        ev.append(s.elapsed_time(e))
+    wall.sort()
+    ev.sort()
+    return {"wall_ms_p50": wall[len(wall) // 2], "event_ms_p50": ev[len(ev) // 2],
+            "wall_ms_min": wall[0], "trials": trials}

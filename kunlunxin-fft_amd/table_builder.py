@@ -1,0 +1,209 @@
+"""Build the MI355X selector table from live measurements.
+
+MI355X counterpart of the reference's table builder
+(scripts/build_selector_table.py; table schema of src/xpu/selector.py:6-41).
+For every cell (N, batch, direction) it times the M0 incumbent (fft_dit /
+fft_dif and their batch forms) and every legal challenger of the published
+design space (config/butterfly_space.json): the radix-4 global-stage flow,
+the single-pass LDS kernel at each elements-per-thread setting, and the
+four-step at each split and chunking.  The fastest challenger is promoted
+only when it beats the incumbent by at least GUARD_PCT percent (M0 closure);
+otherwise the cell keeps M0.  The table is bound to the device profile hash
+and the live environment fingerprint, so it selects only on the stack it was
+measured on.
+
+Timing: forward C2C complex64, inputs resident on the GPU, ``reps``
+back-to-back executes bracketed by HIP events on the launch stream, median of
+``rounds`` such groups (ms per execute, launch gaps included).
+
+Usage (on a GPU box):
+    python kunlunxin-fft_amd/table_builder.py --out path/selector_table.json [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+
+C5_SIZES = [1 << k for k in range(4, 15)]        # N = 16 .. 2^14
+C5_BATCHES = [1, 16, 64, 256]
+ROOF_SIZES = [1 << k for k in range(10, 21)]      # roofline rows: B = max(64, 2^25/N)
+EXTRA_CELLS = [(1 << k, 1) for k in range(15, 21)] + [(1 << 16, 256), (256, 1), (4096, 64)]
+
+
+def cells(quick: bool = False):
+    out = []
+    for n in C5_SIZES:
+        for b in C5_BATCHES:
+            out.append((n, b))
+    for n in ROOF_SIZES:
+        out.append((n, max(64, (1 << 25) // n)))
+    out += EXTRA_CELLS
+    seen, uniq = set(), []
+    for c in out:
+        if c not in seen:
+            seen.add(c)
+            uniq.append(c)
+    if quick:
+        uniq = [c for c in uniq if c[0] * c[1] <= (1 << 22) or c[1] == 1]
+    return uniq
+
+
+def candidates(n: int, b: int, direction: str, space):
+    """(label, runner name, block, params, family) for every legal challenger."""
+    sfx = "" if b == 1 else "_batch"
+    logn = int(math.log2(n))
+    out = []
+    if n >= 4:
+        name = ("fft_dit_radix4" if direction == "dit" else "fft_dif_radix4") + sfx
+        out.append((f"m5_{direction}@256", name, 256, {}, ("global-stage", "radix4-scalar", "baseline-global-stage")))
+    if n <= space.lds_max_n:
+        for e in space.lds_elems:
+            if logn == 13 and e != 16:
+                continue
+            if n <= 16 and e != 16:
+                continue
+            out.append((f"lds_e{e}", "fft_lds_fused" + sfx, 256, {"elems": e},
+                        ("lds-resident", "stockham-radix16", "lds-stockham-single-pass")))
+    if space.fourstep_min_n <= n <= (1 << 20):
+        for n1 in space.fourstep_n1:
+            n2 = n // n1
+            if n2 < 16 or n2 > 1024 or n % n1:
+                continue
+            # keep splits near square (the other ones are never faster)
+            if abs(int(math.log2(n1)) - int(math.log2(n2))) > 2:
+                continue
+            chunks = [0]
+            if b >= 16 and n >= (1 << 14):
+                chunks += [c for c in space.fourstep_chunk_rows if c and c < b and n * c * 8 >= (16 << 20)
+                           and n * c * 8 <= (128 << 20)]
+            for ch in chunks:
+                out.append((f"fs_n1_{n1}_c{ch}", "fft_four_step" + sfx, 256, {"n1": n1, "chunk_rows": ch},
+                            ("four-step", "stockham-radix16", "four-step-two-pass")))
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--out", required=True)
+    ap.add_argument("--quick", action="store_true")
+    ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--rounds", type=int, default=3)
+    args = ap.parse_args()
+
+    import numpy as np  # noqa: F401
+    import torch
+
+    sys.path.insert(0, ROOT)
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    from kunlunxin_fft_amd import envcheck
+    from kunlunxin_fft_amd.config import DesignSpace, DeviceProfile
+    from kunlunxin_fft_amd.entry import ExecutionPlan
+    from kunlunxin_fft_amd.runner import get_native_plan, output_spec
+    from kunlunxin_fft_amd.selector import GUARD_PCT
+
+    space = DesignSpace.load()
+    env = envcheck.collect()
+    env_hash = envcheck.current_env_hash()
+    if env is None or env_hash is None:
+        print("environment fingerprint unknown: refusing to build a table", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+
+    def time_runner(name, n, b, block, params, x):
+        np_ = get_native_plan(name, n, b, "c2c", "forward", "backward", block, params, 0)
+        shape, dt = output_spec("c2c", n, b)
+        out = torch.empty(shape, dtype=dt, device=dev)
+        for _ in range(3):
+            np_.execute(x.data_ptr(), out.data_ptr(), stream.cuda_stream)
+        res = []
+        for _ in range(args.rounds):
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record(stream)
+            for _ in range(args.reps):
+                np_.execute(x.data_ptr(), out.data_ptr(), stream.cuda_stream)
+            e.record(stream)
+            e.synchronize()
+            res.append(s.elapsed_time(e) / args.reps)
+        return statistics.median(res)
+
+    entries, sweep = [], []
+    t_start = time.time()
+    for (n, b) in cells(args.quick):
+        shape = (n,) if b == 1 else (b, n)
+        x = torch.randn(shape, dtype=torch.complex64, device=dev, generator=gen)
+        for direction in ("dit", "dif"):
+            inc_name = ("fft_dit" if direction == "dit" else "fft_dif") + ("" if b == 1 else "_batch")
+            inc_ms = time_runner(inc_name, n, b, 256, {}, x) if n >= 2 else float("inf")
+            best = None
+            row = {"N": n, "batch": b, "direction": direction, f"m0_{direction}@256": round(inc_ms, 5)}
+            for label, name, block, params, fam in candidates(n, b, direction, space):
+                ms = time_runner(name, n, b, block, params, x)
+                row[label] = round(ms, 5)
+                if best is None or ms < best[0]:
+                    best = (ms, label, name, block, params, fam)
+            sweep.append(row)
+            gain = (inc_ms - best[0]) / inc_ms * 100.0 if best else -1.0
+            if best is not None and gain >= GUARD_PCT:
+                ms, label, name, block, params, (real, unit, flow_id) = best
+                entry = {"N": n, "batch": b, "direction": direction, "incumbent_ms": inc_ms,
+                         "incumbent_block": 256, "challenger_ms": ms,
+                         "evidence": {"incumbent": f"m0_{direction}@256", "challenger": label,
+                                      "gain_pct": round(gain, 2)},
+                         "reason": f"challenger {label} beats M0 incumbent m0_{direction}@256 by "
+                                   f"{gain:.1f}% (>= {GUARD_PCT}%)",
+                         "block": block, "flow_id": flow_id, "flow_realization": real,
+                         "processing_unit": unit, "params": dict(params), "executed": name}
+            else:
+                entry = {"N": n, "batch": b, "direction": direction, "incumbent_ms": inc_ms,
+                         "incumbent_block": 256, "challenger_ms": best[0] if best else None,
+                         "evidence": {"incumbent": f"m0_{direction}@256",
+                                      "challenger": best[1] if best else None,
+                                      "gain_pct": round(gain, 2)},
+                         "reason": f"no challenger beats M0 by {GUARD_PCT}%; M0 kept",
+                         "block": 256, "flow_id": "baseline-global-stage",
+                         "flow_realization": "global-stage", "processing_unit": "radix2-scalar",
+                         "params": {}, "executed": inc_name}
+            if b > 1:
+                entry["params"]["variant"] = "folded"
+            entries.append(entry)
+            print(f"N={n:>8} B={b:>6} {direction}: M0 {inc_ms:.4f} ms, best {best[1] if best else '-'} "
+                  f"{best[0] if best else float('nan'):.4f} ms ({gain:+.1f}%) -> {entry['executed']} "
+                  f"[{time.time() - t_start:.0f}s]", flush=True)
+        del x
+    table = {
+        "schema_version": 1, "device": DeviceProfile.load().device,
+        "profile_hash": DeviceProfile.load().hash(), "env_hash": env_hash,
+        "env": {**env, "device_model": env["gfx_arch"]},
+        "precision": "fp32", "guard_pct": GUARD_PCT,
+        "selection_semantics": "median of rounds x (reps back-to-back executes / reps), HIP events; "
+                               "forward C2C complex64; legacy entries answer every semantic",
+        "sources": ["kunlunxin-fft_amd/table_builder.py live sweep"],
+        "entries": entries, "previous_fallbacks": [],
+    }
+    with open(args.out, "w") as f:
+        json.dump(table, f, indent=1)
+    with open(os.path.splitext(args.out)[0] + "_sweep.json", "w") as f:
+        json.dump(sweep, f, indent=1)
+    # the table must pass its own loader's contract
+    pkg.load_table(args.out)
+    print(f"wrote {args.out} ({len(entries)} entries)", flush=True)
+    del ExecutionPlan
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

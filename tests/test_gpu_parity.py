@@ -1,0 +1,355 @@
+"""GPU parity: every native flow against the CPU oracle (float64), through the
+C ABI (via the package's plan API or the ctypes NativePlan).
+
+Gate (north star): relative L2 error <= 1e-5 against the float64 oracle, and
+the reference's peak-normalised worst-element error (max_rel_error) <= 1e-5
+(the reference's own worst published figure is ~1.2e-6; its gate 1e-4).
+At BASELINE's full sizes the C oracle is checked on a subset of rows and
+numpy's float64 FFT on all rows, plus size-independent properties (round
+trip, Parseval, linearity).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from kunlunxin_fft_amd import (
+    DeviceProfile, ExecutionPlan, execute_fft_plan, native, plan_fft, run_fft,
+)
+from kunlunxin_fft_amd.runner import bit_reverse_permute, run
+
+pytestmark = pytest.mark.gpu
+
+RTOL_L2 = 1e-5
+RTOL_MAX = 1e-5
+
+
+def seeded_c64(n, b, session=0):
+    """scripts/issue10_wp3_holdout.py:127-140 input protocol."""
+    rng = np.random.default_rng(102026 + 100000 * session + 10 * n + b)
+    x = (rng.standard_normal((b, n)) + 1j * rng.standard_normal((b, n))).astype(np.complex64)
+    return x[0] if b == 1 else x
+
+
+def seeded_f32(n, b, session=0):
+    rng = np.random.default_rng(102026 + 100000 * session + 10 * n + b)
+    x = rng.standard_normal((b, n)).astype(np.float32)
+    return x[0] if b == 1 else x
+
+
+def mkplan(executed, n, b, tt="c2c", td="forward", norm="backward", params=None, block=256):
+    return ExecutionPlan(n=n, batch=b, direction="dit", precision="fp32", selection_source="table",
+                         reason="test", fallback=False, executed=executed, block=block,
+                         flow_id="test", flow_realization="test", processing_unit="test",
+                         params=params or {}, transform_type=tt, transform_direction=td, norm=norm)
+
+
+def check(got, ref, label):
+    l2 = oracle.rel_l2(got, ref)
+    mx = oracle.max_rel_error(got, ref)
+    assert l2 <= RTOL_L2 and mx <= RTOL_MAX, f"{label}: rel_l2={l2:.3e} max_rel={mx:.3e}"
+    return l2, mx
+
+
+def np_ref(x, td, norm):
+    n = x.shape[-1]
+    if td == "forward":
+        return np.fft.fft(x.astype(np.complex128), norm="backward" if norm == "none" else norm)
+    if norm in ("none", "forward"):
+        return np.fft.ifft(x.astype(np.complex128), norm="backward") * n
+    return np.fft.ifft(x.astype(np.complex128), norm=norm)
+
+
+def test_single_hip_runtime_in_process(gpu):
+    """The library must bind to torch's HIP runtime, not load a second one."""
+    torch.zeros(1, device=gpu)
+    native.load()
+    maps = open("/proc/self/maps").read()
+    paths = {ln.split()[-1] for ln in maps.splitlines() if "libamdhip64" in ln}
+    assert len(paths) == 1, paths
+
+
+# ---------------------------------------------------------------- C2C flows
+FLOW_CASES = []
+for name in ("fft_dit", "fft_dif"):
+    FLOW_CASES += [(name, n) for n in (2, 8, 64, 1024, 4096, 1 << 15)]
+for name in ("fft_dit_radix4", "fft_dif_radix4"):
+    FLOW_CASES += [(name, n) for n in (4, 8, 32, 256, 2048, 1 << 15)]
+FLOW_CASES += [("fft_lds_fused", n) for n in (1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192)]
+FLOW_CASES += [("fft_four_step", n) for n in (256, 1024, 4096, 1 << 14, 1 << 16, 1 << 18, 1 << 20)]
+
+
+@pytest.mark.parametrize("name,n", FLOW_CASES)
+@pytest.mark.parametrize("b", [1, 3])
+def test_c2c_forward_matches_oracle(gpu, name, n, b):
+    if n >= (1 << 18) and b > 1:
+        pytest.skip("large-N batch covered by the config tests")
+    x = seeded_c64(n, b)
+    bname = name + "_batch" if b > 1 else name
+    y = execute_fft_plan(mkplan(bname, n, b), torch.from_numpy(x).to(gpu)).cpu().numpy()
+    ref = oracle.fft_dit(x) if n <= (1 << 16) else np.fft.fft(x.astype(np.complex128))
+    check(y, ref, f"{bname} N={n} B={b}")
+
+
+@pytest.mark.parametrize("name", ["fft_dit", "fft_dif", "fft_dit_radix4", "fft_dif_radix4",
+                                  "fft_lds_fused", "fft_four_step"])
+@pytest.mark.parametrize("norm", ["none", "forward", "backward", "ortho"])
+@pytest.mark.parametrize("td", ["forward", "inverse"])
+def test_c2c_all_norms(gpu, name, norm, td):
+    n, b = 1024, 5
+    x = seeded_c64(n, b, session=1)
+    y = execute_fft_plan(mkplan(name + "_batch", n, b, td=td, norm=norm),
+                         torch.from_numpy(x).to(gpu)).cpu().numpy()
+    check(y, oracle.c2c(x, td, norm), f"{name} {td} {norm}")
+
+
+@pytest.mark.parametrize("elems", [4, 8, 16])
+@pytest.mark.parametrize("n", [32, 256, 2048, 4096])
+def test_lds_elems_axis_neutral(gpu, elems, n):
+    x = seeded_c64(n, 7)
+    y = execute_fft_plan(mkplan("fft_lds_fused_batch", n, 7, params={"elems": elems}),
+                         torch.from_numpy(x).to(gpu)).cpu().numpy()
+    check(y, oracle.fft_dit(x), f"lds elems={elems} N={n}")
+
+
+@pytest.mark.parametrize("n,n1", [(256, 16), (512, 32), (1 << 12, 16), (1 << 12, 256), (1 << 16, 64),
+                                  (1 << 16, 1024), (1 << 20, 1024), (1 << 14, 512)])
+@pytest.mark.parametrize("chunk", [0, 2])
+def test_four_step_split_and_chunk_neutral(gpu, n, n1, chunk):
+    b = 3 if n <= (1 << 16) else 2
+    x = seeded_c64(n, b, session=2)
+    y = execute_fft_plan(mkplan("fft_four_step_batch", n, b, params={"n1": n1, "chunk_rows": chunk}),
+                         torch.from_numpy(x).to(gpu)).cpu().numpy()
+    check(y, np.fft.fft(x.astype(np.complex128)), f"four-step N={n} n1={n1} chunk={chunk}")
+
+
+# ---------------------------------------------------------------- real flows
+REAL_CASES = [("fft_lds_fused", n) for n in (2, 4, 8, 64, 256, 4096, 8192, 16384)]
+REAL_CASES += [("fft_four_step", n) for n in (512, 1 << 15, 1 << 20)]
+REAL_CASES += [("fft_dit", n) for n in (4, 256, 4096)] + [("fft_dif_radix4", n) for n in (8, 256)]
+
+
+@pytest.mark.parametrize("name,n", REAL_CASES)
+@pytest.mark.parametrize("norm", ["backward", "ortho", "forward", "none"])
+def test_r2c_c2r_match_oracle(gpu, name, n, norm):
+    b = 4 if n <= (1 << 15) else 1
+    xr = seeded_f32(n, b)
+    bname = name + ("_batch" if b > 1 else "")
+    X = execute_fft_plan(mkplan(bname, n, b, tt="r2c", norm=norm), torch.from_numpy(xr).to(gpu))
+    check(X.cpu().numpy(), oracle.r2c_dedicated(xr, norm), f"r2c {name} N={n} {norm}")
+    Xh = np.ascontiguousarray(oracle.r2c_dedicated(xr, "backward").astype(np.complex64))
+    y = execute_fft_plan(mkplan(bname, n, b, tt="c2r", td="inverse", norm=norm),
+                         torch.from_numpy(Xh).to(gpu)).cpu().numpy()
+    check(y, oracle.c2r_dedicated(Xh, n, norm), f"c2r {name} N={n} {norm}")
+
+
+@pytest.mark.parametrize("name", ["fft_lds_fused", "fft_four_step", "fft_dit"])
+def test_c2r_ignores_dc_nyquist_imag(gpu, golden, name):
+    n = 256
+    h = golden[f"irfft_in_{n}"].astype(np.complex64)
+    if name == "fft_four_step":
+        n2 = 1024
+        rng = np.random.default_rng(1)
+        h = (rng.standard_normal(n2 // 2 + 1) + 1j * rng.standard_normal(n2 // 2 + 1)).astype(np.complex64)
+        ref = np.fft.irfft(h.astype(np.complex128), n=n2)
+        n = n2
+    else:
+        ref = golden[f"irfft_out_{n}"]
+    y = execute_fft_plan(mkplan(name, n, 1, tt="c2r", td="inverse"), torch.from_numpy(h).to(gpu)).cpu().numpy()
+    check(y, ref, f"c2r DC/Nyquist {name}")
+
+
+# ------------------------------------------------------- BASELINE configs
+def test_config1_n2048_b1(gpu, golden):
+    x = golden["c1_in"]
+    plan = plan_fft("dit", 2048, profile_hash=DeviceProfile.load().hash())
+    y = execute_fft_plan(plan, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    check(y, golden["c1_out"], f"C1 via {plan.executed}")
+    check(y, oracle.fft_dit(x), "C1 vs C oracle")
+    if oracle.reference_lib() is not None:
+        check(y, oracle.reference_fft(x), "C1 vs reference build")
+
+
+@pytest.mark.parametrize("n", [1024, 2048])
+@pytest.mark.parametrize("b", [16, 64])
+@pytest.mark.parametrize("direction", ["dit", "dif"])
+def test_config2_batched(gpu, n, b, direction):
+    x = seeded_c64(n, b)
+    plan = plan_fft(direction, n, batch=b, profile_hash=DeviceProfile.load().hash())
+    y = execute_fft_plan(plan, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    check(y, oracle.fft_dit(x), f"C2 N={n} B={b} via {plan.executed}")
+    y2 = execute_fft_plan(mkplan("fft_lds_fused_batch", n, b), torch.from_numpy(x).to(gpu)).cpu().numpy()
+    check(y2, oracle.fft_dit(x), f"C2 LDS N={n} B={b}")
+
+
+@pytest.mark.parametrize("n", [256, 4096])
+@pytest.mark.parametrize("b", [1, 64])
+@pytest.mark.parametrize("norm", ["none", "forward", "backward", "ortho"])
+def test_config3_inverse_and_real_round_trip(gpu, n, b, norm):
+    prof = DeviceProfile.load().hash()
+    x = seeded_c64(n, b)
+    inv = plan_fft("dit", n, batch=b, profile_hash=prof, transform_direction="inverse", norm=norm)
+    y = execute_fft_plan(inv, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    check(y, np_ref(x, "inverse", norm), f"C3 inverse N={n} B={b} {norm}")
+    xr = seeded_f32(n, b)
+    r2c = plan_fft("dit", n, batch=b, profile_hash=prof, transform_type="r2c", norm=norm)
+    c2r = plan_fft("dit", n, batch=b, profile_hash=prof, transform_type="c2r", norm=norm)
+    X = execute_fft_plan(r2c, torch.from_numpy(xr).to(gpu))
+    npn = "backward" if norm == "none" else norm
+    check(X.cpu().numpy(), np.fft.rfft(xr.astype(np.float64), norm=npn), f"C3 r2c N={n} B={b} {norm}")
+    back = execute_fft_plan(c2r, X).cpu().numpy()
+    # c2r(r2c(x)) = x * (fwd scale * inv scale * n)
+    k = {"none": n, "forward": 1.0, "backward": 1.0, "ortho": 1.0}[norm]
+    check(back, xr.astype(np.float64) * k, f"C3 round trip N={n} B={b} {norm}")
+
+
+def test_config4_n2p20_b1(gpu):
+    n = 1 << 20
+    x = seeded_c64(n, 1)
+    plan = plan_fft("dit", n, profile_hash=DeviceProfile.load().hash())
+    xd = torch.from_numpy(x).to(gpu)
+    y = execute_fft_plan(plan, xd)
+    check(y.cpu().numpy(), oracle.fft_dit(x), f"C4 N=2^20 via {plan.executed}")
+    inv = plan_fft("dit", n, profile_hash=DeviceProfile.load().hash(), transform_direction="inverse")
+    back = execute_fft_plan(inv, y).cpu().numpy()
+    check(back, x.astype(np.complex128), "C4 round trip")
+
+
+def test_config4_n2p16_b256(gpu):
+    n, b = 1 << 16, 256
+    x = seeded_c64(n, b)
+    plan = plan_fft("dit", n, batch=b, profile_hash=DeviceProfile.load().hash())
+    xd = torch.from_numpy(x).to(gpu)
+    y = execute_fft_plan(plan, xd).cpu().numpy()
+    check(y[:4], oracle.fft_dit(x[:4]), f"C4 N=2^16 B=256 rows 0-3 vs C oracle ({plan.executed})")
+    check(y, np.fft.fft(x.astype(np.complex128)), "C4 N=2^16 B=256 vs numpy")
+    # Parseval per row: sum |X|^2 = N * sum |x|^2
+    ex = (np.abs(x.astype(np.complex128)) ** 2).sum(axis=1) * n
+    ey = (np.abs(y.astype(np.complex128)) ** 2).sum(axis=1)
+    assert np.abs(ey / ex - 1).max() < 1e-5
+
+
+@pytest.mark.parametrize("n", [16, 64, 256, 1024, 4096, 16384])
+@pytest.mark.parametrize("b", [1, 16, 64, 256])
+def test_config5_selector_and_m0_cells(gpu, n, b):
+    prof = DeviceProfile.load().hash()
+    x = seeded_c64(n, b)
+    xd = torch.from_numpy(x).to(gpu)
+    ref = oracle.fft_dit(x) if n * b <= (1 << 20) else np.fft.fft(x.astype(np.complex128))
+    plan = plan_fft("dit", n, batch=b, profile_hash=prof)
+    check(execute_fft_plan(plan, xd).cpu().numpy(), ref, f"C5 N={n} B={b} selector ({plan.executed})")
+    m0 = mkplan("fft_dit" if b == 1 else "fft_dit_batch", n, b)
+    check(execute_fft_plan(m0, xd).cpu().numpy(), ref, f"C5 N={n} B={b} M0")
+
+
+# --------------------------------------------------------- properties, KATs
+@pytest.mark.parametrize("name", ["fft_lds_fused", "fft_four_step", "fft_dit_radix4"])
+def test_linearity(gpu, name):
+    n, b = 4096, 4
+    a = seeded_c64(n, b)
+    c = seeded_c64(n, b, session=3)
+    alpha = 0.75 - 0.25j
+    mix = (alpha * a.astype(np.complex128) + c).astype(np.complex64)
+    p = mkplan(name + "_batch", n, b)
+    run_ = lambda h: execute_fft_plan(p, torch.from_numpy(h).to(gpu)).cpu().numpy().astype(np.complex128)
+    check(run_(mix), alpha * run_(a) + run_(c), f"linearity {name}")
+
+
+def test_known_signals(gpu, golden):
+    for name in ("fft_dit", "fft_lds_fused", "fft_four_step"):
+        for kin, kout in (("impulse256_in", "impulse256_out"), ("tone256_in", "tone256_out")):
+            x = golden[kin].astype(np.complex64)
+            y = execute_fft_plan(mkplan(name, 256, 1), torch.from_numpy(x).to(gpu)).cpu().numpy()
+            assert np.abs(y - golden[kout]).max() < 1e-4, (name, kin)
+        s = golden["sentinel1024_in"].astype(np.complex64)
+        y = execute_fft_plan(mkplan(name, 1024, 1), torch.from_numpy(s).to(gpu)).cpu().numpy()
+        dc = golden["sentinel1024_dc"][0]
+        assert abs(y[0] - dc) < 1e-2 * abs(dc) and np.isfinite(y).all() and not np.array_equal(y, s)
+
+
+@pytest.mark.parametrize("n", [8, 16, 64, 256, 1024, 4096])
+def test_fft_check_kat(gpu, golden, n):
+    x = golden[f"kat_in_{n}"].astype(np.complex64)
+    for name in ("fft_dit", "fft_dif", "fft_dit_radix4", "fft_dif_radix4", "fft_lds_fused"):
+        y = execute_fft_plan(mkplan(name, n, 1), torch.from_numpy(x).to(gpu)).cpu().numpy()
+        check(y, golden[f"kat_out_{n}"], f"KAT {name} N={n}")
+
+
+def test_bit_reverse_permute(gpu, golden):
+    n = 64
+    x = torch.complex(torch.arange(n, dtype=torch.float32), torch.arange(n, dtype=torch.float32) * 0.5).to(gpu)
+    y = bit_reverse_permute(x).cpu()
+    expect = [oracle.bit_reverse(i, 6) for i in range(n)]
+    assert torch.equal(y.real.to(torch.int64)[expect], x.real.cpu().to(torch.int64))
+    x8 = torch.arange(8, dtype=torch.float32).to(torch.complex64).to(gpu)
+    y8 = bit_reverse_permute(x8).cpu().real.to(torch.int64).tolist()
+    assert [y8.index(i) for i in range(8)] == list(golden["bitrev8"])
+
+
+def test_reexecution_is_bitwise_stable_and_one_shot_matches(gpu):
+    prof = DeviceProfile.load().hash()
+    for n, b in ((128, 1), (2048, 16), (1 << 16, 2)):
+        x = torch.from_numpy(seeded_c64(n, b)).to(gpu)
+        plan = plan_fft("dit", n, batch=b, profile_hash=prof)
+        y1 = execute_fft_plan(plan, x)
+        y2 = execute_fft_plan(plan, x)
+        assert torch.equal(y1, y2)
+        y3, rep = run_fft(x, "dit", profile_hash=prof)
+        assert torch.equal(y1, y3) and rep.executed == plan.executed
+
+
+def test_run_fft_squeezes_and_infers_c2r_length(gpu):
+    x = torch.from_numpy(seeded_c64(256, 1)).to(gpu).unsqueeze(0)
+    y, rep = run_fft(x, "dit")
+    assert y.shape == (1, 256) and rep.batch == 1
+    h = torch.from_numpy(oracle.r2c_dedicated(seeded_f32(256, 1)).astype(np.complex64)).to(gpu)
+    r, rep = run_fft(h, "dit", transform_type="c2r")
+    assert r.shape == (256,) and rep.n == 256 and r.dtype == torch.float32
+
+
+def test_input_validation_raises_before_launch(gpu):
+    p = mkplan("fft_lds_fused", 16, 1)
+    good = torch.ones(16, dtype=torch.complex64, device=gpu)
+    with pytest.raises(TypeError):
+        execute_fft_plan(p, good.real.contiguous())
+    with pytest.raises(ValueError):
+        execute_fft_plan(p, good.reshape(4, 4))
+    with pytest.raises(ValueError):
+        execute_fft_plan(p, torch.ones(32, dtype=torch.complex64, device=gpu)[::2])
+    with pytest.raises(ValueError):
+        execute_fft_plan(p, torch.ones(16, dtype=torch.complex64))
+    with pytest.raises(TypeError):
+        execute_fft_plan(p, np.ones(16, np.complex64))
+    from kunlunxin_fft_amd.runner import fft_dit
+
+    with pytest.raises(ValueError):
+        fft_dit(torch.ones(12, dtype=torch.complex64, device=gpu))
+
+
+def test_native_rejects_overlap_and_misalignment(gpu):
+    np_ = native.NativePlan(64, 2, flow=native.FLOW_LDS_FUSED)
+    buf = torch.zeros(4 * 64, dtype=torch.complex64, device=gpu)
+    stream = torch.cuda.current_stream().cuda_stream
+    with pytest.raises(ValueError, match="overlap"):
+        np_.execute(buf.data_ptr(), buf.data_ptr() + 8 * 64, stream)
+    with pytest.raises(ValueError, match="aligned"):
+        np_.execute(buf.data_ptr() + 4, buf.data_ptr() + 8 * 200, stream)
+    assert np_.info.launches == 1 and np_.info.workspace_bytes == 0
+
+
+def test_runs_on_a_side_stream(gpu):
+    n, b = 4096, 8
+    x = torch.from_numpy(seeded_c64(n, b)).to(gpu)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        y = run("fft_lds_fused_batch", x, b, n)
+    s.synchronize()
+    check(y.cpu().numpy(), oracle.fft_dit(seeded_c64(n, b)), "side stream")
+
+
+def test_plan_info_reports_flows(gpu):
+    assert native.NativePlan(4096, 4).flow_name == "lds-fused"
+    fs = native.NativePlan(1 << 16, 4)
+    assert fs.flow_name == "four-step" and fs.info.launches == 2 and fs.info.workspace_bytes == 0
+    r2 = native.NativePlan(1024, 2, flow=native.FLOW_RADIX2_DIT)
+    assert r2.info.launches == 10 and r2.info.workspace_bytes == 2 * 1024 * 8

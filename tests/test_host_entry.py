@@ -1,0 +1,309 @@
+"""Host-only plan API contract (no GPU): restates the reference's
+tests/test_entry.py, test_selector.py and test_semantic_key.py contracts
+against this package's plan_fft / select / load_table."""
+import copy
+import json
+import os
+
+import pytest
+
+from kunlunxin_fft_amd import DeviceProfile, ExecutionPlan, load_table, norm_scale, plan_fft
+from kunlunxin_fft_amd.config import ConfigError
+from kunlunxin_fft_amd.entry import (
+    REAL_FLOW_MARK, _check_plan_input, _dispatch, _m0_plan,
+)
+from kunlunxin_fft_amd.selector import GUARD_PCT, Selection, find_entry, select
+
+PROF = DeviceProfile.load().hash()
+ENV = "e" * 16
+
+
+def _entry(n=2048, batch=1, direction="dit", real="lds-resident", unit="stockham-radix16",
+           executed=None, params=None, block=256, **extra):
+    e = {"N": n, "batch": batch, "direction": direction, "block": block,
+         "flow_id": "lds-stockham-single-pass", "flow_realization": real,
+         "processing_unit": unit, "params": params or {}, "incumbent_ms": 1.0,
+         "challenger_ms": 0.5, "reason": "measured"}
+    if executed:
+        e["executed"] = executed
+    e.update(extra)
+    return e
+
+
+def _table(entries=(), fallbacks=()):
+    return {"profile_hash": PROF, "env_hash": ENV, "precision": "fp32", "guard_pct": GUARD_PCT,
+            "env": {"device_model": "gfx950", "multiprocessor_count": 256, "max_shared_mem": 163840},
+            "entries": list(entries), "previous_fallbacks": list(fallbacks)}
+
+
+def _write(tmp_path, table):
+    p = tmp_path / "t.json"
+    p.write_text(json.dumps(table))
+    return str(p)
+
+
+@pytest.mark.parametrize("real,unit,direction,batch,expect", [
+    ("global-stage", "radix2-scalar", "dit", 1, "fft_dit"),
+    ("global-stage", "radix2-scalar", "dif", 1, "fft_dif"),
+    ("global-stage", "radix2-scalar", "dit", 4, "fft_dit_batch"),
+    ("global-stage", "radix4-scalar", "dit", 1, "fft_dit_radix4"),
+    ("global-stage", "radix4-scalar", "dif", 16, "fft_dif_radix4_batch"),
+    ("lds-resident", "stockham-radix16", "dit", 1, "fft_lds_fused"),
+    ("lds-resident", "stockham-radix16", "dif", 64, "fft_lds_fused_batch"),
+    ("four-step", "stockham-radix16", "dit", 1, "fft_four_step"),
+    ("four-step", "stockham-radix16", "dit", 256, "fft_four_step_batch"),
+    ("fused-inplace", "radix2-scalar", "dit", 1, "fft_dit_fused"),
+    ("matrix-resident", "dense-dot-fft64", "dif", 1, "fft_dif_matrix"),
+    ("matrix-resident", "dense-dot-fft64", "dit", 4, "fft_dit_matrix_batch"),
+    ("grouped-boundary", "composite-linear-map", "dit", 1, "fft_dit_grouped"),
+])
+def test_dispatch_covers_known_lowerings(real, unit, direction, batch, expect):
+    sel = Selection(n=2048, direction=direction, batch=batch, precision="fp32", source="table",
+                    reason="t", block=256, flow_id="x", flow_realization=real, processing_unit=unit)
+    assert _dispatch(sel) == expect
+
+
+@pytest.mark.parametrize("real,unit,direction,batch", [
+    ("fused-inplace", "radix2-scalar", "dif", 1),
+    ("fused-inplace", "radix2-scalar", "dit", 4),
+    ("grouped-boundary", "composite-linear-map", "dit", 16),
+])
+def test_dispatch_returns_none_for_unlowered(real, unit, direction, batch):
+    sel = Selection(n=16, direction=direction, batch=batch, precision="fp32", source="table",
+                    reason="t", block=256, flow_id="x", flow_realization=real, processing_unit=unit)
+    assert _dispatch(sel) is None
+
+
+def test_plan_rejects_invalid_direction():
+    for bad in ("inverse", "r2c"):
+        with pytest.raises(ValueError, match="unsupported direction"):
+            plan_fft(bad, 16, profile_hash=PROF, table=_table())
+
+
+def test_plan_rejects_invalid_precision():
+    with pytest.raises(ValueError, match="unsupported precision"):
+        plan_fft("dit", 16, precision="fp64", profile_hash=PROF, table=_table())
+
+
+@pytest.mark.parametrize("kwargs", [dict(transform_type="stft"), dict(transform_type="dct"),
+                                    dict(transform_direction="sideways"), dict(norm="l2")])
+def test_plan_rejects_unsupported_semantics(kwargs):
+    with pytest.raises(ValueError):
+        plan_fft("dit", 16, profile_hash=PROF, table=_table(), **kwargs)
+
+
+@pytest.mark.parametrize("kwargs", [dict(transform_type="r2c", transform_direction="inverse"),
+                                    dict(transform_type="c2r", transform_direction="forward")])
+def test_real_transforms_are_direction_locked(kwargs):
+    with pytest.raises(ValueError, match="forward transform|inverse transform"):
+        plan_fft("dit", 16, profile_hash=PROF, table=_table(), **kwargs)
+
+
+def test_plan_rejects_before_table_query():
+    class Boom:
+        def __getitem__(self, key):
+            raise AssertionError("table queried before validation")
+
+        def get(self, *a):
+            raise AssertionError("table queried before validation")
+
+    for bad in (dict(transform_type="stft"), dict(norm="madeup"), dict(transform_direction="x")):
+        with pytest.raises(ValueError):
+            plan_fft("dit", 16, table=Boom(), **bad)
+
+
+@pytest.mark.parametrize("n", [0, 3, 12, 1 << 21])
+def test_plan_rejects_bad_lengths(n):
+    with pytest.raises(ValueError):
+        plan_fft("dit", n, profile_hash=PROF, table=_table())
+
+
+def test_plan_executes_table_winner():
+    t = _table([_entry(2048, 1, "dit", executed="fft_lds_fused", params={"elems": 16})])
+    plan = plan_fft("dit", 2048, profile_hash=PROF, table=t, env_hash=ENV)
+    assert not plan.fallback and plan.selection_source == "table"
+    assert plan.executed == "fft_lds_fused" and plan.params["elems"] == 16
+
+
+def test_plan_falls_back_on_unknown_n():
+    plan = plan_fft("dit", 4096, profile_hash=PROF, table=_table([_entry(2048)]), env_hash=ENV)
+    assert plan.fallback and plan.executed == "fft_dit" and plan.selection_source == "abstain"
+    assert "no measured entry" in plan.reason
+
+
+def test_plan_falls_back_on_missing_profile():
+    plan = plan_fft("dit", 2048, profile_hash=None, table=_table([_entry()]), env_hash=ENV)
+    assert plan.fallback and plan.executed == "fft_dit"
+    assert "profile_hash is required" in plan.reason
+
+
+def test_plan_falls_back_on_profile_mismatch():
+    plan = plan_fft("dit", 2048, profile_hash="f" * 16, table=_table([_entry()]), env_hash=ENV)
+    assert plan.fallback and "profile hash" in plan.reason
+
+
+def test_plan_falls_back_on_env_mismatch_or_unknown():
+    t = _table([_entry()])
+    assert "environment hash" in plan_fft("dit", 2048, profile_hash=PROF, table=t, env_hash="0" * 16).reason
+    assert "unknown" in plan_fft("dit", 2048, profile_hash=PROF, table=t, env_hash=None).reason
+    unbound = dict(t, env_hash="")
+    assert "env_hash" in plan_fft("dit", 2048, profile_hash=PROF, table=unbound, env_hash=ENV).reason
+
+
+def test_plan_falls_back_for_dif_fused_entry():
+    t = _table([_entry(16, 1, "dif", real="fused-inplace", unit="radix2-scalar", params={})])
+    plan = plan_fft("dif", 16, profile_hash=PROF, table=t, env_hash=ENV)
+    assert plan.fallback and plan.executed == "fft_dif" and "no lowering" in plan.reason
+
+
+def test_plan_falls_back_for_batched_m1_entry():
+    t = _table([_entry(16, 4, "dit", real="fused-inplace", unit="radix2-scalar")])
+    plan = plan_fft("dit", 16, batch=4, profile_hash=PROF, table=t, env_hash=ENV)
+    assert plan.fallback and plan.executed == "fft_dit_batch" and "no lowering" in plan.reason
+    assert plan.params["variant"] == "folded"
+
+
+def test_semantic_tier_outranks_legacy_and_fallback_outranks_both():
+    legacy = _entry(1024, 1, "dit", executed="fft_lds_fused")
+    sem = _entry(1024, 1, "dit", executed="fft_four_step", real="four-step",
+                 transform_type="c2c", transform_direction="inverse", normalization="backward")
+    t = _table([legacy, sem])
+    inv = plan_fft("dit", 1024, profile_hash=PROF, table=t, env_hash=ENV, transform_direction="inverse")
+    fwd = plan_fft("dit", 1024, profile_hash=PROF, table=t, env_hash=ENV)
+    assert inv.executed == "fft_four_step" and fwd.executed == "fft_lds_fused"
+    fb = _entry(1024, 1, "dit", real="global-stage", unit="radix2-scalar", executed="fft_dit",
+                transform_type="c2c", transform_direction="inverse", normalization="backward",
+                previous_fallback_provenance={})
+    t2 = _table([legacy, sem], [fb])
+    e = find_entry(t2, 1024, 1, "dit", "c2c", "inverse", "backward")
+    assert e is fb
+    plan = plan_fft("dit", 1024, profile_hash=PROF, table=t2, env_hash=ENV, transform_direction="inverse")
+    assert plan.executed == "fft_dit" and plan.params.get("previous_fallback") is True
+
+
+def test_real_plans_are_dedicated_and_marked():
+    t = _table([_entry(1024, 1, "dit", executed="fft_lds_fused")])
+    r2c = plan_fft("dit", 1024, profile_hash=PROF, table=t, env_hash=ENV, transform_type="r2c")
+    c2r = plan_fft("dif", 1024, profile_hash=None, table=t, transform_type="c2r", norm="ortho")
+    assert r2c.transform_direction == "forward" and c2r.transform_direction == "inverse"
+    assert r2c.params["real_compat"] == REAL_FLOW_MARK == c2r.params["real_compat"]
+    assert r2c.executed == "fft_lds_fused" and c2r.fallback
+
+
+def test_inverse_reuses_forward_lowering_on_legacy_entry():
+    t = _table([_entry(1024, 16, "dif", executed="fft_lds_fused_batch")])
+    inv = plan_fft("dif", 1024, batch=16, profile_hash=PROF, table=t, env_hash=ENV,
+                   transform_direction="inverse", norm="ortho")
+    fwd = plan_fft("dif", 1024, batch=16, profile_hash=PROF, table=t, env_hash=ENV)
+    assert inv.executed == fwd.executed and inv.params == fwd.params and inv.norm == "ortho"
+
+
+def test_norm_scale_matches_torch_fft_semantics():
+    n = 16
+    assert norm_scale(n, "forward", "none") == 1.0
+    assert norm_scale(n, "forward", "forward") == 1.0 / n
+    assert norm_scale(n, "forward", "backward") == 1.0
+    assert norm_scale(n, "inverse", "none") == 1.0
+    assert norm_scale(n, "inverse", "forward") == 1.0
+    assert norm_scale(n, "inverse", "backward") == 1.0 / n
+    for d in ("forward", "inverse"):
+        assert norm_scale(n, d, "ortho") == 1.0 / n ** 0.5
+    with pytest.raises(ValueError):
+        norm_scale(n, "sideways", "none")
+
+
+def _plan(n=16, batch=1, tt="c2c"):
+    return ExecutionPlan(n=n, batch=batch, direction="dit", precision="fp32",
+                         selection_source="table", reason="t", fallback=False, executed="fft_dit",
+                         block=256, transform_type=tt)
+
+
+def test_plan_input_contracts():
+    _check_plan_input(_plan(16, 1), (16,), "complex64")
+    _check_plan_input(_plan(4096, 16), (16, 4096), "complex64")
+    with pytest.raises(ValueError, match="N=16"):
+        _check_plan_input(_plan(16, 1), (32,), "complex64")
+    with pytest.raises(ValueError, match="rank-1"):
+        _check_plan_input(_plan(16, 1), (1, 16), "complex64")
+    with pytest.raises(ValueError, match=r"\(4, 4096\)"):
+        _check_plan_input(_plan(4096, 4), (16, 4096), "complex64")
+    with pytest.raises(TypeError, match="complex64"):
+        _check_plan_input(_plan(16, 1), (16,), "float32")
+    _check_plan_input(_plan(64, 1, "r2c"), (64,), "float32")
+    with pytest.raises(TypeError):
+        _check_plan_input(_plan(64, 1, "r2c"), (64,), "complex64")
+    _check_plan_input(_plan(64, 1, "c2r"), (33,), "complex64")
+    with pytest.raises(ValueError):
+        _check_plan_input(_plan(64, 1, "c2r"), (64,), "complex64")
+
+
+def test_m0_plan_is_reference_shaped():
+    p = _m0_plan(64, 4, "dif", "fp32", "why", True)
+    assert p.executed == "fft_dif_batch" and p.fallback and p.selection_source == "abstain"
+    assert p.flow_realization == "global-stage" and p.processing_unit == "radix2-scalar"
+
+
+def test_load_table_refuses_contract_violations(tmp_path):
+    bad = [
+        _entry(2048, 1, "dit", real="lds-resident", params={"elems": 32}),
+        _entry(2048, 1, "dit", real="nope", unit="nope"),
+        _entry(2048, 1, "dit", executed="fft_dit"),          # runner outside its family
+        _entry(2048, 4, "dit", executed="fft_lds_fused"),    # single runner at batch 4
+        _entry(2048, 1, "dit", real="four-step", params={"n1": 3}),
+        _entry(2048, 1, "dit", real="global-stage", unit="radix2-scalar", block=32),
+        _entry(3000, 1, "dit"),
+    ]
+    for e in bad:
+        with pytest.raises(ConfigError):
+            load_table(_write(tmp_path, _table([e])))
+    ok = load_table(_write(tmp_path, _table([_entry(executed="fft_lds_fused", params={"elems": 8})])))
+    assert len(ok["entries"]) == 1
+
+
+def test_load_table_refuses_unbound_fallbacks(tmp_path):
+    fb = _entry(1024, 1, "dit", executed="fft_lds_fused", transform_type="c2c",
+                transform_direction="forward", normalization="backward")
+    with pytest.raises(ConfigError, match="provenance"):
+        load_table(_write(tmp_path, _table([], [fb])))
+
+
+def test_shipped_table_loads_and_binds_this_profile():
+    t = load_table()
+    assert t["profile_hash"] == PROF
+    assert t["precision"] == "fp32"
+
+
+def test_select_abstains_without_profile():
+    s = select("dit", 2048, table=_table([_entry()]), env_hash=ENV)
+    assert not s.selected and "profile_hash is required" in s.reason
+
+
+def test_composition_fails_closed():
+    from kunlunxin_fft_amd.composition import composition_select, load_composition_table
+
+    assert load_composition_table() is None
+    assert composition_select("dit", 2048, batch=16, profile_hash=PROF, env_hash=ENV) is None
+
+
+def test_entry_module_does_not_import_torch():
+    import kunlunxin_fft_amd.entry as entry_mod
+
+    src = open(entry_mod.__file__).read()
+    lines = [ln for ln in src.splitlines() if "import torch" in ln and not ln.strip().startswith("#")]
+    assert all(ln.startswith("    ") for ln in lines), lines
+
+
+def test_device_profile_hash_is_stable():
+    p = DeviceProfile.load()
+    assert p.hash() == DeviceProfile.load().hash() and len(p.hash()) == 16
+    assert p.gfx_arch == "gfx950" and p.compute_units == 256
+
+
+def test_env_fingerprint_unknown_without_gpu():
+    import torch
+
+    from kunlunxin_fft_amd import envcheck
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    assert envcheck.current_env_hash() is None

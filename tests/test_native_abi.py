@@ -1,0 +1,64 @@
+"""The C ABI library loads and exports every symbol include/mfft.h declares
+(CPU only: no compute calls).  Also checks that the ctypes structs match the
+header's layout, and that invalid arguments are rejected before any device
+work (these checks run on the host side of mfft_plan_create)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from kunlunxin_fft_amd import native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mfft.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*|void)\s+\**(mfft_\w+)\s*\(", src, re.M)))
+
+
+def test_header_declares_what_the_binding_expects():
+    assert _declared() == sorted(native.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    if not os.path.exists(native.LIB_PATH):
+        pytest.fail("libmfft.so not built: run __graft_entry__.build()")
+    lib = native.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.mfft_abi_version() == 1
+
+
+def test_struct_layouts():
+    # int64 x3, int32 x8, int64 x5, double
+    assert ctypes.sizeof(native.PlanInfo) == 3 * 8 + 8 * 4 + 5 * 8 + 8
+    assert ctypes.sizeof(native.DeviceProps) == 256 + 256 + 4 * 2 + 8 * 3 + 4 * 8
+
+
+@pytest.mark.parametrize("kwargs,match", [
+    (dict(n=12, batch=1), "power of two"),
+    (dict(n=16, batch=0), "batch"),
+    (dict(n=1 << 21, batch=1), "maximum"),
+    (dict(n=16, batch=1, transform_type="r2c", transform_direction="inverse"), "forward"),
+    (dict(n=16, batch=1, transform_type="c2r", transform_direction="forward"), "inverse"),
+    (dict(n=16, batch=1, flow=native.FLOW_FOUR_STEP), "FOUR_STEP"),
+    (dict(n=1 << 14, batch=1, flow=native.FLOW_LDS_FUSED), "LDS_FUSED"),
+    (dict(n=2, batch=1, flow=native.FLOW_RADIX4_DIT), "core length"),
+    (dict(n=64, batch=1, flow=native.FLOW_RADIX2_DIT, params=(32,)), "threads per block"),
+    (dict(n=64, batch=1, flow=99), "unknown flow"),
+])
+def test_plan_create_rejects_before_device_work(kwargs, match):
+    if not os.path.exists(native.LIB_PATH):
+        pytest.fail("libmfft.so not built")
+    with pytest.raises(ValueError, match=match):
+        native.NativePlan(**kwargs)
+
+
+def test_execute_rejects_null_plan():
+    lib = native.load()
+    assert lib.mfft_execute(None, None, None, None) == native.ERR_VALUE
+    assert b"plan" in lib.mfft_last_error()
+    assert lib.mfft_plan_destroy(None) == 0
