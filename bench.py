@@ -114,7 +114,7 @@ def main() -> int:
 
     # ---- per size: event time of one execute, and per-launch durations
     per_size = []
-    kernels = {}  # (flow, n, launch index) -> [ms]
+    kernels = {}  # (kernel, flow, n, rows per launch) -> [launch ms, ...] within one execute
     stream = torch.cuda.current_stream(dev)
     for n, b, x, plan in work:
         nplan, (shape, dt) = _resolve(plan, 0)
@@ -129,32 +129,38 @@ def main() -> int:
             evs.append((s, e))
         torch.cuda.synchronize()
         ms = statistics.median(s.elapsed_time(e) for s, e in evs)
-        launches = []
-        for _ in range(5):
-            launches.append(nplan.execute_timed(x.data_ptr(), out.data_ptr(), stream.cuda_stream))
+        launches = [nplan.execute_timed(x.data_ptr(), out.data_ptr(), stream.cuda_stream) for _ in range(5)]
         per_launch = [statistics.median(col) for col in zip(*launches)]
+        flow = nplan.flow_name
+        rows = int(nplan.info.chunk_rows) or b
         for i, t in enumerate(per_launch):
-            kernels[(nplan.flow_name, n, b, i, len(per_launch))] = t
+            if flow == "four-step":
+                kname = f"fourstep_pass_kernel pass {i % 2 + 1} (n{'12'[i % 2]}={nplan.info.n1 if i % 2 == 0 else nplan.info.n2})"
+            elif flow == "lds-fused":
+                kname = "lds_fft_kernel"
+            else:
+                kname = f"{flow} stage {i + 1}"
+            kernels.setdefault((kname, flow, n, b, rows), []).append(t)
         gbps = 16 * n * b / (ms * 1e-3) / 1e9
         per_size.append({
-            "n": n, "batch": b, "executed": plan.executed, "flow": nplan.flow_name,
+            "n": n, "batch": b, "executed": plan.executed, "flow": flow,
             "fallback": plan.fallback, "launches": len(per_launch),
             "ms": round(ms, 5), "gbps": round(gbps, 1), "frac_hbm": round(gbps / PEAK_GBPS, 4),
             "gflops": round(5 * n * math.log2(n) * b / (ms * 1e-3) / 1e9, 1),
             "launch_ms": [round(t, 5) for t in per_launch],
-            "split": [int(nplan.info.n1), int(nplan.info.n2)] if nplan.info.n1 else None,
+            "split": [int(nplan.info.n1), int(nplan.info.n2), rows] if nplan.info.n1 else None,
         })
-        log(f"N={n:>8} B={b:>6} {nplan.flow_name:>10} {ms:8.4f} ms {gbps:8.1f} GB/s "
+        log(f"N={n:>8} B={b:>6} {flow:>10} {ms:8.4f} ms {gbps:8.1f} GB/s "
             f"({gbps / PEAK_GBPS:.1%}) launches={['%.4f' % t for t in per_launch]}")
 
-    # ---- dominant kernel: the launch with the largest share of a step
-    (dflow, dn, db, di, dk), dms = max(kernels.items(), key=lambda kv: kv[1])
-    d_bytes = 16 * dn * db  # every pass of every flow reads and writes all B*N elements once
+    # ---- dominant kernel: the (kernel, size) with the largest total time per step
+    (kname, dflow, dn, db, drows), dts = max(kernels.items(), key=lambda kv: sum(kv[1]))
+    dms = sum(dts) / len(dts)
+    d_bytes = 16 * dn * drows  # each launch reads and writes every element of its rows once
     d_ach = d_bytes / (dms * 1e-3) / 1e9
-    kname = {"lds-fused": "lds_fft_kernel", "four-step": "fourstep_pass_kernel"}.get(dflow, dflow)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "pmc_traffic.json")
-    key = f"{dflow}:N={dn}:B={db}:launch={di}"
+    key = f"{kname}|N={dn}|rows={drows}"
     if os.path.exists(tpath):
         try:
             traffic = json.load(open(tpath)).get(key)
@@ -162,8 +168,11 @@ def main() -> int:
             traffic = None
     roofline = {"bound": "hbm", "achieved": round(d_ach, 1), "peak": PEAK_GBPS, "unit": "GB/s",
                 "frac": round(d_ach / PEAK_GBPS, 4), "traffic": traffic,
-                "kernel": f"{kname} ({dflow}, N={dn}, B={db}, launch {di + 1}/{dk})",
-                "algorithmic_bytes_per_launch": d_bytes, "mean_launch_ms": round(dms, 5)}
+                "kernel": f"{kname} [{dflow}, N={dn}, B={db}, {drows} rows per launch, "
+                          f"{len(dts)} launches per execute]",
+                "algorithmic_bytes_per_launch": d_bytes, "mean_launch_ms": round(dms, 5),
+                "share_of_step": round(sum(dts) / ms_per_step, 3)}
+    log(f"dominant kernel: {roofline}")
 
     # ---- latency at N=2048 B=1 (reference protocol) and config 2
     def latency(n, b):
