@@ -58,6 +58,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-latency", action="store_true", help="skip the latency / config-2 legs")
+    ap.add_argument("--sizes", default="", help="comma-separated subset of N (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every box here has one MI355X; "
@@ -84,9 +86,30 @@ def main() -> int:
     gen = torch.Generator(device=dev)
     gen.manual_seed(102026)
 
+    sizes = [int(v) for v in args.sizes.split(",") if v] if args.sizes else SIZES
+
+    # ---- device-to-device copy of 256 MiB: the measured bandwidth ceiling
+    src = torch.empty(1 << 25, dtype=torch.complex64, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    evs = []
+    for _ in range(10):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        dst.copy_(src)
+        e.record()
+        evs.append((s, e))
+    torch.cuda.synchronize()
+    copy_ms = statistics.median(s.elapsed_time(e) for s, e in evs)
+    copy_gbps = 2 * src.numel() * 8 / (copy_ms * 1e-3) / 1e9
+    log(f"d2d copy 256 MiB: {copy_ms:.4f} ms, {copy_gbps:.1f} GB/s (read + write)")
+    del src, dst
+
     # ---- inputs resident in HBM, plans resolved once (plan reuse)
     work = []
-    for n in SIZES:
+    for n in sizes:
         b = batch_for(n)
         x = torch.randn((b, n), dtype=torch.complex64, device=dev, generator=gen) * math.sqrt(2.0)
         plan = pkg.plan_fft("dit", n, batch=b, profile_hash=prof)
@@ -207,11 +230,13 @@ def main() -> int:
                 "kernel_event_p50_ms": round(ev, 5),
                 "api_gbps": round(16 * n * b / (p50 * 1e-3) / 1e9, 3)}
 
-    lat = latency(2048, 1)
-    log(f"latency N=2048 B=1: {lat}")
-    cfg2 = [latency(n, b) for n in (1024, 2048) for b in (16, 64)]
-    for c in cfg2:
-        log(f"config2: {c}")
+    lat, cfg2 = None, []
+    if not args.no_latency:
+        lat = latency(2048, 1)
+        log(f"latency N=2048 B=1: {lat}")
+        cfg2 = [latency(n, b) for n in (1024, 2048) for b in (16, 64)]
+        for c in cfg2:
+            log(f"config2: {c}")
 
     # ---- CPU baseline (reference CPU path, 1 core, bounded sample)
     cpu = None
@@ -222,7 +247,7 @@ def main() -> int:
         rng = np.random.default_rng(7)
         tot_s, tot_bytes, kinds = 0.0, 0, set()
         for n in SIZES:
-            h = rng.standard_normal(n) + 1j * rng.standard_normal(n)
+            h = rng.standard_normal(n) + 1j * rng.standard_normal(n)  # one row of each size
             s, kind = oracle.time_cpu_fft(h, threads=1, reps=3)
             kinds.add(kind)
             tot_s += s
@@ -244,7 +269,9 @@ def main() -> int:
         "config": {"workload": "forward C2C complex64 via plan_fft/execute_fft_plan, "
                                "N=2^10..2^20, B=max(64, 2^25/N) per N (256 MiB in + 256 MiB out "
                                "per N); one step = all 11 sizes",
-                   "frac_hbm_of_value": round(value / PEAK_GBPS, 4)},
+                   "frac_hbm_of_value": round(value / PEAK_GBPS, 4),
+                   "d2d_copy_gbps": round(copy_gbps, 1),
+                   "frac_of_d2d_copy": round(value / copy_gbps, 4)},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "latency_n2048_b1": lat,

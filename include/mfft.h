@@ -76,7 +76,7 @@ enum {
     MFFT_FLOW_RADIX2_DIF = 2,  /* M0 fft_dif: bit reversal folded into the last stage (runner.py:165-206) */
     MFFT_FLOW_RADIX4_DIT = 3,  /* M5 fft_dit_radix4: digit reversal folded into stage 0 (runner.py:1399-1470) */
     MFFT_FLOW_RADIX4_DIF = 4,  /* M5 fft_dif_radix4 (runner.py:1473-1540) */
-    MFFT_FLOW_LDS_FUSED = 5,   /* one pass: whole transform resident in LDS/registers (core n <= 8192) */
+    MFFT_FLOW_LDS_FUSED = 5,   /* one pass: whole transform resident in LDS/registers (core n <= 16384) */
     MFFT_FLOW_FOUR_STEP = 6    /* two passes: column FFTs + twiddle, then row FFTs (core n >= 256) */
 };
 

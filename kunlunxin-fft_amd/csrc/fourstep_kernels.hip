@@ -17,27 +17,59 @@
 // keeps them in LDS, and runs the same Stockham passes as the single-pass
 // kernel on each column.  Inverse = conjugated roots; the norm scale is applied
 // by pass 2's store.  The big twiddle W_N^e (e < N) is the product of two
-// small tables, W_N^(e mod 2^h) * W_N^(2^h * (e >> h)).
+// small tables, W_N^(e mod 2^h) * W_N^(2^h * (e >> h)); pass 1 applies it in
+// registers after its last Stockham pass, as W_N^(n2*b) * (W_N^(n2*NS))^q,
+// so each thread does a few table lookups instead of two per element.
+// Stockham twiddles come from per-pass tables (rows W^k, W^2k, W^4k, W^8k).
 #include "mfft_device.hpp"
 #include "mfft_internal.hpp"
 
 namespace mfft {
+
+// column-group width and elements per thread for a pass of length 2^logl
+constexpr int col_loge(int logl) { return logl >= 8 ? 4 : (logl >= 6 ? 3 : 2); }
+constexpr int col_logc(int logl) { return logl >= 9 ? 3 : 4; }
+int fourstep_col_loge(int logl) { return col_loge(logl); }
+
 namespace {
 
 __device__ __forceinline__ int pad(int i) { return i + (i >> 4); }
 
+// Workgroups are dispatched to the 8 XCDs round-robin (block p -> XCD p % 8),
+// and each XCD has its own L2.  With 8 columns per block a 128-byte row
+// segment is shared by logical blocks 2k and 2k+1; this map puts both on the
+// same XCD (physical blocks 16q + x and 16q + 8 + x), dispatched together, so
+// the line is fetched once into that XCD's L2.  A bijection on every full
+// group of 16 blocks; the tail keeps its order.
+__device__ __forceinline__ int xcd_pair_block(int p, int total) {
+    if (p >= (total & ~15)) return p;
+    const int r = p & 15;
+    return (p & ~15) + ((r & 7) << 1) + (r >> 3);
+}
+
 template <int LOGL, int LOGE, int LOGC>
 struct ColCfg {
+    static_assert(LOGE < LOGL, "a column pass needs more than one thread per column");
     static constexpr int L = 1 << LOGL;
     static constexpr int E = 1 << LOGE;
     static constexpr int C = 1 << LOGC;
     static constexpr int T = L / E;  // threads per column
     static constexpr int WG = C * T;
-    static constexpr int P = (LOGL + LOGE - 1) / LOGE;
-    static constexpr int PITCH = L + (L >> 4) + 1;
-    static constexpr int logr(int p) { return p < P - 1 ? LOGE : LOGL - LOGE * (P - 1); }
-    static constexpr int lns(int p) { return LOGE * p; }
+    static constexpr int P = sched_passes(LOGL, LOGE);
+    // Column pitch in float2 units, == 32/C (mod 32): a half-wave (32 lanes)
+    // covers C columns x 32/C rows, and with this pitch the C columns start
+    // 64/C dwords apart, tiling the 64 LDS banks without conflicts.
+    static constexpr int PITCH0 = L + (L >> 4);
+    static constexpr int PITCH = PITCH0 + ((32 / C - PITCH0 % 32) + 32) % 32;
+    static constexpr int logr(int p) { return sched_logr(LOGL, LOGE, p); }
+    static constexpr int lns(int p) { return sched_lns(LOGE, p); }
 };
+
+// W_N^e for e < N as the product of the two small tables
+__device__ __forceinline__ float2 big_root(const float2* __restrict__ lo, const float2* __restrict__ hi,
+                                          int h, uint32_t e) {
+    return cmul(lo[e & ((1u << h) - 1)], hi[e >> h]);
+}
 
 // KIND 0: pass 1 (column FFT of length L = N1 over S = N2 columns, twiddle,
 //         transposed store).  KIND 1: pass 2 (in place, L = N2, S = N1 columns).
@@ -54,8 +86,9 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_pass_
     const int c = tid & (NC - 1);
     const int j = tid >> LOGC;
     const int groups = (1 << log_s) >> LOGC;  // column groups per transform
-    const int64_t row = blockIdx.x / groups;
-    const int c0 = (blockIdx.x - (int)(row * groups)) << LOGC;
+    const int bid = xcd_pair_block((int)blockIdx.x, (int)gridDim.x);
+    const int64_t row = bid / groups;
+    const int c0 = (bid - (int)(row * groups)) << LOGC;
     const int64_t base = row << logn;
     const float2* s = src + base + c0 + c;
     float2* lt = lds + c * C::PITCH;
@@ -91,16 +124,30 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_pass_
             });
         }
         static_for<0, NB>([&](auto m) {
+            const int b = j + m.value * T;
             if constexpr (NS > 1) {
-                const int b = j + m.value * T;
-                const int k = b & (NS - 1);
-                constexpr int LST = LOGL - LNS - LR;
-                static_for<1, R>([&](auto q) {
-                    const float2 w = tw[(q.value * k) << LST];
-                    v[m.value * R + q.value] = cmul_tw<DIR>(v[m.value * R + q.value], w);
-                });
+                constexpr int TW_OFF = sched_tw_off(LOGL, LOGE, p);
+                pass_twiddle<R, DIR, m.value * R>(v, tw + TW_OFF, NS, b & (NS - 1));
             }
             dft<R, DIR, m.value * R, 1>(v);
+            if constexpr (KIND == 0 && p == P - 1) {
+                // four-step twiddle W_N^(n2*k1) on the pass-1 outputs, in
+                // registers: k1 = b + q*NS, so W = W_N^(n2*b) * (W_N^(n2*NS))^q
+                const uint32_t n2 = (uint32_t)(c0 + c);
+                const float2 w0 = big_root(tw_lo, tw_hi, tw_h, n2 * (uint32_t)b);
+                float2 sp[R];
+                static_for<0, LR>([&](auto i) {
+                    sp[1 << i.value] = big_root(tw_lo, tw_hi, tw_h, n2 * (uint32_t)(NS << i.value));
+                });
+                static_for<3, R>([&](auto q) {
+                    constexpr int hb = high_bit(q.value);
+                    if constexpr (hb != q.value) sp[q.value] = cmul(sp[q.value - hb], sp[hb]);
+                });
+                v[m.value * R] = cmul_tw<DIR>(v[m.value * R], w0);
+                static_for<1, R>([&](auto q) {
+                    v[m.value * R + q.value] = cmul_tw<DIR>(v[m.value * R + q.value], cmul(w0, sp[q.value]));
+                });
+            }
         });
         if constexpr (p < P - 1 || KIND == 0) {
             if constexpr (p > 0) __syncthreads();
@@ -114,17 +161,13 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_pass_
     });
 
     if constexpr (KIND == 0) {
-        // transposed, twiddled store: lanes run along k1 inside one column
-        const int hmask = (1 << tw_h) - 1;
+        // transposed store (the twiddle was applied in registers): lanes run
+        // along k1 inside one column, one contiguous run of L per column
         static_for<0, E>([&](auto r) {
             const int e = tid + r.value * C::WG;
             const int cc = e >> LOGL;
             const int k1 = e & (L - 1);
-            const int n2 = c0 + cc;
-            const uint32_t ex = (uint32_t)n2 * (uint32_t)k1;  // < N
-            const float2 w = cmul(tw_lo[ex & hmask], tw_hi[ex >> tw_h]);
-            const float2 val = cmul_tw<DIR>(lds[cc * C::PITCH + pad(k1)], w);
-            dst[base + ((int64_t)n2 << LOGL) + k1] = val;
+            dst[base + ((int64_t)(c0 + cc) << LOGL) + k1] = lds[cc * C::PITCH + pad(k1)];
         });
     } else {
         constexpr int LR = C::logr(P - 1);
@@ -141,9 +184,6 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_pass_
     }
 }
 
-// column-group width and elements per thread for a pass of length 2^logl
-constexpr int col_loge(int logl) { return logl >= 8 ? 4 : (logl >= 6 ? 3 : 2); }
-constexpr int col_logc(int logl) { return logl >= 9 ? 3 : 4; }
 
 template <int LOGL, int DIR, int KIND>
 hipError_t launch_pass(const float2* src, float2* dst, const mfft_plan* p, int64_t rows,

@@ -1,4 +1,4 @@
-// lds_kernels.hip -- single-pass LDS-resident FFT for core lengths 1..8192.
+// lds_kernels.hip -- single-pass LDS-resident FFT for core lengths 1..16384.
 //
 // One HBM read and one HBM write per element: every transform stays inside
 // one workgroup from its first load to its last store.  This is the MI355X
@@ -13,7 +13,10 @@
 // b in [0, L/R): inputs b + q*L/R, twiddles W_{NS*R}^(q*(b % NS)), an
 // in-register radix-R DFT, outputs (b/NS)*NS*R + b%NS + q*NS.  Each thread
 // owns E = L/T elements (T threads per transform), i.e. E/R butterflies per
-// pass.  Pass 0 reads HBM directly and the last pass writes HBM directly --
+// pass.  Twiddles come from a per-pass table holding, for each span NS, the
+// rows W^(k), W^(2k), W^(4k), W^(8k) (k < NS) -- a few coalesced loads per
+// butterfly; the other powers are composed with one complex product each.
+// Pass 0 reads HBM directly and the last pass writes HBM directly --
 // both are unit-stride across lanes -- and the passes in between exchange
 // through LDS.  LDS addresses carry one pad slot per 16 elements and an odd
 // per-transform pitch, which spreads the stride-R Stockham writes over banks.
@@ -35,16 +38,16 @@ namespace {
 template <int LOGL, int LOGE>
 struct LdsCfg {
     static constexpr int L = 1 << LOGL;
-    static constexpr int LE = LOGE < LOGL ? LOGE : LOGL;  // log2 elements per thread
+    static constexpr int LE = sched_le(LOGL, LOGE);  // log2 elements per thread
     static constexpr int E = 1 << LE;
     static constexpr int T = L / E;                        // threads per transform
     static constexpr int WG = T >= 256 ? T : 256;          // threads per block
     static constexpr int TPB = WG / T;                     // transforms per block
-    static constexpr int P = (LOGL == 0) ? 1 : (LOGL + LE - 1) / LE;  // passes
+    static constexpr int P = sched_passes(LOGL, LE);       // passes
     static constexpr int PITCH = L + (L >> 4) + 1;
     static constexpr int LDS_ELEMS = TPB * PITCH;
-    static constexpr int logr(int p) { return p < P - 1 ? LE : LOGL - LE * (P - 1); }
-    static constexpr int lns(int p) { return LE * p; }
+    static constexpr int logr(int p) { return sched_logr(LOGL, LE, p); }
+    static constexpr int lns(int p) { return sched_lns(LE, p); }
 };
 
 __device__ __forceinline__ int pad(int i) { return i + (i >> 4); }
@@ -123,12 +126,8 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG)) void lds_fft_kernel(
         static_for<0, NB>([&](auto m) {
             if constexpr (NS > 1) {
                 const int b = j + m.value * T;
-                const int k = b & (NS - 1);
-                constexpr int LST = LOGL - LNS - LR;  // log2(L / (NS*R))
-                static_for<1, R>([&](auto q) {
-                    const float2 w = tw[(q.value * k) << LST];
-                    v[m.value * R + q.value] = cmul_tw<DIR>(v[m.value * R + q.value], w);
-                });
+                constexpr int TW_OFF = sched_tw_off(LOGL, C::LE, p);
+                pass_twiddle<R, DIR, m.value * R>(v, tw + TW_OFF, NS, b & (NS - 1));
             }
             dft<R, DIR, m.value * R, 1>(v);
         });
@@ -214,8 +213,9 @@ hipError_t dispatch_elems(int loge, int mode, int dir, const void* src, void* ds
 bool lds_supported(int log2l, int elems) {
     if (log2l < 0 || log2l > kMaxLdsLog2) return false;
     if (elems != 0 && elems != 4 && elems != 8 && elems != 16) return false;
-    // a 8192-point transform needs 16 elements per thread (512 threads, 69 KiB LDS)
-    if (log2l == 13 && elems != 0 && elems != 16) return false;
+    // 8192 and 16384 points need 16 elements per thread (512 / 1024 threads,
+    // 69 / 139 KiB of LDS: one transform per workgroup)
+    if (log2l >= 13 && elems != 0 && elems != 16) return false;
     return true;
 }
 
@@ -251,6 +251,7 @@ hipError_t launch_lds(int mode, int dir, int log2l, int elems, const void* src, 
         case 11: return dispatch_elems<11>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
         case 12: return dispatch_elems<12>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
         case 13: return dispatch_mode<13, 4>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 14: return dispatch_mode<14, 4>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
         default: return hipErrorInvalidValue;
     }
 }

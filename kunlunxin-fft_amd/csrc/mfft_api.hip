@@ -56,21 +56,42 @@ double norm_scale(int64_t n, int dir, int norm) {
     return 1.0;
 }
 
-// forward roots exp(-2*pi*i*m/len) for m in [0, count), rounded from double
+// forward root exp(-2*pi*i*e/len), computed in long double and rounded once;
+// exact values on the axes keep symmetric roots symmetric
+float2 root(int64_t len, int64_t e) {
+    e %= len;
+    if (e == 0) return make_float2(1.0f, 0.0f);
+    if (4 * e == len) return make_float2(0.0f, -1.0f);
+    if (2 * e == len) return make_float2(-1.0f, 0.0f);
+    if (4 * e == 3 * len) return make_float2(0.0f, 1.0f);
+    const long double two_pi = 6.283185307179586476925286766559005768L;
+    const long double a = -two_pi * (long double)e / (long double)len;
+    return make_float2((float)cosl(a), (float)sinl(a));
+}
+
+// roots W_len^(m*step) for m in [0, count)
 std::vector<float2> roots(int64_t len, int64_t count, int64_t step) {
     std::vector<float2> w((size_t)count);
-    const long double two_pi = 6.283185307179586476925286766559005768L;
-    for (int64_t m = 0; m < count; ++m) {
-        const int64_t e = (m * step) % len;
-        // exact values on the axes keep symmetric roots symmetric
-        if (e == 0) { w[m] = make_float2(1.0f, 0.0f); continue; }
-        if (4 * e == len) { w[m] = make_float2(0.0f, -1.0f); continue; }
-        if (2 * e == len) { w[m] = make_float2(-1.0f, 0.0f); continue; }
-        if (4 * e == 3 * len) { w[m] = make_float2(0.0f, 1.0f); continue; }
-        const long double a = -two_pi * (long double)e / (long double)len;
-        w[m] = make_float2((float)cosl(a), (float)sinl(a));
-    }
+    for (int64_t m = 0; m < count; ++m) w[m] = root(len, m * step);
     return w;
+}
+
+// Stockham pass table of a length-2^logl transform at 2^le elements per
+// thread: pass p >= 1 (span NS, radix R) holds rows i < log2 R of
+// W_{NS*R}^(2^i * k), k < NS, at offset sched_tw_off (mfft_device.hpp).
+std::vector<float2> pass_table(int logl, int le) {
+    const int passes = mfft::sched_passes(logl, le);
+    const int size = mfft::sched_tw_size(logl, le);
+    std::vector<float2> t((size_t)(size > 0 ? size : 1), make_float2(0.0f, 0.0f));
+    for (int p = 1; p < passes; ++p) {
+        const int lr = mfft::sched_logr(logl, le, p);
+        const int64_t ns = (int64_t)1 << mfft::sched_lns(le, p);
+        const int64_t span = ns << lr;
+        const int off = mfft::sched_tw_off(logl, le, p);
+        for (int i = 0; i < lr; ++i)
+            for (int64_t k = 0; k < ns; ++k) t[(size_t)(off + i * ns + k)] = root(span, k << i);
+    }
+    return t;
 }
 
 int upload(float2** dptr, const std::vector<float2>& h, int64_t* bytes) {
@@ -197,7 +218,7 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
                             "(got core length %lld, elements %d)",
                             mfft::kMaxLdsLog2, (long long)core_n, prm[0]);
             elems = prm[0] ? prm[0] : mfft::lds_default_elems(logc);
-            if (logc == 13) elems = 16;
+            if (logc >= 13) elems = 16;
             block = mfft::lds_threads_per_block(logc, elems);
             break;
         case MFFT_FLOW_FOUR_STEP: {
@@ -251,12 +272,15 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
     // ---- twiddle tables
     if (flow == MFFT_FLOW_FOUR_STEP) {
         const int lc = logc;
+        const int l1 = mfft::ilog2((int)n1), l2 = mfft::ilog2((int)n2);
         p->tw_h = (lc + 1) / 2;
-        if (rc == MFFT_OK) rc = upload(&p->tw_n1, roots(n1, n1, 1), &p->table_bytes);
-        if (rc == MFFT_OK) rc = upload(&p->tw_n2, roots(n2, n2, 1), &p->table_bytes);
+        if (rc == MFFT_OK) rc = upload(&p->tw_n1, pass_table(l1, mfft::fourstep_col_loge(l1)), &p->table_bytes);
+        if (rc == MFFT_OK) rc = upload(&p->tw_n2, pass_table(l2, mfft::fourstep_col_loge(l2)), &p->table_bytes);
         if (rc == MFFT_OK) rc = upload(&p->tw_lo, roots(core_n, (int64_t)1 << p->tw_h, 1), &p->table_bytes);
         if (rc == MFFT_OK)
             rc = upload(&p->tw_hi, roots(core_n, core_n >> p->tw_h, (int64_t)1 << p->tw_h), &p->table_bytes);
+    } else if (flow == MFFT_FLOW_LDS_FUSED) {
+        rc = upload(&p->tw, pass_table(logc, mfft::sched_le(logc, mfft::ilog2(elems))), &p->table_bytes);
     } else {
         rc = upload(&p->tw, roots(core_n, core_n, 1), &p->table_bytes);
     }

@@ -139,6 +139,44 @@ __device__ __forceinline__ void dft(float2 (&v)[E]) {
     }
 }
 
+// ---- Stockham schedule shared by the host (table builder) and the kernels --
+// A transform of length 2^logl with up to 2^loge elements per thread runs P
+// passes; pass p has radix 2^logr(p) and accumulated span NS = 2^(le*p).
+// Every pass but the last has radix 2^le (the remainder goes last).
+constexpr int sched_le(int logl, int loge) { return loge < logl ? loge : logl; }
+constexpr int sched_passes(int logl, int le) { return logl == 0 ? 1 : (logl + le - 1) / le; }
+constexpr int sched_logr(int logl, int le, int p) {
+    return p < sched_passes(logl, le) - 1 ? le : logl - le * (sched_passes(logl, le) - 1);
+}
+constexpr int sched_lns(int le, int p) { return le * p; }
+// Pass twiddle table: pass p >= 1 owns logr(p) rows of NS entries, row i
+// holding W_{NS*R}^(2^i * k) for k < NS (forward roots).  Offset of pass p:
+constexpr int sched_tw_off(int logl, int le, int p) {
+    int off = 0;
+    for (int q = 1; q < p; ++q) off += sched_logr(logl, le, q) << sched_lns(le, q);
+    return off;
+}
+constexpr int sched_tw_size(int logl, int le) { return sched_tw_off(logl, le, sched_passes(logl, le)); }
+
+// highest power of two <= q (q >= 1)
+constexpr int high_bit(int q) { return q <= 1 ? 1 : 2 * high_bit(q >> 1); }
+
+// Multiply v[OFF + q] (q = 1..R-1) by W^(q*k) of a pass whose table rows
+// `tp[i*NS + k]` hold W^(2^i * k): loads the log2(R) power-of-two roots
+// (coalesced across lanes) and composes the rest, w_q = w_(q - hb) * w_hb,
+// one complex product each.
+template <int R, int DIR, int OFF, int E>
+__device__ __forceinline__ void pass_twiddle(float2 (&v)[E], const float2* __restrict__ tp, int ns, int k) {
+    constexpr int LOGR = ilog2(R);
+    float2 w[R];
+    static_for<0, LOGR>([&](auto i) { w[1 << i.value] = tp[i.value * ns + k]; });
+    static_for<3, R>([&](auto q) {
+        constexpr int hb = high_bit(q.value);
+        if constexpr (hb != q.value) w[q.value] = cmul(w[q.value - hb], w[hb]);
+    });
+    static_for<1, R>([&](auto q) { v[OFF + q.value] = cmul_tw<DIR>(v[OFF + q.value], w[q.value]); });
+}
+
 // 32-bit bit reversal of the low `bits` bits (bits in [1, 31]).
 __device__ __forceinline__ uint32_t brev_low(uint32_t x, int bits) {
     return __brev(x) >> (32 - bits);

@@ -22,9 +22,9 @@ struct mfft_plan {
     bool r2c_fused = false, c2r_fused = false;
 
     // device memory owned by the plan
-    float2* tw = nullptr;       // W_core^m, m in [0, core_n)   (stage + LDS flows)
-    float2* tw_n1 = nullptr;    // W_n1^m                        (four-step pass 1)
-    float2* tw_n2 = nullptr;    // W_n2^m                        (four-step pass 2)
+    float2* tw = nullptr;       // stage flows: W_core^m, m in [0, core_n); LDS flow: pass table
+    float2* tw_n1 = nullptr;    // four-step pass-1 Stockham pass table (length n1)
+    float2* tw_n2 = nullptr;    // four-step pass-2 Stockham pass table (length n2)
     float2* tw_lo = nullptr;    // W_core^m, m < 2^h             (four-step twiddle, low digit)
     float2* tw_hi = nullptr;    // W_core^(m*2^h)                (four-step twiddle, high digit)
     int tw_h = 0;
@@ -53,7 +53,7 @@ inline void mark(hipStream_t s) {
 }
 
 constexpr int kMaxLog2N = 20;        // reference range: 8 .. 2^20 (docs/user-guide/transforms.md)
-constexpr int kMaxLdsLog2 = 13;      // single-pass LDS kernel: core length <= 8192
+constexpr int kMaxLdsLog2 = 14;      // single-pass LDS kernel: core length <= 16384
 constexpr int kMinFourStepLog2 = 8;  // four-step needs n1, n2 >= 16
 
 // ---- stage_kernels.hip: reference global-stage flows, real epilogues ------
@@ -85,6 +85,7 @@ hipError_t launch_lds(int mode, int dir, int log2l, int elems, const void* src, 
 
 // ---- fourstep_kernels.hip: two-pass column/row FFT -----------------------
 bool fourstep_supported(int log2n1, int log2n2);
+int fourstep_col_loge(int logl);  // log2 elements per thread of a pass of length 2^logl
 void fourstep_default_split(int log2n, int* log2n1, int* log2n2);
 hipError_t launch_fourstep(int dir, const float2* src, float2* dst, const mfft_plan* p,
                            int64_t rows, float scale, hipStream_t stream, int* launches);

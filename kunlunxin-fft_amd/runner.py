@@ -22,7 +22,7 @@ run_hybrid (adapter_hybrid.py:224)           FOUR_STEP (n1 = N/tile)         til
 The M1/M2/M3 names exist so a plan naming them still runs: on MI355X the
 stages they fuse (in global memory, as a dense matmul, or as XOR-gather
 maps) all run inside one LDS-resident kernel, or the four-step for core
-lengths above 8192.
+lengths above 16384.
 
 Every transform semantic -- C2C forward/inverse with its norm, R2C and C2R
 -- is one native plan: the conjugation, the norm scale and the real-FFT
@@ -79,8 +79,8 @@ def flow_params(executed: str, n: int, transform_type: str, block, params: dict)
     core = n // 2 if transform_type in ("r2c", "c2r") else n
     # A legacy table entry measured on the c2c core of length n also answers
     # r2c/c2r, whose core is n/2: keep its flow where the flow can run that
-    # core, else let the library pick (LDS up to 8192, four-step above).
-    if kind == "lds" and core > 8192:
+    # core, else let the library pick (LDS up to 16384, four-step above).
+    if kind == "lds" and core > 16384:
         return native.FLOW_AUTO, ()
     if kind == "fourstep":
         n1 = int(params.get("n1", 0))
@@ -232,7 +232,7 @@ def fft_dif_radix4_batch(x, block: int = DEFAULT_STAGE_BLOCK, variant: str = "fo
 
 
 def fft_lds_fused(x, elems: int = 0):
-    """Single-pass LDS-resident Stockham FFT (core length <= 8192)."""
+    """Single-pass LDS-resident Stockham FFT (core length <= 16384)."""
     return _single("fft_lds_fused", x, None, {"elems": elems})
 
 
