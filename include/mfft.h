@@ -76,13 +76,14 @@ enum {
     MFFT_FLOW_RADIX2_DIF = 2,  /* M0 fft_dif: bit reversal folded into the last stage (runner.py:165-206) */
     MFFT_FLOW_RADIX4_DIT = 3,  /* M5 fft_dit_radix4: digit reversal folded into stage 0 (runner.py:1399-1470) */
     MFFT_FLOW_RADIX4_DIF = 4,  /* M5 fft_dif_radix4 (runner.py:1473-1540) */
-    MFFT_FLOW_LDS_FUSED = 5,   /* one pass: whole transform resident in LDS/registers (core n <= 16384) */
+    MFFT_FLOW_LDS_FUSED = 5,   /* one pass: whole transform resident in LDS/registers (core n <= 32768) */
     MFFT_FLOW_FOUR_STEP = 6    /* two passes: column FFTs + twiddle, then row FFTs (core n >= 256) */
 };
 
 /* Flow parameters (params[i], all optional, 0 = library default):
  *   RADIX2_* / RADIX4_*: params[0] = threads per block (64..1024, power of two)
- *   LDS_FUSED:           params[0] = elements per thread (4, 8 or 16)
+ *   LDS_FUSED:           params[0] = elements per thread (4, 8, 16 or 32; 32 from 2^10,
+ *                                    >= 16 from 2^13, 32 at 2^15, not 32 for r2c)
  *   FOUR_STEP:           params[0] = n1 (column FFT length; n2 = core_n/n1),
  *                        params[1] = batch rows per chunk (both passes run
  *                                    chunk by chunk; 0 = whole batch) */

@@ -1,4 +1,4 @@
-// lds_kernels.hip -- single-pass LDS-resident FFT for core lengths 1..16384.
+// lds_kernels.hip -- single-pass LDS-resident FFT for core lengths 1..32768.
 //
 // One HBM read and one HBM write per element: every transform stays inside
 // one workgroup from its first load to its last store.  This is the MI355X
@@ -45,7 +45,10 @@ struct LdsCfg {
     static constexpr int TPB = WG / T;                     // transforms per block
     static constexpr int P = sched_passes(LOGL, LE);       // passes
     static constexpr int PITCH = L + (L >> 4) + 1;
-    static constexpr int LDS_ELEMS = TPB * PITCH;
+    // 32 elements per thread exchange real and imaginary parts separately
+    // through a float array: half the LDS, twice the barriers.
+    static constexpr bool SPLIT = LE == 5;
+    static constexpr int LDS_FLOATS = TPB * PITCH * (SPLIT ? 1 : 2);
     static constexpr int logr(int p) { return sched_logr(LOGL, LE, p); }
     static constexpr int lns(int p) { return sched_lns(LE, p); }
 };
@@ -59,7 +62,10 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG)) void lds_fft_kernel(
     using C = LdsCfg<LOGL, LOGE>;
     constexpr int L = C::L, E = C::E, T = C::T, P = C::P;
     constexpr bool NEED_LDS = (P > 1) || (MODE == 1);
-    __shared__ float2 lds[NEED_LDS ? C::LDS_ELEMS : 1];
+    static_assert(!(C::SPLIT && MODE == 1), "the r2c stitch needs whole complex values in LDS");
+    __shared__ float2 lds_raw[NEED_LDS ? (C::LDS_FLOATS + 1) / 2 : 1];
+    float2* const lds = lds_raw;
+    float* const ldsf = reinterpret_cast<float*>(lds_raw);
 
     const int tid = threadIdx.x;
     const int tl = tid / T;
@@ -67,6 +73,7 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG)) void lds_fft_kernel(
     const int64_t row = (int64_t)blockIdx.x * C::TPB + tl;
     const bool active = row < rows;
     float2* lt = lds + (NEED_LDS ? tl * C::PITCH : 0);
+    float* ltf = ldsf + (NEED_LDS ? tl * C::PITCH : 0);
 
     float2 v[E];
 
@@ -115,7 +122,7 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG)) void lds_fft_kernel(
         constexpr int NB = E / R;
         constexpr int LNS = C::lns(p);
         constexpr int NS = 1 << LNS;
-        if constexpr (p > 0) {
+        if constexpr (p > 0 && !C::SPLIT) {
             static_for<0, NB>([&](auto m) {
                 static_for<0, R>([&](auto q) {
                     const int i = j + m.value * T + q.value * (L / R);
@@ -131,7 +138,7 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG)) void lds_fft_kernel(
             }
             dft<R, DIR, m.value * R, 1>(v);
         });
-        if constexpr (p < P - 1 || MODE == 1) {
+        if constexpr ((p < P - 1 || MODE == 1) && !C::SPLIT) {
             if constexpr (p > 0) __syncthreads();  // every thread has read this pass's inputs
             static_for<0, NB>([&](auto m) {
                 const int b = j + m.value * T;
@@ -139,6 +146,35 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG)) void lds_fft_kernel(
                 static_for<0, R>([&](auto q) { lt[pad(base + q.value * NS)] = v[m.value * R + q.value]; });
             });
             __syncthreads();
+        }
+        if constexpr (p < P - 1 && C::SPLIT) {
+            // Exchange with the next pass one component at a time.  The real
+            // parts are written from v[].x (this pass's layout) and read back
+            // into v[].x (the next pass's layout) while v[].y still holds this
+            // pass's imaginary parts; then the same for .y.
+            constexpr int LR1 = C::logr(p + 1);
+            constexpr int R1 = 1 << LR1;
+            constexpr int NB1 = E / R1;
+            static_for<0, 2>([&](auto comp) {
+                __syncthreads();  // the previous readers of this LDS are done
+                static_for<0, NB>([&](auto m) {
+                    const int b = j + m.value * T;
+                    const int base = ((b >> LNS) << (LNS + LR)) + (b & (NS - 1));
+                    static_for<0, R>([&](auto q) {
+                        const float2 x = v[m.value * R + q.value];
+                        ltf[pad(base + q.value * NS)] = comp.value == 0 ? x.x : x.y;
+                    });
+                });
+                __syncthreads();
+                static_for<0, NB1>([&](auto m) {
+                    static_for<0, R1>([&](auto q) {
+                        const int i = j + m.value * T + q.value * (L / R1);
+                        const float x = ltf[pad(i)];
+                        if constexpr (comp.value == 0) v[m.value * R1 + q.value].x = x;
+                        else v[m.value * R1 + q.value].y = x;
+                    });
+                });
+            });
         }
     });
 
@@ -198,9 +234,24 @@ hipError_t dispatch_mode(int mode, int dir, const void* src, void* dst, const fl
     return launch_one<LOGL, LOGE, 1, 2>(src, dst, tw, tw_real, rows, scale, stream);
 }
 
+// 32 elements per thread (split exchange): c2c and c2r only
+template <int LOGL>
+hipError_t dispatch_split(int mode, int dir, const void* src, void* dst, const float2* tw,
+                          const float2* tw_real, int64_t rows, float scale, hipStream_t stream) {
+    if (mode == 0) {
+        return dir < 0 ? launch_one<LOGL, 5, -1, 0>(src, dst, tw, tw_real, rows, scale, stream)
+                       : launch_one<LOGL, 5, 1, 0>(src, dst, tw, tw_real, rows, scale, stream);
+    }
+    if (mode == 2) return launch_one<LOGL, 5, 1, 2>(src, dst, tw, tw_real, rows, scale, stream);
+    return hipErrorInvalidValue;
+}
+
 template <int LOGL>
 hipError_t dispatch_elems(int loge, int mode, int dir, const void* src, void* dst, const float2* tw,
                           const float2* tw_real, int64_t rows, float scale, hipStream_t stream) {
+    if constexpr (LOGL >= 10) {
+        if (loge == 5) return dispatch_split<LOGL>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+    }
     switch (loge) {
         case 2: return dispatch_mode<LOGL, 2>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
         case 3: return dispatch_mode<LOGL, 3>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
@@ -210,18 +261,21 @@ hipError_t dispatch_elems(int loge, int mode, int dir, const void* src, void* ds
 
 }  // namespace
 
-bool lds_supported(int log2l, int elems) {
+bool lds_supported(int log2l, int elems, int mode) {
     if (log2l < 0 || log2l > kMaxLdsLog2) return false;
-    if (elems != 0 && elems != 4 && elems != 8 && elems != 16) return false;
-    // 8192 and 16384 points need 16 elements per thread (512 / 1024 threads,
-    // 69 / 139 KiB of LDS: one transform per workgroup)
-    if (log2l >= 13 && elems != 0 && elems != 16) return false;
+    if (elems != 0 && elems != 4 && elems != 8 && elems != 16 && elems != 32) return false;
+    // 32 elements per thread (split exchange) exist for 2^10..2^15 and never
+    // for the r2c stitch; 8192 and 16384 points take 16 or 32; 32768 only 32
+    if (elems == 32 && (log2l < 10 || mode == 1)) return false;
+    if (log2l >= 13 && elems != 0 && elems < 16) return false;
+    if (log2l == 15 && (mode == 1 || (elems != 0 && elems != 32))) return false;
     return true;
 }
 
 int lds_default_elems(int log2l) {
     if (log2l <= 4) return 16;  // one thread holds the whole transform (min(L, 16))
     if (log2l <= 6) return 8;
+    if (log2l >= 15) return 32;
     return 16;
 }
 
@@ -250,8 +304,9 @@ hipError_t launch_lds(int mode, int dir, int log2l, int elems, const void* src, 
         case 10: return dispatch_elems<10>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
         case 11: return dispatch_elems<11>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
         case 12: return dispatch_elems<12>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 13: return dispatch_mode<13, 4>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 14: return dispatch_mode<14, 4>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 13: return dispatch_elems<13>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 14: return dispatch_elems<14>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 15: return dispatch_split<15>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -191,7 +191,10 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
     const int dir = transform_direction == MFFT_FORWARD ? -1 : 1;
 
     // ---- resolve and check the flow
-    if (flow == MFFT_FLOW_AUTO) flow = logc <= mfft::kMaxLdsLog2 ? MFFT_FLOW_LDS_FUSED : MFFT_FLOW_FOUR_STEP;
+    // LDS kernel mode: 0 c2c core (also the non-fused real cores), 1 r2c, 2 c2r
+    const int lds_mode = transform_type == MFFT_R2C ? 1 : (transform_type == MFFT_C2R ? 2 : 0);
+    if (flow == MFFT_FLOW_AUTO)
+        flow = mfft::lds_supported(logc, 0, lds_mode) ? MFFT_FLOW_LDS_FUSED : MFFT_FLOW_FOUR_STEP;
     int block = 256, elems = 0;
     int64_t n1 = 0, n2 = 0, chunk = 0;
     switch (flow) {
@@ -212,13 +215,13 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
             break;
         }
         case MFFT_FLOW_LDS_FUSED:
-            if (!mfft::lds_supported(logc, prm[0]))
+            if (!mfft::lds_supported(logc, prm[0], lds_mode))
                 return fail(MFFT_ERR_UNSUPPORTED,
-                            "LDS_FUSED runs core lengths up to 2^%d with 4, 8 or 16 elements per thread "
+                            "LDS_FUSED runs core lengths up to 2^%d (r2c: 2^14) with 4, 8, 16 or 32 "
+                            "elements per thread (32 from 2^10; 2^13, 2^14: 16 or 32; 2^15: 32) "
                             "(got core length %lld, elements %d)",
                             mfft::kMaxLdsLog2, (long long)core_n, prm[0]);
             elems = prm[0] ? prm[0] : mfft::lds_default_elems(logc);
-            if (logc >= 13) elems = 16;
             block = mfft::lds_threads_per_block(logc, elems);
             break;
         case MFFT_FLOW_FOUR_STEP: {

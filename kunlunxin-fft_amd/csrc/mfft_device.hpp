@@ -165,16 +165,27 @@ constexpr int high_bit(int q) { return q <= 1 ? 1 : 2 * high_bit(q >> 1); }
 // `tp[i*NS + k]` hold W^(2^i * k): loads the log2(R) power-of-two roots
 // (coalesced across lanes) and composes the rest, w_q = w_(q - hb) * w_hb,
 // one complex product each.
+// Radix 32 instead multiplies v[q] by w_(2^i) for every set bit i of q, so
+// only log2(R) roots are live (the composed form would hold R of them).
 template <int R, int DIR, int OFF, int E>
 __device__ __forceinline__ void pass_twiddle(float2 (&v)[E], const float2* __restrict__ tp, int ns, int k) {
     constexpr int LOGR = ilog2(R);
-    float2 w[R];
-    static_for<0, LOGR>([&](auto i) { w[1 << i.value] = tp[i.value * ns + k]; });
-    static_for<3, R>([&](auto q) {
-        constexpr int hb = high_bit(q.value);
-        if constexpr (hb != q.value) w[q.value] = cmul(w[q.value - hb], w[hb]);
-    });
-    static_for<1, R>([&](auto q) { v[OFF + q.value] = cmul_tw<DIR>(v[OFF + q.value], w[q.value]); });
+    if constexpr (R <= 16) {
+        float2 w[R];
+        static_for<0, LOGR>([&](auto i) { w[1 << i.value] = tp[i.value * ns + k]; });
+        static_for<3, R>([&](auto q) {
+            constexpr int hb = high_bit(q.value);
+            if constexpr (hb != q.value) w[q.value] = cmul(w[q.value - hb], w[hb]);
+        });
+        static_for<1, R>([&](auto q) { v[OFF + q.value] = cmul_tw<DIR>(v[OFF + q.value], w[q.value]); });
+    } else {
+        static_for<0, LOGR>([&](auto i) {
+            const float2 w = tp[i.value * ns + k];
+            static_for<1, R>([&](auto q) {
+                if constexpr ((q.value >> i.value) & 1) v[OFF + q.value] = cmul_tw<DIR>(v[OFF + q.value], w);
+            });
+        });
+    }
 }
 
 // 32-bit bit reversal of the low `bits` bits (bits in [1, 31]).

@@ -53,7 +53,7 @@ inline void mark(hipStream_t s) {
 }
 
 constexpr int kMaxLog2N = 20;        // reference range: 8 .. 2^20 (docs/user-guide/transforms.md)
-constexpr int kMaxLdsLog2 = 14;      // single-pass LDS kernel: core length <= 16384
+constexpr int kMaxLdsLog2 = 15;      // single-pass LDS kernel: core length <= 32768
 constexpr int kMinFourStepLog2 = 8;  // four-step needs n1, n2 >= 16
 
 // ---- stage_kernels.hip: reference global-stage flows, real epilogues ------
@@ -76,7 +76,7 @@ hipError_t launch_c2r_pre(const float2* x, float2* z, const float2* tw_real, int
 // ---- lds_kernels.hip: single-pass LDS-resident Stockham kernel ------------
 // mode 0: c2c core; 1: r2c (core forward + fused stitch); 2: c2r (fused
 // pre-twiddle + inverse core).  `log2l` is the core length's log2.
-bool lds_supported(int log2l, int elems);
+bool lds_supported(int log2l, int elems, int mode);  // mode as launch_lds
 int lds_default_elems(int log2l);
 int lds_threads_per_block(int log2l, int elems);
 hipError_t launch_lds(int mode, int dir, int log2l, int elems, const void* src, void* dst,

@@ -22,7 +22,7 @@ run_hybrid (adapter_hybrid.py:224)           FOUR_STEP (n1 = N/tile)         til
 The M1/M2/M3 names exist so a plan naming them still runs: on MI355X the
 stages they fuse (in global memory, as a dense matmul, or as XOR-gather
 maps) all run inside one LDS-resident kernel, or the four-step for core
-lengths above 16384.
+lengths above 32768.
 
 Every transform semantic -- C2C forward/inverse with its norm, R2C and C2R
 -- is one native plan: the conjugation, the norm scale and the real-FFT
@@ -79,9 +79,21 @@ def flow_params(executed: str, n: int, transform_type: str, block, params: dict)
     core = n // 2 if transform_type in ("r2c", "c2r") else n
     # A legacy table entry measured on the c2c core of length n also answers
     # r2c/c2r, whose core is n/2: keep its flow where the flow can run that
-    # core, else let the library pick (LDS up to 16384, four-step above).
-    if kind == "lds" and core > 16384:
-        return native.FLOW_AUTO, ()
+    # core, else let the library pick (LDS up to 32768, four-step above).
+    if kind == "lds":
+        # LDS kernel limits: core <= 32768 (r2c: 16384); 32 elements per
+        # thread from 1024 points and never for r2c; >= 16 from 8192 points
+        e = int(params.get("elems", 0))
+        logc = core.bit_length() - 1
+        if core > 32768 or (transform_type == "r2c" and core > 16384):
+            return native.FLOW_AUTO, ()
+        if e == 32 and (logc < 10 or transform_type == "r2c"):
+            e = 0
+        if logc >= 13 and 0 < e < 16:
+            e = 0
+        if logc == 15:
+            e = 0
+        return flow, (e,)
     if kind == "fourstep":
         n1 = int(params.get("n1", 0))
         if core < 256:
@@ -99,8 +111,6 @@ def flow_params(executed: str, n: int, transform_type: str, block, params: dict)
         if b < 64 or b > 1024:
             raise ValueError(f"block must be a power of two in [64, 1024], got {b}")
         return flow, (b,)
-    if kind == "lds":
-        return flow, (int(params.get("elems", 0)),)
     if kind == "hybrid":
         tile = int(params.get("tile", 0))
         n1 = core // tile if tile and core % tile == 0 else 0
@@ -232,7 +242,7 @@ def fft_dif_radix4_batch(x, block: int = DEFAULT_STAGE_BLOCK, variant: str = "fo
 
 
 def fft_lds_fused(x, elems: int = 0):
-    """Single-pass LDS-resident Stockham FFT (core length <= 16384)."""
+    """Single-pass LDS-resident Stockham FFT (core length <= 32768)."""
     return _single("fft_lds_fused", x, None, {"elems": elems})
 
 

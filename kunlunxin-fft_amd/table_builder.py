@@ -66,7 +66,11 @@ def candidates(n: int, b: int, direction: str, space):
         out.append((f"m5_{direction}@256", name, 256, {}, ("global-stage", "radix4-scalar", "baseline-global-stage")))
     if n <= space.lds_max_n:
         for e in space.lds_elems:
-            if logn >= 13 and e != 16:
+            if logn >= 13 and e < 16:
+                continue
+            if logn == 15 and e != 32:
+                continue
+            if e == 32 and logn < 10:
                 continue
             if n <= 16 and e != 16:
                 continue

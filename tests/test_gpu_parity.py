@@ -75,7 +75,8 @@ for name in ("fft_dit", "fft_dif"):
     FLOW_CASES += [(name, n) for n in (2, 8, 64, 1024, 4096, 1 << 15)]
 for name in ("fft_dit_radix4", "fft_dif_radix4"):
     FLOW_CASES += [(name, n) for n in (4, 8, 32, 256, 2048, 1 << 15)]
-FLOW_CASES += [("fft_lds_fused", n) for n in (1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192, 16384)]
+FLOW_CASES += [("fft_lds_fused", n) for n in (1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192, 16384,
+                                             32768)]
 FLOW_CASES += [("fft_four_step", n) for n in (256, 1024, 4096, 1 << 14, 1 << 16, 1 << 18, 1 << 20)]
 
 
@@ -103,8 +104,8 @@ def test_c2c_all_norms(gpu, name, norm, td):
     check(y, oracle.c2c(x, td, norm), f"{name} {td} {norm}")
 
 
-@pytest.mark.parametrize("elems", [4, 8, 16])
-@pytest.mark.parametrize("n", [32, 256, 2048, 4096])
+@pytest.mark.parametrize("elems,n", [(e, n) for e in (4, 8, 16) for n in (32, 256, 2048, 4096)]
+                         + [(32, n) for n in (1024, 2048, 4096, 8192, 16384, 32768)] + [(16, 16384)])
 def test_lds_elems_axis_neutral(gpu, elems, n):
     x = seeded_c64(n, 7)
     y = execute_fft_plan(mkplan("fft_lds_fused_batch", n, 7, params={"elems": elems}),
@@ -124,7 +125,7 @@ def test_four_step_split_and_chunk_neutral(gpu, n, n1, chunk):
 
 
 # ---------------------------------------------------------------- real flows
-REAL_CASES = [("fft_lds_fused", n) for n in (2, 4, 8, 64, 256, 4096, 8192, 16384, 32768)]
+REAL_CASES = [("fft_lds_fused", n) for n in (2, 4, 8, 64, 256, 4096, 8192, 16384, 32768, 65536)]
 REAL_CASES += [("fft_four_step", n) for n in (512, 1 << 15, 1 << 20)]
 REAL_CASES += [("fft_dit", n) for n in (4, 256, 4096)] + [("fft_dif_radix4", n) for n in (8, 256)]
 

@@ -245,7 +245,7 @@ def test_m0_plan_is_reference_shaped():
 
 def test_load_table_refuses_contract_violations(tmp_path):
     bad = [
-        _entry(2048, 1, "dit", real="lds-resident", params={"elems": 32}),
+        _entry(2048, 1, "dit", real="lds-resident", params={"elems": 64}),
         _entry(2048, 1, "dit", real="nope", unit="nope"),
         _entry(2048, 1, "dit", executed="fft_dit"),          # runner outside its family
         _entry(2048, 4, "dit", executed="fft_lds_fused"),    # single runner at batch 4
