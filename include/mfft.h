@@ -86,7 +86,12 @@ enum {
  *                                    >= 16 from 2^13, 32 at 2^15, not 32 for r2c)
  *   FOUR_STEP:           params[0] = n1 (column FFT length; n2 = core_n/n1),
  *                        params[1] = batch rows per chunk (both passes run
- *                                    chunk by chunk; 0 = whole batch) */
+ *                                    chunk by chunk; 0 = whole batch),
+ *                        params[2] = schedule: 0 = one column group per
+ *                                    workgroup; 1 = persistent workgroups (one
+ *                                    resident wave of them) that load their
+ *                                    next column group while transforming the
+ *                                    current one */
 #define MFFT_MAX_PARAMS 4
 
 typedef struct mfft_plan mfft_plan;

@@ -26,14 +26,37 @@
 
 namespace mfft {
 
-// column-group width and elements per thread for a pass of length 2^logl
-constexpr int col_loge(int logl) { return logl >= 8 ? 4 : (logl >= 6 ? 3 : 2); }
-constexpr int col_logc(int logl) { return logl >= 9 ? 3 : 4; }
+// Elements per thread and column-group width for a pass of length 2^logl.
+// 16 columns make every row access a 128-byte run (8 columns: 64-byte runs,
+// which measured about 20% less HBM bandwidth for these strided reads).  From
+// 512 points a thread holds 32 elements and the exchange is split into real
+// and imaginary halves, which keeps a block of 16 columns within 70 KB of LDS
+// and about 100 VGPRs, so two blocks share a CU.
+constexpr int col_loge(int logl) { return logl >= 9 ? 5 : (logl >= 8 ? 4 : (logl >= 6 ? 3 : 2)); }
+constexpr int col_logc(int) { return 4; }
 int fourstep_col_loge(int logl) { return col_loge(logl); }
 
 namespace {
 
 __device__ __forceinline__ int pad(int i) { return i + (i >> 4); }
+// pad(i + K) from pi = pad(i), for a compile-time K: when K is a multiple of
+// 16 it is pi + K + K/16, a constant offset the LDS instruction encodes, so
+// a run of accesses shares one address register.
+template <int K>
+__device__ __forceinline__ int pad_add(int pi, int i) {
+    if constexpr (K % 16 == 0) return pi + K + K / 16;
+    else return pad(i + K);
+}
+
+// p + bytes for a wave-uniform p and a 32-bit lane offset: the address then
+// takes the scalar-base + 32-bit vector-offset form (one VGPR per access, no
+// 64-bit address arithmetic per element).  Offsets stay below 2^23 bytes
+// because they never leave one transform of at most 2^20 points.
+template <typename T>
+__device__ __forceinline__ T* byte_off(T* p, uint32_t bytes) {
+    using B = std::conditional_t<std::is_const<T>::value, const char, char>;
+    return reinterpret_cast<T*>(reinterpret_cast<B*>(p) + bytes);
+}
 
 // Workgroups are dispatched to the 8 XCDs round-robin (block p -> XCD p % 8),
 // and each XCD has its own L2.  With 8 columns per block a 128-byte row
@@ -50,6 +73,7 @@ __device__ __forceinline__ int xcd_pair_block(int p, int total) {
 template <int LOGL, int LOGE, int LOGC>
 struct ColCfg {
     static_assert(LOGE < LOGL, "a column pass needs more than one thread per column");
+    static constexpr int LOG_L = LOGL, LOG_E = LOGE;
     static constexpr int L = 1 << LOGL;
     static constexpr int E = 1 << LOGE;
     static constexpr int C = 1 << LOGC;
@@ -63,7 +87,42 @@ struct ColCfg {
     static constexpr int PITCH = PITCH0 + ((32 / C - PITCH0 % 32) + 32) % 32;
     static constexpr int logr(int p) { return sched_logr(LOGL, LOGE, p); }
     static constexpr int lns(int p) { return sched_lns(LOGE, p); }
+    // last pass: radix, butterflies per thread, span
+    static constexpr int LR_LAST = sched_logr(LOGL, LOGE, P - 1);
+    static constexpr int R_LAST = 1 << LR_LAST;
+    static constexpr int NB_LAST = E / R_LAST;
+    static constexpr int NS_LAST = L / R_LAST;
+    static constexpr int TW_SIZE = sched_tw_size(LOGL, LOGE);  // pass twiddle table entries
+    // 32 elements per thread exchange real and imaginary parts separately
+    // through a float array (half the LDS of a float2 exchange).  Its column
+    // pitch, in floats, is == 64/C (mod 64) for the same bank tiling.
+    static constexpr bool SPLIT = LOGE == 5;
+    static constexpr int PITCHF = PITCH0 + ((64 / C - PITCH0 % 64) + 64) % 64;
+    // LDS floats: the exchange, and the float2 staging of the transposed
+    // store (all C columns at once, or C/2 at a time when split)
+    static constexpr int XCH_FLOATS = SPLIT ? C * PITCHF : 2 * C * PITCH;
+    static constexpr int STORE_FLOATS = SPLIT ? C * PITCH : 2 * C * PITCH;
+    static constexpr int LDS_FLOAT2 = ((XCH_FLOATS > STORE_FLOATS ? XCH_FLOATS : STORE_FLOATS) + 1) / 2;
 };
+
+// The value unchanged, but hidden from the optimizer: work derived from it
+// (twiddle reads, products) stays inside the loop that uses it instead of
+// being hoisted out and held in registers across the loop.
+__device__ __forceinline__ int opaque(int x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+__device__ __forceinline__ float2 opaque(float2 x) {
+    asm volatile("" : "+v"(x.x), "+v"(x.y));
+    return x;
+}
+// For a wave-uniform element offset (kept in SGPRs): stops the loop optimizer
+// from turning per-element addresses into one 64-bit pointer register per
+// access.  (An offset, not a pointer, so the pointer stays a known global one.)
+__device__ __forceinline__ int64_t opaque_uniform(int64_t x) {
+    asm volatile("" : "+s"(x));
+    return x;
+}
 
 // W_N^e for e < N as the product of the two small tables
 __device__ __forceinline__ float2 big_root(const float2* __restrict__ lo, const float2* __restrict__ hi,
@@ -71,43 +130,83 @@ __device__ __forceinline__ float2 big_root(const float2* __restrict__ lo, const 
     return cmul(lo[e & ((1u << h) - 1)], hi[e >> h]);
 }
 
-// KIND 0: pass 1 (column FFT of length L = N1 over S = N2 columns, twiddle,
-//         transposed store).  KIND 1: pass 2 (in place, L = N2, S = N1 columns).
-template <int LOGL, int LOGE, int LOGC, int DIR, int KIND>
-__global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_pass_kernel(
-    const float2* src, float2* dst, const float2* __restrict__ tw,
-    const float2* __restrict__ tw_lo, const float2* __restrict__ tw_hi, int tw_h, int logn,
-    int log_s, float scale) {
-    using C = ColCfg<LOGL, LOGE, LOGC>;
-    constexpr int L = C::L, E = C::E, T = C::T, P = C::P, NC = C::C;
-    __shared__ float2 lds[NC * C::PITCH];
+// Pass-1 four-step twiddles of one thread, for its column n2: the outputs of
+// last-pass butterfly b = j + m*T sit at k1 = b + q*NS, so W_N^(n2*k1) =
+// W_N^(n2*b) * (W_N^(n2*NS))^q.  Holds W_N^(n2*b) per butterfly and
+// W_N^(n2*NS*2^i); the other powers are composed when applied.
+template <class C>
+struct BigTw {
+    float2 w0[C::NB_LAST];
+    float2 sp[C::LR_LAST];
+};
 
-    const int tid = threadIdx.x;
-    const int c = tid & (NC - 1);
-    const int j = tid >> LOGC;
-    const int groups = (1 << log_s) >> LOGC;  // column groups per transform
-    const int bid = xcd_pair_block((int)blockIdx.x, (int)gridDim.x);
-    const int64_t row = bid / groups;
-    const int c0 = (bid - (int)(row * groups)) << LOGC;
-    const int64_t base = row << logn;
-    const float2* s = src + base + c0 + c;
-    float2* lt = lds + c * C::PITCH;
+template <class C>
+__device__ __forceinline__ void big_tw_load(BigTw<C>& f, const float2* __restrict__ lo,
+                                            const float2* __restrict__ hi, int h, uint32_t n2, int j) {
+    static_for<0, C::NB_LAST>([&](auto m) { f.w0[m.value] = big_root(lo, hi, h, n2 * (uint32_t)(j + m.value * C::T)); });
+    static_for<0, C::LR_LAST>([&](auto i) {
+        f.sp[i.value] = big_root(lo, hi, h, n2 * (uint32_t)(C::NS_LAST << i.value));
+    });
+}
 
-    float2 v[E];
-    {
-        constexpr int R0 = 1 << C::logr(0);
-        constexpr int NB0 = E / R0;
-        static_for<0, NB0>([&](auto m) {
-            static_for<0, R0>([&](auto q) {
-                const int i = j + m.value * T + q.value * (L / R0);
-                v[m.value * R0 + q.value] = s[(int64_t)i << log_s];
+template <class C, int DIR, int M, int E>
+__device__ __forceinline__ void big_tw_apply(float2 (&v)[E], const BigTw<C>& f) {
+    constexpr int R = C::R_LAST;
+    if constexpr (R <= 16) {
+        float2 s[R];
+        static_for<0, C::LR_LAST>([&](auto i) { s[1 << i.value] = f.sp[i.value]; });
+        static_for<3, R>([&](auto q) {
+            constexpr int hb = high_bit(q.value);
+            if constexpr (hb != q.value) s[q.value] = cmul(s[q.value - hb], s[hb]);
+        });
+        v[M * R] = cmul_tw<DIR>(v[M * R], f.w0[M]);
+        static_for<1, R>([&](auto q) {
+            v[M * R + q.value] = cmul_tw<DIR>(v[M * R + q.value], cmul(f.w0[M], s[q.value]));
+        });
+    } else {
+        // radix 32: one factor per set bit of q (no table of R powers in registers)
+        static_for<0, R>([&](auto q) { v[M * R + q.value] = cmul_tw<DIR>(v[M * R + q.value], f.w0[M]); });
+        static_for<0, C::LR_LAST>([&](auto i) {
+            static_for<1, R>([&](auto q) {
+                if constexpr ((q.value >> i.value) & 1)
+                    v[M * R + q.value] = cmul_tw<DIR>(v[M * R + q.value], f.sp[i.value]);
             });
         });
     }
-    // KIND 1 runs in place (src == dst): every element of this block's columns
-    // is in registers before the first barrier, all stores come after it, and
-    // no other block touches these columns.
+}
 
+// Pass-0 operands of one column group: s = the group's first element of the
+// transform (wave-uniform), lane (c, j) reads rows j + m*T + q*L/R0 of column c.
+// Every address is a wave-uniform row pointer (SGPRs) plus one lane offset
+// shared by all rows, so the 2^LOGE loads hold one address VGPR, not one each.
+template <class C>
+__device__ __forceinline__ void col_load(float2 (&v)[C::E], const float2* s, int c, int j, int log_s) {
+    constexpr int R0 = 1 << C::logr(0);
+    constexpr int NB0 = C::E / R0;
+    const uint32_t lane = (uint32_t)(c + (j << log_s)) * 8u;
+    static_for<0, NB0>([&](auto m) {
+        static_for<0, R0>([&](auto q) {
+            const int row = m.value * C::T + q.value * (C::L / R0);
+            v[m.value * R0 + q.value] = *byte_off(s + ((int64_t)row << log_s), lane);
+        });
+    });
+}
+
+// The Stockham passes of one column group, in place in v.  Pass p > 0 reads
+// its operands from this thread's column in LDS; every pass but the last
+// writes its outputs back (float2 through `lds`, or, SPLIT, one component at
+// a time through the same memory as floats).  The last pass leaves its
+// outputs in registers, multiplied by the four-step twiddles for KIND 0,
+// which big() returns when the last pass starts (so they are not held in
+// registers through the earlier passes).  tw: the pass twiddle table, in
+// global memory or LDS.  With BARRIER0 the first LDS write also waits for
+// the previous group's LDS readers.
+template <class C, int DIR, int KIND, bool BARRIER0, class BigF>
+__device__ __forceinline__ void col_passes(float2 (&v)[C::E], float2* lds, const float2* tw, int c, int j,
+                                           BigF&& big) {
+    constexpr int L = C::L, E = C::E, T = C::T, P = C::P;
+    float2* lt = lds + c * C::PITCH;
+    float* ltf = reinterpret_cast<float*>(lds) + c * C::PITCHF;
     static_for<0, P>([&](auto pp) {
         constexpr int p = pp.value;
         constexpr int LR = C::logr(p);
@@ -115,75 +214,214 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_pass_
         constexpr int NB = E / R;
         constexpr int LNS = C::lns(p);
         constexpr int NS = 1 << LNS;
-        if constexpr (p > 0) {
+        const int pj = pad(j);
+        if constexpr (p > 0 && !C::SPLIT) {
             static_for<0, NB>([&](auto m) {
                 static_for<0, R>([&](auto q) {
-                    const int i = j + m.value * T + q.value * (L / R);
-                    v[m.value * R + q.value] = lt[pad(i)];
+                    v[m.value * R + q.value] = lt[pad_add<m.value * T + q.value * (L / R)>(pj, j)];
                 });
             });
         }
+        BigTw<C> f;
+        if constexpr (KIND == 0 && p == P - 1) f = big();
         static_for<0, NB>([&](auto m) {
             const int b = j + m.value * T;
             if constexpr (NS > 1) {
-                constexpr int TW_OFF = sched_tw_off(LOGL, LOGE, p);
+                constexpr int TW_OFF = sched_tw_off(C::LOG_L, C::LOG_E, p);
                 pass_twiddle<R, DIR, m.value * R>(v, tw + TW_OFF, NS, b & (NS - 1));
             }
             dft<R, DIR, m.value * R, 1>(v);
-            if constexpr (KIND == 0 && p == P - 1) {
-                // four-step twiddle W_N^(n2*k1) on the pass-1 outputs, in
-                // registers: k1 = b + q*NS, so W = W_N^(n2*b) * (W_N^(n2*NS))^q
-                const uint32_t n2 = (uint32_t)(c0 + c);
-                const float2 w0 = big_root(tw_lo, tw_hi, tw_h, n2 * (uint32_t)b);
-                float2 sp[R];
-                static_for<0, LR>([&](auto i) {
-                    sp[1 << i.value] = big_root(tw_lo, tw_hi, tw_h, n2 * (uint32_t)(NS << i.value));
-                });
-                static_for<3, R>([&](auto q) {
-                    constexpr int hb = high_bit(q.value);
-                    if constexpr (hb != q.value) sp[q.value] = cmul(sp[q.value - hb], sp[hb]);
-                });
-                v[m.value * R] = cmul_tw<DIR>(v[m.value * R], w0);
-                static_for<1, R>([&](auto q) {
-                    v[m.value * R + q.value] = cmul_tw<DIR>(v[m.value * R + q.value], cmul(w0, sp[q.value]));
-                });
-            }
+            if constexpr (KIND == 0 && p == P - 1) big_tw_apply<C, DIR, m.value>(v, f);
         });
-        if constexpr (p < P - 1 || KIND == 0) {
-            if constexpr (p > 0) __syncthreads();
+        if constexpr (p < P - 1 && !C::SPLIT) {
+            if constexpr (p > 0 || BARRIER0) __syncthreads();
             static_for<0, NB>([&](auto m) {
                 const int b = j + m.value * T;
                 const int base_o = ((b >> LNS) << (LNS + LR)) + (b & (NS - 1));
-                static_for<0, R>([&](auto q) { lt[pad(base_o + q.value * NS)] = v[m.value * R + q.value]; });
+                const int pb = pad(base_o);
+                static_for<0, R>([&](auto q) { lt[pad_add<q.value * NS>(pb, base_o)] = v[m.value * R + q.value]; });
             });
             __syncthreads();
         }
+        if constexpr (p < P - 1 && C::SPLIT) {
+            // real parts out of v[].x (this pass's layout) and back into v[].x
+            // (the next pass's layout) while v[].y still holds this pass's
+            // imaginary parts; then the same for .y
+            constexpr int R1 = 1 << C::logr(p + 1);
+            constexpr int NB1 = E / R1;
+            static_for<0, 2>([&](auto comp) {
+                if constexpr (p > 0 || BARRIER0 || comp.value > 0) __syncthreads();
+                static_for<0, NB>([&](auto m) {
+                    const int b = j + m.value * T;
+                    const int base_o = ((b >> LNS) << (LNS + LR)) + (b & (NS - 1));
+                    const int pb = pad(base_o);
+                    static_for<0, R>([&](auto q) {
+                        const float2 x = v[m.value * R + q.value];
+                        ltf[pad_add<q.value * NS>(pb, base_o)] = comp.value == 0 ? x.x : x.y;
+                    });
+                });
+                __syncthreads();
+                static_for<0, NB1>([&](auto m) {
+                    static_for<0, R1>([&](auto q) {
+                        const float x = ltf[pad_add<m.value * T + q.value * (L / R1)>(pj, j)];
+                        if constexpr (comp.value == 0) v[m.value * R1 + q.value].x = x;
+                        else v[m.value * R1 + q.value].y = x;
+                    });
+                });
+            });
+        }
     });
+}
 
+// KIND 0: Z[n2*N1 + k1] through LDS: the last-pass outputs (k1 = b + q*NS)
+// are staged per column, then read back with the lanes along k1 inside one
+// column, so every wave writes whole 128-byte lines (a direct store from the
+// Stockham registers writes 512/C-byte runs and measured slower).  SPLIT
+// stages half the columns at a time.  d = Z + c0*N1.
+// KIND 1: X[k1 + N1*k2] from registers, in place; d = X + c0 (k1 = c0 + c).
+template <class C, int KIND>
+__device__ __forceinline__ void col_store(const float2 (&v)[C::E], float2* d, float2* lds, int tid, int c, int j,
+                                          int log_s, float scale) {
     if constexpr (KIND == 0) {
-        // transposed store (the twiddle was applied in registers): lanes run
-        // along k1 inside one column, one contiguous run of L per column
-        static_for<0, E>([&](auto r) {
-            const int e = tid + r.value * C::WG;
-            const int cc = e >> LOGL;
-            const int k1 = e & (L - 1);
-            dst[base + ((int64_t)(c0 + cc) << LOGL) + k1] = lds[cc * C::PITCH + pad(k1)];
+        constexpr int HALVES = C::SPLIT ? 2 : 1;
+        constexpr int CH = C::C / HALVES;  // columns staged per round
+        static_for<0, HALVES>([&](auto h) {
+            __syncthreads();  // every read of the previous LDS contents is done
+            if (HALVES == 1 || c / CH == h.value) {
+                float2* lt = lds + (c - h.value * CH) * C::PITCH;
+                const int pj = pad(j);
+                static_for<0, C::NB_LAST>([&](auto m) {
+                    static_for<0, C::R_LAST>([&](auto q) {
+                        lt[pad_add<m.value * C::T + q.value * C::NS_LAST>(pj, j)] = v[m.value * C::R_LAST + q.value];
+                    });
+                });
+            }
+            __syncthreads();
+            float2* dh = d + ((int64_t)(h.value * CH) << C::LOG_L);
+            static_for<0, C::E / HALVES>([&](auto r) {
+                const int e = tid + r.value * C::WG;
+                const int cc = e >> C::LOG_L;
+                const int k1 = e & (C::L - 1);
+                *byte_off(dh + r.value * C::WG, (uint32_t)tid * 8u) = lds[cc * C::PITCH + pad(k1)];
+            });
         });
     } else {
-        constexpr int LR = C::logr(P - 1);
-        constexpr int R = 1 << LR;
-        constexpr int NB = E / R;
-        constexpr int NS = L / R;
-        float2* d = dst + base + c0 + c;
-        static_for<0, NB>([&](auto m) {
-            const int b = j + m.value * T;
-            static_for<0, R>([&](auto q) {
-                d[(int64_t)(b + q.value * NS) << log_s] = cscale(v[m.value * R + q.value], scale);
+        const uint32_t lane = (uint32_t)(c + (j << log_s)) * 8u;
+        static_for<0, C::NB_LAST>([&](auto m) {
+            static_for<0, C::R_LAST>([&](auto q) {
+                const int row = m.value * C::T + q.value * C::NS_LAST;
+                *byte_off(d + ((int64_t)row << log_s), lane) = cscale(v[m.value * C::R_LAST + q.value], scale);
             });
         });
     }
 }
 
+// KIND 0: pass 1 (column FFTs of length L = N1 over S = N2 columns, twiddle,
+//         transposed store).  KIND 1: pass 2 (in place, L = N2, S = N1 columns).
+// One column group per block: the C columns [c0, c0 + C) of one batch row.
+// KIND 1 runs in place (src == dst): every element of the block's columns is
+// in registers before the first barrier, all stores come after it, and no
+// other block touches these columns.
+template <int LOGL, int LOGE, int LOGC, int DIR, int KIND>
+__global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_pass_kernel(
+    const float2* src, float2* dst, const float2* __restrict__ tw,
+    const float2* __restrict__ tw_lo, const float2* __restrict__ tw_hi, int tw_h, int logn,
+    int log_s, float scale) {
+    using C = ColCfg<LOGL, LOGE, LOGC>;
+    __shared__ float2 lds[C::LDS_FLOAT2];
+    const int groups = (1 << log_s) >> LOGC;  // column groups per transform
+    const int bid = xcd_pair_block((int)blockIdx.x, (int)gridDim.x);
+    const int64_t row = bid / groups;
+    const int c0 = (bid - (int)(row * groups)) << LOGC;
+    const int tid = threadIdx.x;
+    const int c = tid & (C::C - 1);
+    const int j = tid >> LOGC;
+    const int64_t base = row << logn;
+
+    float2 v[C::E];
+    col_load<C>(v, src + base + c0, c, j, log_s);
+    col_passes<C, DIR, KIND, false>(v, lds, tw, c, j, [&] {
+        BigTw<C> f;
+        big_tw_load<C>(f, tw_lo, tw_hi, tw_h, (uint32_t)(c0 + c), j);
+        return f;
+    });
+    col_store<C, KIND>(v, KIND == 0 ? dst + base + ((int64_t)c0 << LOGL) : dst + base + c0, lds, tid, c, j,
+                       log_s, scale);
+}
+
+// Persistent form of the same pass: gridDim.x blocks, a multiple of the
+// column groups per transform, walk the `tiles` column groups of the launch
+// with stride gridDim.x, so a block keeps one column index c0 (and its
+// four-step twiddles, loaded once) while the batch row advances.  While a
+// group is transformed the next one is already loading into registers, so
+// HBM traffic continues through the block's compute and LDS phases; the pass
+// twiddles sit in LDS, which keeps the only global loads in flight during
+// the compute those of the next group.
+template <int LOGL, int LOGE, int LOGC, int DIR, int KIND>
+__global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG), 4) void fourstep_persist_kernel(
+    const float2* src, float2* dst, const float2* __restrict__ tw,
+    const float2* __restrict__ tw_lo, const float2* __restrict__ tw_hi, int tw_h, int logn,
+    int log_s, float scale, int64_t tiles) {
+    using C = ColCfg<LOGL, LOGE, LOGC>;
+    __shared__ float2 lds[C::LDS_FLOAT2];
+    __shared__ float2 lds_tw[C::TW_SIZE > 0 ? C::TW_SIZE : 1];
+    const int tid = threadIdx.x;
+    const int c = tid & (C::C - 1);
+    const int j = tid >> LOGC;
+    const int log_groups = log_s - LOGC;  // column groups per transform = 2^log_groups
+    const int64_t stride = gridDim.x;
+    const int64_t t0 = xcd_pair_block((int)blockIdx.x, (int)gridDim.x);
+    const int c0 = (int)(t0 & ((1 << log_groups) - 1)) << LOGC;
+
+    for (int i = tid; i < C::TW_SIZE; i += C::WG) lds_tw[i] = tw[i];
+    BigTw<C> f;
+    if constexpr (KIND == 0) big_tw_load<C>(f, tw_lo, tw_hi, tw_h, (uint32_t)(c0 + c), j);
+    float2 v[C::E];
+    col_load<C>(v, src + ((t0 >> log_groups) << logn) + c0, c, j, log_s);
+    __syncthreads();  // lds_tw complete
+
+    // one column group: transform v (group t) and store it.  Per-call copies
+    // of the loop invariants: recomputing addresses and the pass and
+    // four-step twiddles costs less than the registers that holding them
+    // across the loop (next to the prefetched group) would take.
+    auto process = [&](int64_t t) {
+        const int jl = opaque(j), cl = opaque(c), tl = opaque(tid);
+        col_passes<C, DIR, KIND, true>(v, lds, lds_tw, cl, jl, [&] {
+            BigTw<C> fl;
+            static_for<0, C::NB_LAST>([&](auto m) { fl.w0[m.value] = opaque(f.w0[m.value]); });
+            static_for<0, C::LR_LAST>([&](auto i) { fl.sp[i.value] = opaque(f.sp[i.value]); });
+            return fl;
+        });
+        const int64_t base = (t >> log_groups) << logn;
+        col_store<C, KIND>(v, dst + opaque_uniform(KIND == 0 ? base + ((int64_t)c0 << LOGL) : base + c0), lds, tl, cl,
+                           jl, log_s, scale);
+    };
+    int64_t t = t0;
+    for (; t + stride < tiles; t += stride) {
+        float2 vn[C::E];
+        col_load<C>(vn, src + opaque_uniform((((t + stride) >> log_groups) << logn) + c0), opaque(c), opaque(j),
+                    log_s);
+        process(t);
+        static_for<0, C::E>([&](auto r) { v[r.value] = vn[r.value]; });
+    }
+    process(t);
+}
+
+// Blocks of the persistent kernel one CU holds at once (occupancy query,
+// made once per kernel).
+template <int LOGL, int LOGE, int LOGC, int DIR, int KIND>
+int persist_blocks_per_cu() {
+    static const int n = [] {
+        int b = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fourstep_persist_kernel<LOGL, LOGE, LOGC, DIR, KIND>,
+                                                         ColCfg<LOGL, LOGE, LOGC>::WG, 0) != hipSuccess) {
+            (void)hipGetLastError();
+            b = 1;
+        }
+        return b > 0 ? b : 1;
+    }();
+    return n;
+}
 
 template <int LOGL, int DIR, int KIND>
 hipError_t launch_pass(const float2* src, float2* dst, const mfft_plan* p, int64_t rows,
@@ -193,10 +431,22 @@ hipError_t launch_pass(const float2* src, float2* dst, const mfft_plan* p, int64
     using C = ColCfg<LOGL, LOGE, LOGC>;
     const int logn = ilog2((int)p->core_n);
     const int64_t groups = ((int64_t)1 << log_s) >> LOGC;
-    const int64_t blocks = rows * groups;
+    const int64_t tiles = rows * groups;
     const float2* tw = KIND == 0 ? p->tw_n1 : p->tw_n2;
-    fourstep_pass_kernel<LOGL, LOGE, LOGC, DIR, KIND><<<(unsigned)blocks, C::WG, 0, stream>>>(
-        src, dst, tw, p->tw_lo, p->tw_hi, p->tw_h, logn, log_s, scale);
+    if (p->persistent) {
+        // a multiple of the column groups (fixed c0 per block) and of 16
+        // (whole XCD-pairing groups), at most one resident wave of blocks
+        const int64_t unit = groups > 16 ? groups : 16;
+        int64_t g = (int64_t)persist_blocks_per_cu<LOGL, LOGE, LOGC, DIR, KIND>() * p->num_cus;
+        g = g / unit * unit;
+        if (g < unit) g = unit;
+        if (g > tiles) g = tiles;
+        fourstep_persist_kernel<LOGL, LOGE, LOGC, DIR, KIND><<<(unsigned)g, C::WG, 0, stream>>>(
+            src, dst, tw, p->tw_lo, p->tw_hi, p->tw_h, logn, log_s, scale, tiles);
+    } else {
+        fourstep_pass_kernel<LOGL, LOGE, LOGC, DIR, KIND><<<(unsigned)tiles, C::WG, 0, stream>>>(
+            src, dst, tw, p->tw_lo, p->tw_hi, p->tw_h, logn, log_s, scale);
+    }
     mark(stream);
     return hipGetLastError();
 }

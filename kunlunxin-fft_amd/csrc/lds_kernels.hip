@@ -49,14 +49,27 @@ struct LdsCfg {
     // through a float array: half the LDS, twice the barriers.
     static constexpr bool SPLIT = LE == 5;
     static constexpr int LDS_FLOATS = TPB * PITCH * (SPLIT ? 1 : 2);
+    // Waves per SIMD the register allocation must allow.  A split-exchange
+    // block uses at most 70 KB of LDS, so up to 16 waves of it fit a CU when
+    // each wave stays within 128 VGPRs; left to itself the compiler takes up
+    // to 167 for 32 elements and the CU then holds one block fewer.
+    static constexpr int MIN_WAVES = SPLIT ? 4 : 1;
     static constexpr int logr(int p) { return sched_logr(LOGL, LE, p); }
     static constexpr int lns(int p) { return sched_lns(LE, p); }
 };
 
 __device__ __forceinline__ int pad(int i) { return i + (i >> 4); }
+// pad(i + K) from pi = pad(i), for a compile-time K: when K is a multiple of
+// 16 it is pi + K + K/16, a constant offset the LDS instruction encodes, so
+// a run of accesses shares one address register.
+template <int K>
+__device__ __forceinline__ int pad_add(int pi, int i) {
+    if constexpr (K % 16 == 0) return pi + K + K / 16;
+    else return pad(i + K);
+}
 
 template <int LOGL, int LOGE, int DIR, int MODE>
-__global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG)) void lds_fft_kernel(
+__global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG), (LdsCfg<LOGL, LOGE>::MIN_WAVES)) void lds_fft_kernel(
     const void* __restrict__ src_v, void* __restrict__ dst_v, const float2* __restrict__ tw,
     const float2* __restrict__ tw_real, int64_t rows, float scale) {
     using C = LdsCfg<LOGL, LOGE>;
@@ -122,11 +135,11 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG)) void lds_fft_kernel(
         constexpr int NB = E / R;
         constexpr int LNS = C::lns(p);
         constexpr int NS = 1 << LNS;
+        const int pj = pad(j);
         if constexpr (p > 0 && !C::SPLIT) {
             static_for<0, NB>([&](auto m) {
                 static_for<0, R>([&](auto q) {
-                    const int i = j + m.value * T + q.value * (L / R);
-                    v[m.value * R + q.value] = lt[pad(i)];
+                    v[m.value * R + q.value] = lt[pad_add<m.value * T + q.value * (L / R)>(pj, j)];
                 });
             });
         }
@@ -143,7 +156,8 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG)) void lds_fft_kernel(
             static_for<0, NB>([&](auto m) {
                 const int b = j + m.value * T;
                 const int base = ((b >> LNS) << (LNS + LR)) + (b & (NS - 1));
-                static_for<0, R>([&](auto q) { lt[pad(base + q.value * NS)] = v[m.value * R + q.value]; });
+                const int pb = pad(base);
+                static_for<0, R>([&](auto q) { lt[pad_add<q.value * NS>(pb, base)] = v[m.value * R + q.value]; });
             });
             __syncthreads();
         }
@@ -160,16 +174,16 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG)) void lds_fft_kernel(
                 static_for<0, NB>([&](auto m) {
                     const int b = j + m.value * T;
                     const int base = ((b >> LNS) << (LNS + LR)) + (b & (NS - 1));
+                    const int pb = pad(base);
                     static_for<0, R>([&](auto q) {
                         const float2 x = v[m.value * R + q.value];
-                        ltf[pad(base + q.value * NS)] = comp.value == 0 ? x.x : x.y;
+                        ltf[pad_add<q.value * NS>(pb, base)] = comp.value == 0 ? x.x : x.y;
                     });
                 });
                 __syncthreads();
                 static_for<0, NB1>([&](auto m) {
                     static_for<0, R1>([&](auto q) {
-                        const int i = j + m.value * T + q.value * (L / R1);
-                        const float x = ltf[pad(i)];
+                        const float x = ltf[pad_add<m.value * T + q.value * (L / R1)>(pj, j)];
                         if constexpr (comp.value == 0) v[m.value * R1 + q.value].x = x;
                         else v[m.value * R1 + q.value].y = x;
                     });

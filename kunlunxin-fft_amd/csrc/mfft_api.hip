@@ -197,6 +197,7 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
         flow = mfft::lds_supported(logc, 0, lds_mode) ? MFFT_FLOW_LDS_FUSED : MFFT_FLOW_FOUR_STEP;
     int block = 256, elems = 0;
     int64_t n1 = 0, n2 = 0, chunk = 0;
+    int persistent = 0;
     switch (flow) {
         case MFFT_FLOW_RADIX2_DIT:
         case MFFT_FLOW_RADIX2_DIF:
@@ -240,6 +241,9 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
             n1 = (int64_t)1 << l1;
             n2 = (int64_t)1 << l2;
             chunk = prm[1] > 0 ? prm[1] : 0;
+            if (prm[2] < 0 || prm[2] > 1)
+                return fail(MFFT_ERR_VALUE, "FOUR_STEP schedule must be 0 or 1, got %d", prm[2]);
+            persistent = prm[2];
             break;
         }
         default:
@@ -249,6 +253,9 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
     int dev = 0;
     hipError_t he = hipGetDevice(&dev);
     if (he != hipSuccess) return hip_fail(he, "hipGetDevice");
+    int num_cus = 0;
+    he = hipDeviceGetAttribute(&num_cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (he != hipSuccess) return hip_fail(he, "hipDeviceGetAttribute(MultiprocessorCount)");
 
     mfft_plan* p = new (std::nothrow) mfft_plan();
     if (!p) return fail(MFFT_ERR_RUNTIME, "out of host memory");
@@ -265,6 +272,8 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
     p->n1 = n1;
     p->n2 = n2;
     p->chunk_rows = chunk;
+    p->persistent = persistent;
+    p->num_cus = num_cus > 0 ? num_cus : 1;
     p->r2c_fused = transform_type == MFFT_R2C && flow == MFFT_FLOW_LDS_FUSED;
     p->c2r_fused = transform_type == MFFT_C2R && flow == MFFT_FLOW_LDS_FUSED;
     // c2r: the half-length inverse core carries a factor 2 (entry.py:583-587)
@@ -317,7 +326,8 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
         case MFFT_FLOW_LDS_FUSED: core_launches = 1; break;
         case MFFT_FLOW_FOUR_STEP: {
             const int64_t ch = chunk > 0 ? chunk : batch;
-            core_launches = (int)(2 * ((batch + ch - 1) / ch));
+            const int64_t nc = (batch + ch - 1) / ch;
+            core_launches = (int)(2 * nc);
             break;
         }
     }

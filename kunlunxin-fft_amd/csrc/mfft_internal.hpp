@@ -19,6 +19,8 @@ struct mfft_plan {
     int elems = 16;      // LDS_FUSED: elements per thread
     int launches = 0;
     int64_t n1 = 0, n2 = 0, chunk_rows = 0;
+    int persistent = 0;  // FOUR_STEP: persistent blocks that prefetch their next column group
+    int num_cus = 0;     // compute units of `device` (persistent grid size)
     bool r2c_fused = false, c2r_fused = false;
 
     // device memory owned by the plan

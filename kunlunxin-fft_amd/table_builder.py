@@ -6,7 +6,8 @@ For every cell (N, batch, direction) it times the M0 incumbent (fft_dit /
 fft_dif and their batch forms) and every legal challenger of the published
 design space (config/butterfly_space.json): the radix-4 global-stage flow,
 the single-pass LDS kernel at each elements-per-thread setting, and the
-four-step at each split and chunking.  The fastest challenger is promoted
+four-step at each split, chunking and schedule (one column group per
+workgroup, or persistent workgroups).  The fastest challenger is promoted
 only when it beats the incumbent by at least GUARD_PCT percent (M0 closure);
 otherwise the cell keeps M0.  The table is bound to the device profile hash
 and the live environment fingerprint, so it selects only on the stack it was
@@ -89,8 +90,12 @@ def candidates(n: int, b: int, direction: str, space):
                 chunks += [c for c in space.fourstep_chunk_rows if c and c < b and n * c * 8 >= (16 << 20)
                            and n * c * 8 <= (128 << 20)]
             for ch in chunks:
-                out.append((f"fs_n1_{n1}_c{ch}", "fft_four_step" + sfx, 256, {"n1": n1, "chunk_rows": ch},
-                            ("four-step", "stockham-radix16", "four-step-two-pass")))
+                for pers in space.fourstep_persistent:
+                    params = {"n1": n1, "chunk_rows": ch}
+                    if pers:
+                        params["persistent"] = 1
+                    out.append((f"{'fsp' if pers else 'fs'}_n1_{n1}_c{ch}", "fft_four_step" + sfx, 256, params,
+                                ("four-step", "stockham-radix16", "four-step-two-pass")))
     return out
 
 

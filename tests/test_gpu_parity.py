@@ -124,6 +124,46 @@ def test_four_step_split_and_chunk_neutral(gpu, n, n1, chunk):
     check(y, np.fft.fft(x.astype(np.complex128)), f"four-step N={n} n1={n1} chunk={chunk}")
 
 
+@pytest.mark.parametrize("n,n1", [(256, 16), (1 << 10, 32), (1 << 12, 64), (1 << 14, 128), (1 << 15, 128),
+                                  (1 << 15, 256), (1 << 16, 256), (1 << 17, 256), (1 << 17, 512),
+                                  (1 << 18, 512), (1 << 19, 512), (1 << 19, 1024), (1 << 20, 1024)])
+@pytest.mark.parametrize("b,chunk", [(5, 0), (7, 3), (1, 0)])
+def test_four_step_persistent(gpu, n, n1, b, chunk):
+    """Persistent workgroups walk the column groups with a grid stride and
+    prefetch the next group; batches and chunks whose group count is not a
+    multiple of the grid leave some workgroups one group short."""
+    if n >= (1 << 19):
+        b = min(b, 3)
+    x = seeded_c64(n, b, session=4)
+    td = "inverse" if chunk == 3 else "forward"
+    norm = "ortho" if chunk == 3 else "backward"
+    plan = mkplan("fft_four_step_batch", n, b, td=td, norm=norm,
+                  params={"n1": n1, "chunk_rows": chunk, "persistent": 1})
+    y = execute_fft_plan(plan, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    check(y, np_ref(x, td, norm), f"persistent four-step N={n} n1={n1} B={b} chunk={chunk} {td}")
+
+
+def test_four_step_persistent_matches_per_group(gpu):
+    """Both schedules run the same butterflies and twiddles (only the
+    compiler's instruction choices may differ): outputs agree to 1e-6."""
+    n, b = 1 << 18, 40
+    x = torch.from_numpy(seeded_c64(n, b, session=5)).to(gpu)
+    y0 = execute_fft_plan(mkplan("fft_four_step_batch", n, b, params={"n1": 512}), x)
+    y1 = execute_fft_plan(mkplan("fft_four_step_batch", n, b, params={"n1": 512, "persistent": 1}), x)
+    d = (torch.linalg.vector_norm(y1 - y0) / torch.linalg.vector_norm(y0)).item()
+    assert d <= 1e-6, f"schedules differ: rel L2 {d:.3e}"
+
+
+def test_four_step_persistent_real(gpu):
+    n, b = 1 << 17, 6
+    xr = seeded_f32(n, b)
+    p = {"n1": 256, "chunk_rows": 4, "persistent": 1}
+    X = execute_fft_plan(mkplan("fft_four_step_batch", n, b, tt="r2c", params=p), torch.from_numpy(xr).to(gpu))
+    check(X.cpu().numpy(), oracle.r2c_dedicated(xr), "persistent r2c")
+    y = execute_fft_plan(mkplan("fft_four_step_batch", n, b, tt="c2r", td="inverse", params=p), X).cpu().numpy()
+    check(y, xr.astype(np.float64), "persistent r2c->c2r round trip")
+
+
 # ---------------------------------------------------------------- real flows
 REAL_CASES = [("fft_lds_fused", n) for n in (2, 4, 8, 64, 256, 4096, 8192, 16384, 32768, 65536)]
 REAL_CASES += [("fft_four_step", n) for n in (512, 1 << 15, 1 << 20)]
