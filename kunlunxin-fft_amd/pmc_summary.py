@@ -1,0 +1,185 @@
+"""Profile summaries for bench.py runs under rocprofv3 (CSV output).
+
+``traffic``: HBM traffic per kernel launch from two ``rocprofv3 --pmc`` runs.
+
+Reads the counter CSVs of a FETCH_SIZE run and a WRITE_SIZE run (counter
+values in KiB per dispatch, ``--output-format csv``), averages them per
+(kernel, grid), scales each counter by what it reads for the device copy of
+known size that bench.py performs first (256 MiB read + 256 MiB written,
+kernel ``__amd_rocclr_copyBuffer``), and matches every FFT kernel to the
+bench.py size it belongs to using ``gpurun_out/bench_detail.json`` of the same
+command: a dispatch of ``grid`` threads with 2^LOGE elements per thread covers
+grid * 2^LOGE complex points.
+
+Writes
+  * a JSON map ``"<kernel as bench.py names it>|N=<n>|rows=<rows per launch>"
+    -> HBM bytes per launch``, which bench.py reports as ``roofline.traffic``;
+  * a Markdown table (algorithmic bytes, measured bytes, their ratio).
+
+``stats``: the per-kernel duration table of ``rocprofv3 --kernel-trace
+--stats`` (its kernel_stats.csv) as Markdown.
+
+Usage:
+    python kunlunxin-fft_amd/pmc_summary.py traffic --fetch DIR --write DIR --detail bench_detail.json \
+        --json profiles/pmc_traffic.json --md profiles/<name>.md [--command TEXT]
+    python kunlunxin-fft_amd/pmc_summary.py stats --dir DIR --md profiles/<name>.md [--command TEXT]
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import glob
+import json
+import os
+import re
+import sys
+
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+COPY_BYTES = 256 << 20  # bench.py's calibration copy: 256 MiB each way
+
+
+def _counter_rows(d: str):
+    files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {d}")
+    for path in files:
+        with open(path, newline="") as f:
+            yield from csv.DictReader(f)
+
+
+def _short(name: str) -> str:
+    """Kernel symbol without return type, namespaces and parameter list."""
+    name = name.replace("void ", "").replace("mfft::(anonymous namespace)::", "")
+    return re.sub(r"\(.*$", "", name)
+
+
+def _template_args(name: str):
+    m = re.search(r"<([^<>]*)>", name)
+    if not m:
+        return None
+    try:
+        return [int(t.strip()) for t in m.group(1).split(",")]
+    except ValueError:
+        return None
+
+
+def per_kernel(d: str, counter: str):
+    acc = collections.defaultdict(list)
+    for r in _counter_rows(d):
+        if r.get("Counter_Name") != counter:
+            continue
+        name = _short(r["Kernel_Name"])
+        acc[(name, int(r["Grid_Size"]))].append(float(r["Counter_Value"]))
+    return {k: sum(v) / len(v) for k, v in acc.items()}
+
+
+def calibration(vals: dict) -> float:
+    """Counter KiB per KiB actually moved, from the largest copy dispatch."""
+    cands = [(g, v) for (n, g), v in vals.items() if n.startswith(COPY_KERNEL)]
+    if not cands:
+        raise SystemExit("the run holds no device copy to calibrate against")
+    g, v = max(cands)
+    return v / (COPY_BYTES / 1024)
+
+
+def _commands(f, command: str) -> None:
+    if command:
+        f.write("Commands (repo root, TMPDIR=/tmp):\n\n")
+        for line in command.split(";"):
+            f.write(f"    {line.strip()}\n")
+        f.write("\n")
+
+
+def stats(args) -> int:
+    files = glob.glob(os.path.join(args.dir, "**", "*kernel_stats.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no *kernel_stats.csv under {args.dir}")
+    with open(files[0], newline="") as f:
+        rows = list(csv.DictReader(f))
+    with open(args.md, "w") as f:
+        f.write("# Kernel durations (rocprofv3 --kernel-trace --stats)\n\n")
+        _commands(f, args.command)
+        f.write("| kernel | calls | total ms | average us | min us | max us | share |\n")
+        f.write("|---|---:|---:|---:|---:|---:|---:|\n")
+        for r in rows:
+            name = _short(r["Name"])
+            f.write(f"| {name} | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.3f} | "
+                    f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                    f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.1f}% |\n")
+    print(f"wrote {args.md} ({len(rows)} kernels)")
+    return 0
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    t = sub.add_parser("traffic")
+    t.add_argument("--fetch", required=True, help="output dir of the FETCH_SIZE run")
+    t.add_argument("--write", required=True, help="output dir of the WRITE_SIZE run")
+    t.add_argument("--detail", required=True, help="bench_detail.json written by the same bench command")
+    t.add_argument("--json", required=True)
+    t.add_argument("--md", required=True)
+    t.add_argument("--command", default="", help="commands that made the input, quoted in the Markdown")
+    st = sub.add_parser("stats")
+    st.add_argument("--dir", required=True, help="output dir of the --kernel-trace --stats run")
+    st.add_argument("--md", required=True)
+    st.add_argument("--command", default="")
+    args = ap.parse_args()
+    if args.cmd == "stats":
+        return stats(args)
+
+    fetch = per_kernel(args.fetch, "FETCH_SIZE")
+    write = per_kernel(args.write, "WRITE_SIZE")
+    f_cal, w_cal = calibration(fetch), calibration(write)
+    sizes = json.load(open(args.detail))["per_size"]
+
+    rows_out, traffic = [], {}
+    for (name, grid) in sorted(set(fetch) | set(write)):
+        t = _template_args(name)
+        if t is None or not name.startswith(("fourstep_pass_kernel", "fourstep_persist_kernel", "lds_fft_kernel")):
+            continue
+        logl, loge = t[0], t[1]
+        if name.startswith("fourstep_persist_kernel"):
+            continue  # grid is the resident wave, not the work: not matched by size
+        points = grid << loge
+        # every bench size this dispatch shape serves (two sizes can share
+        # one (kernel, grid), e.g. pass 2 of 2^19 and 2^20 points)
+        keys = []
+        for s in sizes:
+            n = s["n"]
+            if name.startswith("lds_fft_kernel") and s["flow"] == "lds-fused" and n == (1 << logl):
+                keys.append(f"lds_fft_kernel|N={n}|rows={points // n}")
+            elif name.startswith("fourstep") and s["flow"] == "four-step" and s.get("split"):
+                n1, n2, rows = s["split"]
+                kind = t[4]
+                if rows * n == points and (n1 if kind == 0 else n2) == (1 << logl):
+                    keys.append(f"fourstep_pass_kernel pass {kind + 1} (n{kind + 1}={1 << logl})"
+                                f"|N={n}|rows={rows}")
+        fb = fetch.get((name, grid), float("nan")) * 1024 / f_cal
+        wb = write.get((name, grid), float("nan")) * 1024 / w_cal
+        alg = 16 * points
+        for key in keys:
+            traffic[key] = round(fb + wb)
+            rows_out.append((key, name, grid, alg, fb, wb))
+
+    with open(args.json, "w") as f:
+        json.dump(traffic, f, indent=1, sort_keys=True)
+    with open(args.md, "w") as f:
+        f.write("# HBM traffic per launch (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE)\n\n")
+        _commands(f, args.command)
+        f.write(f"Calibration: the 256 MiB device copy ({COPY_KERNEL}) reads FETCH_SIZE = "
+                f"{f_cal * 256:.2f} MiB and WRITE_SIZE = {w_cal * 256:.2f} MiB, so FETCH_SIZE is scaled "
+                f"by {1 / f_cal:.3f} and WRITE_SIZE by {1 / w_cal:.3f}.  Algorithmic bytes = 16 per point "
+                f"(one complex64 read + one written).\n\n")
+        f.write("| bench kernel key | kernel | grid | algorithmic MiB | fetch MiB | write MiB | traffic / algorithmic |\n")
+        f.write("|---|---|---:|---:|---:|---:|---:|\n")
+        for key, name, grid, alg, fb, wb in rows_out:
+            f.write(f"| {key} | {name} | {grid} | {alg / 2**20:.1f} | {fb / 2**20:.1f} | {wb / 2**20:.1f} | "
+                    f"{(fb + wb) / alg:.3f} |\n")
+    print(f"wrote {args.json} ({len(traffic)} kernels) and {args.md}")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
