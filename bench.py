@@ -1,5 +1,5 @@
 """Benchmark: C2C complex64 GB/s and % of HBM peak, N = 2^10..2^20, plus the
-p50 latency at N=2048 B=1 (BASELINE.json metric), on one MI355X.
+p50 latency at N=2048 B=1 (the reference's headline metric), on one MI355X.
 
 One step = one forward C2C complex64 transform (through the public plan API:
 ``plan_fft`` with the device profile -> ``execute_fft_plan``) of every size
@@ -19,7 +19,7 @@ Also reported (on the same JSON line):
 * ``latency_n2048_b1``: the reference protocol (warmup 5, 5 x 32 trials,
   device sync per trial, pooled p50, scripts/issue10_wp3_holdout.py:176-190)
   for execute_fft_plan, plus the kernel-only event p50;
-* ``config2``: latency and GB/s of BASELINE config 2 (N in {1024, 2048}, B in
+* ``config2``: latency and GB/s of the reference's small-batch configuration (N in {1024, 2048}, B in
   {16, 64});
 * ``cpu_baseline``: the reference's own CPU FFT (butterfly::fft_dit built
   into oracle/_ref; the C restatement when that build is absent) on one core,
@@ -30,6 +30,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -63,7 +64,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every box here has one MI355X; "
-                                   "the batch shards across GPUs with no exchange (see DESIGN.md), "
+                                   "the batch would shard across GPUs with no exchange, "
                                    "but multi-GPU runs are not part of this benchmark",
                           "n_gpus": args.gpus}))
         return 2
@@ -124,11 +125,18 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # A full cyclic-GC pass over torch's object graph stalls the host for tens
+    # of milliseconds and leaves the GPU idle; collect and freeze the heap
+    # first and keep the collector off while the steps are timed.
+    gc.collect()
+    gc.freeze()
+    gc.disable()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    gc.enable()
     step_bytes = sum(16 * n * b for n, b, _, _ in work)
     wall = t1 - t0
     value = step_bytes * args.steps / wall / 1e9

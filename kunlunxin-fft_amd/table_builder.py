@@ -33,7 +33,7 @@ import time
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 
-C5_SIZES = [1 << k for k in range(4, 15)]        # N = 16 .. 2^14
+C5_SIZES = [1 << k for k in range(4, 15)]        # the reference's size sweep: N = 16 .. 2^14
 C5_BATCHES = [1, 16, 64, 256]
 ROOF_SIZES = [1 << k for k in range(10, 21)]      # roofline rows: B = max(64, 2^25/N)
 EXTRA_CELLS = [(1 << k, 1) for k in range(15, 21)] + [(1 << 16, 256), (256, 1), (4096, 64)]

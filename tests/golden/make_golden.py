@@ -12,7 +12,7 @@ expected output comes from a closed form or from the float64 DFT matrix
 * ``impulse256``    delta at 0 -> all ones (tests/test_fft.py:196-203)
 * ``tone256``       exp(2*pi*i*5*n/256) -> 256 at bin 5 (test_fft.py:205-211)
 * ``sentinel1024``  x = (1..N) - i*(1..N); DC bin = sum (scripts/smoke.py:72-94)
-* ``c1_in`` / ``c1_out``  BASELINE config C1: N=2048, B=1, seed
+* ``c1_in`` / ``c1_out``  the reference's headline case: N=2048, B=1, seed
                     102026 + 10*N + B, real/imag iid N(0,1) complex64 and
                     its float64 FFT (scripts/issue10_wp3_holdout.py:127-140)
 * ``rfft_in_<N>`` / ``rfft_out_<N>`` / ``irfft_out_<N>``  real input, its

@@ -4,7 +4,7 @@ C ABI (via the package's plan API or the ctypes NativePlan).
 Gate (north star): relative L2 error <= 1e-5 against the float64 oracle, and
 the reference's peak-normalised worst-element error (max_rel_error) <= 1e-5
 (the reference's own worst published figure is ~1.2e-6; its gate 1e-4).
-At BASELINE's full sizes the C oracle is checked on a subset of rows and
+At the benchmark's full sizes the C oracle is checked on a subset of rows and
 numpy's float64 FFT on all rows, plus size-independent properties (round
 trip, Parseval, linearity).
 """
@@ -200,7 +200,7 @@ def test_c2r_ignores_dc_nyquist_imag(gpu, golden, name):
     check(y, ref, f"c2r DC/Nyquist {name}")
 
 
-# ------------------------------------------------------- BASELINE configs
+# ------------------------------------ the reference's benchmark configurations
 def test_config1_n2048_b1(gpu, golden):
     x = golden["c1_in"]
     plan = plan_fft("dit", 2048, profile_hash=DeviceProfile.load().hash())
