@@ -20,10 +20,13 @@ Also reported (on the same JSON line):
   device sync per trial, pooled p50, scripts/issue10_wp3_holdout.py:176-190)
   for execute_fft_plan, plus the kernel-only event p50;
 * ``config2``: latency and GB/s of the reference's small-batch configuration (N in {1024, 2048}, B in
-  {16, 64});
+  {16, 64}); ``config4``: the same for N=2^20 B=1 and N=2^16 B=256;
+* ``per_size[].vendor_*``: torch.fft.fft (rocFFT) on the same inputs, a
+  comparison column only;
 * ``cpu_baseline``: the reference's own CPU FFT (butterfly::fft_dit built
   into oracle/_ref; the C restatement when that build is absent) on one core,
-  on a bounded sample -- one transform of each N = 2^10..2^20 -- median of 3.
+  on a bounded sample -- 16 transforms of each N = 2^10..2^20 -- median of 3,
+  plus the same rows spread over up to 16 host threads (``all_cores``).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -59,7 +62,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-latency", action="store_true", help="skip the latency / config-2 legs")
+    ap.add_argument("--no-latency", action="store_true", help="skip the latency / config-2 / config-4 legs")
+    ap.add_argument("--no-vendor", action="store_true", help="skip the torch.fft (rocFFT) comparison column")
     ap.add_argument("--sizes", default="", help="comma-separated subset of N (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -243,15 +247,39 @@ def main() -> int:
         p50 = statistics.median(wall)
         return {"n": n, "batch": b, "executed": plan.executed, "api_wall_p50_ms": round(p50, 5),
                 "kernel_event_p50_ms": round(ev, 5),
-                "api_gbps": round(16 * n * b / (p50 * 1e-3) / 1e9, 3)}
+                "api_gbps": round(16 * n * b / (p50 * 1e-3) / 1e9, 3),
+                "kernel_gbps": round(16 * n * b / (ev * 1e-3) / 1e9, 1)}
 
-    lat, cfg2 = None, []
+    lat, cfg2, cfg4 = None, [], []
     if not args.no_latency:
         lat = latency(2048, 1)
         log(f"latency N=2048 B=1: {lat}")
         cfg2 = [latency(n, b) for n in (1024, 2048) for b in (16, 64)]
         for c in cfg2:
             log(f"config2: {c}")
+        cfg4 = [latency(1 << 20, 1), latency(1 << 16, 256)]
+        for c in cfg4:
+            log(f"config4: {c}")
+
+    # ---- vendor comparison column: rocFFT through torch.fft on the same inputs
+    if not args.no_vendor:
+        for (n, b, x, plan), row in zip(work, per_size):
+            for _ in range(3):
+                torch.fft.fft(x, dim=-1)
+            evs = []
+            for _ in range(10):
+                s = torch.cuda.Event(enable_timing=True)
+                e = torch.cuda.Event(enable_timing=True)
+                s.record(stream)
+                torch.fft.fft(x, dim=-1)
+                e.record(stream)
+                evs.append((s, e))
+            torch.cuda.synchronize()
+            vms = statistics.median(s.elapsed_time(e) for s, e in evs)
+            row["vendor_ms"] = round(vms, 5)
+            row["vendor_gbps"] = round(16 * n * b / (vms * 1e-3) / 1e9, 1)
+            log(f"N={n:>8} B={b:>6} torch.fft (rocFFT) {vms:8.4f} ms {row['vendor_gbps']:8.1f} GB/s "
+                f"(this library {row['ms']:.4f} ms)")
 
     # ---- CPU baseline (reference CPU path, 1 core, bounded sample)
     cpu = None
@@ -260,19 +288,26 @@ def main() -> int:
         import oracle  # the reference CPU path / its restatement, timed as the baseline
 
         rng = np.random.default_rng(7)
-        tot_s, tot_bytes, kinds = 0.0, 0, set()
+        rows = 16  # per size: a batch of 16 transforms of each N
+        threads = max(1, min(16, os.cpu_count() or 1))
+        tot_s, tot_mt, tot_bytes, kinds = 0.0, 0.0, 0, set()
         for n in SIZES:
-            h = rng.standard_normal(n) + 1j * rng.standard_normal(n)  # one row of each size
+            h = rng.standard_normal((rows, n)) + 1j * rng.standard_normal((rows, n))
             s, kind = oracle.time_cpu_fft(h, threads=1, reps=3)
             kinds.add(kind)
             tot_s += s
-            tot_bytes += 16 * n
+            s_mt, kind_mt = oracle.time_cpu_fft(h, threads=threads, reps=3)
+            kinds.add(kind_mt)
+            tot_mt += s_mt
+            tot_bytes += 16 * n * rows
         cpu = {"value": round(tot_bytes / tot_s / 1e9, 4), "unit": "GB/s", "cores": 1,
                "kind": "reference" if kinds == {"reference"} else "port",
-               "sample": "one transform of each N = 2^10..2^20 (11 transforms, complex<double>, "
-                         "butterfly::fft_dit with its per-stage twiddle rebuild), median of 3, "
-                         f"{tot_s:.2f} s per pass; host has {os.cpu_count()} CPUs",
-               "gpu_over_cpu": round(value / (tot_bytes / tot_s / 1e9), 1)}
+               "sample": f"{rows} transforms of each N = 2^10..2^20 (complex<double>, butterfly::fft_dit "
+                         f"with its per-stage twiddle rebuild), median of 3 passes, {tot_s:.1f} s per pass",
+               "gpu_over_cpu": round(value / (tot_bytes / tot_s / 1e9), 1),
+               "all_cores": {"value": round(tot_bytes / tot_mt / 1e9, 4), "cores": threads,
+                             "sample": f"the same rows split over {threads} std::threads "
+                                       f"(host reports {os.cpu_count()} CPUs), {tot_mt:.2f} s per pass"}}
         log(f"cpu baseline: {cpu}")
 
     line = {
@@ -291,6 +326,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "latency_n2048_b1": lat,
         "config2": cfg2,
+        "config4": cfg4,
         "per_size": per_size,
     }
     print(json.dumps(line), flush=True)

@@ -47,6 +47,13 @@ __device__ __forceinline__ int pad_add(int pi, int i) {
     if constexpr (K % 16 == 0) return pi + K + K / 16;
     else return pad(i + K);
 }
+// the same with one slot per 32 elements (split exchange)
+__device__ __forceinline__ int pad32(int i) { return i + (i >> 5); }
+template <int K>
+__device__ __forceinline__ int pad32_add(int pi, int i) {
+    if constexpr (K % 32 == 0) return pi + K + K / 32;
+    else return pad32(i + K);
+}
 
 // p + bytes for a wave-uniform p and a 32-bit lane offset: the address then
 // takes the scalar-base + 32-bit vector-offset form (one VGPR per access, no
@@ -94,10 +101,13 @@ struct ColCfg {
     static constexpr int NS_LAST = L / R_LAST;
     static constexpr int TW_SIZE = sched_tw_size(LOGL, LOGE);  // pass twiddle table entries
     // 32 elements per thread exchange real and imaginary parts separately
-    // through a float array (half the LDS of a float2 exchange).  Its column
-    // pitch, in floats, is == 64/C (mod 64) for the same bank tiling.
+    // through a float array (half the LDS of a float2 exchange), padded one
+    // slot per 32 elements (pad32: the stride-32 writes of a radix-32 pass
+    // then fall 33 floats apart).  Its column pitch, in floats, is == 64/C
+    // (mod 64) for the same bank tiling.
     static constexpr bool SPLIT = LOGE == 5;
-    static constexpr int PITCHF = PITCH0 + ((64 / C - PITCH0 % 64) + 64) % 64;
+    static constexpr int PITCH0F = L + (L >> 5);
+    static constexpr int PITCHF = PITCH0F + ((64 / C - PITCH0F % 64) + 64) % 64;
     // LDS floats: the exchange, and the float2 staging of the transposed
     // store (all C columns at once, or C/2 at a time when split)
     static constexpr int XCH_FLOATS = SPLIT ? C * PITCHF : 2 * C * PITCH;
@@ -214,7 +224,7 @@ __device__ __forceinline__ void col_passes(float2 (&v)[C::E], float2* lds, const
         constexpr int NB = E / R;
         constexpr int LNS = C::lns(p);
         constexpr int NS = 1 << LNS;
-        const int pj = pad(j);
+        const int pj = pad(j), pj32 = pad32(j);
         if constexpr (p > 0 && !C::SPLIT) {
             static_for<0, NB>([&](auto m) {
                 static_for<0, R>([&](auto q) {
@@ -254,16 +264,16 @@ __device__ __forceinline__ void col_passes(float2 (&v)[C::E], float2* lds, const
                 static_for<0, NB>([&](auto m) {
                     const int b = j + m.value * T;
                     const int base_o = ((b >> LNS) << (LNS + LR)) + (b & (NS - 1));
-                    const int pb = pad(base_o);
+                    const int pb = pad32(base_o);
                     static_for<0, R>([&](auto q) {
                         const float2 x = v[m.value * R + q.value];
-                        ltf[pad_add<q.value * NS>(pb, base_o)] = comp.value == 0 ? x.x : x.y;
+                        ltf[pad32_add<q.value * NS>(pb, base_o)] = comp.value == 0 ? x.x : x.y;
                     });
                 });
                 __syncthreads();
                 static_for<0, NB1>([&](auto m) {
                     static_for<0, R1>([&](auto q) {
-                        const float x = ltf[pad_add<m.value * T + q.value * (L / R1)>(pj, j)];
+                        const float x = ltf[pad32_add<m.value * T + q.value * (L / R1)>(pj32, j)];
                         if constexpr (comp.value == 0) v[m.value * R1 + q.value].x = x;
                         else v[m.value * R1 + q.value].y = x;
                     });

@@ -44,7 +44,12 @@ struct LdsCfg {
     static constexpr int WG = T >= 256 ? T : 256;          // threads per block
     static constexpr int TPB = WG / T;                     // transforms per block
     static constexpr int P = sched_passes(LOGL, LE);       // passes
-    static constexpr int PITCH = L + (L >> 4) + 1;
+    // Exchange padding: one slot per 16 elements in float2 rows (pad; a
+    // half-wave's stride-16 writes then tile the 64 banks), one per 32 in the
+    // split exchange's float rows (pad32), so the stride-32 writes of a
+    // radix-32 pass land 33 floats apart, one bank each, and the two 32-lane
+    // transforms of a wave sit half a bank row apart (1056 == 32 mod 64).
+    static constexpr int PITCH = LE == 5 ? L + (L >> 5) : L + (L >> 4) + 1;
     // 32 elements per thread exchange real and imaginary parts separately
     // through a float array: half the LDS, twice the barriers.
     static constexpr bool SPLIT = LE == 5;
@@ -66,6 +71,13 @@ template <int K>
 __device__ __forceinline__ int pad_add(int pi, int i) {
     if constexpr (K % 16 == 0) return pi + K + K / 16;
     else return pad(i + K);
+}
+// the same with one slot per 32 elements (split exchange)
+__device__ __forceinline__ int pad32(int i) { return i + (i >> 5); }
+template <int K>
+__device__ __forceinline__ int pad32_add(int pi, int i) {
+    if constexpr (K % 32 == 0) return pi + K + K / 32;
+    else return pad32(i + K);
 }
 
 template <int LOGL, int LOGE, int DIR, int MODE>
@@ -135,7 +147,7 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG), (LdsCfg<LOGL, LOGE>::MIN_
         constexpr int NB = E / R;
         constexpr int LNS = C::lns(p);
         constexpr int NS = 1 << LNS;
-        const int pj = pad(j);
+        const int pj = pad(j), pj32 = pad32(j);
         if constexpr (p > 0 && !C::SPLIT) {
             static_for<0, NB>([&](auto m) {
                 static_for<0, R>([&](auto q) {
@@ -174,16 +186,16 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG), (LdsCfg<LOGL, LOGE>::MIN_
                 static_for<0, NB>([&](auto m) {
                     const int b = j + m.value * T;
                     const int base = ((b >> LNS) << (LNS + LR)) + (b & (NS - 1));
-                    const int pb = pad(base);
+                    const int pb = pad32(base);
                     static_for<0, R>([&](auto q) {
                         const float2 x = v[m.value * R + q.value];
-                        ltf[pad_add<q.value * NS>(pb, base)] = comp.value == 0 ? x.x : x.y;
+                        ltf[pad32_add<q.value * NS>(pb, base)] = comp.value == 0 ? x.x : x.y;
                     });
                 });
                 __syncthreads();
                 static_for<0, NB1>([&](auto m) {
                     static_for<0, R1>([&](auto q) {
-                        const float x = ltf[pad_add<m.value * T + q.value * (L / R1)>(pj, j)];
+                        const float x = ltf[pad32_add<m.value * T + q.value * (L / R1)>(pj32, j)];
                         if constexpr (comp.value == 0) v[m.value * R1 + q.value].x = x;
                         else v[m.value * R1 + q.value].y = x;
                     });

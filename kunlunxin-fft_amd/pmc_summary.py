@@ -74,6 +74,9 @@ def per_kernel(d: str, counter: str):
     return {k: sum(v) / len(v) for k, v in acc.items()}
 
 
+SQ_COUNTERS = ("SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_INSTS_LDS", "SQ_INSTS_VALU")
+
+
 def calibration(vals: dict) -> float:
     """Counter KiB per KiB actually moved, from the largest copy dispatch."""
     cands = [(g, v) for (n, g), v in vals.items() if n.startswith(COPY_KERNEL)]
@@ -121,6 +124,7 @@ def main() -> int:
     t.add_argument("--json", required=True)
     t.add_argument("--md", required=True)
     t.add_argument("--command", default="", help="commands that made the input, quoted in the Markdown")
+    t.add_argument("--sq", default="", help="output dir of an SQ counter run (" + " ".join(SQ_COUNTERS) + ")")
     st = sub.add_parser("stats")
     st.add_argument("--dir", required=True, help="output dir of the --kernel-trace --stats run")
     st.add_argument("--md", required=True)
@@ -132,6 +136,7 @@ def main() -> int:
     fetch = per_kernel(args.fetch, "FETCH_SIZE")
     write = per_kernel(args.write, "WRITE_SIZE")
     f_cal, w_cal = calibration(fetch), calibration(write)
+    sq = {c: per_kernel(args.sq, c) for c in SQ_COUNTERS} if args.sq else {}
     sizes = json.load(open(args.detail))["per_size"]
 
     rows_out, traffic = [], {}
@@ -172,11 +177,21 @@ def main() -> int:
                 f"{f_cal * 256:.2f} MiB and WRITE_SIZE = {w_cal * 256:.2f} MiB, so FETCH_SIZE is scaled "
                 f"by {1 / f_cal:.3f} and WRITE_SIZE by {1 / w_cal:.3f}.  Algorithmic bytes = 16 per point "
                 f"(one complex64 read + one written).\n\n")
-        f.write("| bench kernel key | kernel | grid | algorithmic MiB | fetch MiB | write MiB | traffic / algorithmic |\n")
-        f.write("|---|---|---:|---:|---:|---:|---:|\n")
+        if sq:
+            f.write("SQ columns (a third run): LDS bank-conflict cycles per LDS-active cycle "
+                    "(SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE) and LDS per VALU instructions.\n\n")
+        f.write("| bench kernel key | kernel | grid | algorithmic MiB | fetch MiB | write MiB | traffic / algorithmic |"
+                + (" LDS conflict / active | LDS / VALU insts |" if sq else "") + "\n")
+        f.write("|---|---|---:|---:|---:|---:|---:|" + ("---:|---:|" if sq else "") + "\n")
         for key, name, grid, alg, fb, wb in rows_out:
+            extra = ""
+            if sq:
+                g = lambda c: sq[c].get((name, grid))  # noqa: E731
+                bc, act, li, vi = (g(c) for c in SQ_COUNTERS)
+                extra = (f" {bc / act:.3f} |" if bc is not None and act else " - |") + \
+                        (f" {li / vi:.3f} |" if li is not None and vi else " - |")
             f.write(f"| {key} | {name} | {grid} | {alg / 2**20:.1f} | {fb / 2**20:.1f} | {wb / 2**20:.1f} | "
-                    f"{(fb + wb) / alg:.3f} |\n")
+                    f"{(fb + wb) / alg:.3f} |{extra}\n")
     print(f"wrote {args.json} ({len(traffic)} kernels) and {args.md}")
     return 0
 

@@ -88,6 +88,10 @@ def reference_lib():
         lib.ref_time_fft_batch.argtypes = [dp, ctypes.c_int64, ctypes.c_int64,
                                            ctypes.c_int, ctypes.c_int]
         lib.ref_time_fft_batch.restype = ctypes.c_double
+        if hasattr(lib, "ref_time_fft_batch_mt"):
+            lib.ref_time_fft_batch_mt.argtypes = [dp, ctypes.c_int64, ctypes.c_int64,
+                                                  ctypes.c_int, ctypes.c_int, ctypes.c_int]
+            lib.ref_time_fft_batch_mt.restype = ctypes.c_double
         lib.ref_bit_reverse.argtypes = [ctypes.c_uint, ctypes.c_int]
         lib.ref_bit_reverse.restype = ctypes.c_uint
         _ref = lib
@@ -318,7 +322,9 @@ def time_cpu_fft(x, threads: int = 1, reps: int = 5, use_reference: bool = True)
     else the C restatement) over the rows of ``x``; returns (seconds, kind)."""
     a, _ = _rows(x)
     n, b = a.shape[-1], a.shape[0]
-    lib = reference_lib() if (use_reference and threads <= 1) else None
-    if lib is not None:
+    lib = reference_lib() if use_reference else None
+    if lib is not None and threads <= 1:
         return float(lib.ref_time_fft_batch(_dptr(a), n, b, 0, reps)), "reference"
+    if lib is not None and hasattr(lib, "ref_time_fft_batch_mt"):
+        return float(lib.ref_time_fft_batch_mt(_dptr(a), n, b, 0, reps, threads)), "reference"
     return float(_load().oracle_time_fft_batch(_dptr(a), n, b, 0, threads, reps)), "port"

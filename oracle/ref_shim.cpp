@@ -5,11 +5,12 @@
 // restatement with the reference code itself, and lets bench.py time the
 // reference CPU path (cpu_baseline kind "reference").  No reference source is
 // copied here; this file only calls butterfly::fft_dit / fft_dif.
+#include <algorithm>
 #include <chrono>
 #include <complex>
 #include <cstdint>
+#include <thread>
 #include <vector>
-#include <algorithm>
 
 #include "butterfly/fft.hpp"
 
@@ -39,6 +40,31 @@ double ref_time_fft_batch(const double* a, int64_t n, int64_t batch, int dif, in
         std::copy(a, a + 2 * n * batch, work.begin());
         auto s0 = std::chrono::steady_clock::now();
         ref_fft_batch(work.data(), n, batch, dif);
+        auto s1 = std::chrono::steady_clock::now();
+        t.push_back(std::chrono::duration<double>(s1 - s0).count());
+    }
+    std::sort(t.begin(), t.end());
+    return t[t.size() / 2];
+}
+
+// As ref_time_fft_batch, with the rows split into `threads` contiguous
+// ranges, one std::thread each (the reference path is single-threaded per
+// transform; this is the all-cores figure of the same work).
+double ref_time_fft_batch_mt(const double* a, int64_t n, int64_t batch, int dif, int reps, int threads) {
+    if (reps < 1) reps = 1;
+    if (threads < 1) threads = 1;
+    if (threads > batch) threads = static_cast<int>(batch);
+    std::vector<double> work(static_cast<std::size_t>(2 * n * batch));
+    std::vector<double> t;
+    for (int r = 0; r < reps; ++r) {
+        std::copy(a, a + 2 * n * batch, work.begin());
+        auto s0 = std::chrono::steady_clock::now();
+        std::vector<std::thread> pool;
+        for (int k = 0; k < threads; ++k) {
+            const int64_t r0 = batch * k / threads, r1 = batch * (k + 1) / threads;
+            pool.emplace_back([&, r0, r1] { ref_fft_batch(work.data() + 2 * r0 * n, n, r1 - r0, dif); });
+        }
+        for (auto& th : pool) th.join();
         auto s1 = std::chrono::steady_clock::now();
         t.push_back(std::chrono::duration<double>(s1 - s0).count());
     }
