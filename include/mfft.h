@@ -91,7 +91,12 @@ enum {
  *                                    workgroup; 1 = persistent workgroups (one
  *                                    resident wave of them) that load their
  *                                    next column group while transforming the
- *                                    current one */
+ *                                    current one; 2 = fused: both passes in
+ *                                    one launch, each transform's pass 2 on
+ *                                    the XCD whose L2 holds its pass-1 output
+ *                                    (n1, n2 in [128, 512] within 2x; one
+ *                                    execute of such a plan at a time: its
+ *                                    counters live in the plan) */
 #define MFFT_MAX_PARAMS 4
 
 typedef struct mfft_plan mfft_plan;
@@ -153,6 +158,13 @@ int mfft_plan_destroy(mfft_plan* plan);
 
 /* Describe a plan (resolved flow, launch count, memory held). */
 int mfft_plan_query(const mfft_plan* plan, mfft_plan_info* info);
+
+/* FOUR_STEP schedule 2 only (no counterpart in the reference: a diagnostic of
+ * this library's fused schedule): how many pass-2 waits of this plan's
+ * launches so far gave up at their poll limit instead of seeing pass 1
+ * complete -- 0 unless something is wrong.  Copies one int from the device
+ * (synchronous); *count = 0 for plans of any other flow. */
+int mfft_plan_sync_overruns(const mfft_plan* plan, int64_t* count);
 
 /* out[r][bit_reverse(i)] = in[r][i] over `batch` rows of n complex64
  * (runner.bit_reverse_permute, runner.py:1542-1552); n a power of two. */

@@ -108,7 +108,7 @@ class DesignSpace:
     fourstep_n1: tuple
     fourstep_chunk_rows: tuple
     fourstep_min_n: int
-    fourstep_persistent: tuple
+    fourstep_schedule: tuple
     batch_candidates: tuple
     batch_variants: tuple
     layout_in: str
@@ -132,9 +132,9 @@ class DesignSpace:
         _require(isinstance(ch, list) and ch and all(isinstance(c, int) and c >= 0 for c in ch),
                  "butterfly_space.json: P.four_step.chunk_rows must be non-negative ints")
         _require(isinstance(fs.get("min_n"), int) and fs["min_n"] > 0, "butterfly_space.json: P.four_step.min_n required")
-        pers = fs.get("persistent", [0])
-        _require(isinstance(pers, list) and pers and all(v in (0, 1) for v in pers),
-                 "butterfly_space.json: P.four_step.persistent must be a list of 0/1")
+        sched = fs.get("schedule", [0])
+        _require(isinstance(sched, list) and sched and all(v in (0, 1, 2) for v in sched),
+                 "butterfly_space.json: P.four_step.schedule must be a list of 0/1/2")
         b = p.get("batch_expansion", {})
         _require(_pow2_list(b.get("candidates")), "butterfly_space.json: P.batch_expansion.candidates must be powers of two")
         variants = b.get("variants", [])
@@ -147,7 +147,7 @@ class DesignSpace:
             space_id=d["space_id"], target=d["target"], radix=tuple(p["radix"]),
             stage_blocks=tuple(st["blocks"]), lds_elems=tuple(lds["elems"]), lds_max_n=lds["max_n"],
             fourstep_n1=tuple(fs["n1"]), fourstep_chunk_rows=tuple(ch), fourstep_min_n=fs["min_n"],
-            fourstep_persistent=tuple(pers),
+            fourstep_schedule=tuple(sched),
             batch_candidates=tuple(b["candidates"]), batch_variants=tuple(variants),
             layout_in=lay["in"][0], layout_out=lay["out"][0],
         )

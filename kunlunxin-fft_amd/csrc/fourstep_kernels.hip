@@ -417,6 +417,109 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG), 4) void fourstep_pe
     process(t);
 }
 
+// Fused schedule: both passes in one launch, each transform's pass 2 reading
+// pass 1's output Z while it is still in the L2 of the XCD that wrote it.
+// Every block reads the XCD it runs on (hardware register XCC_ID) and takes
+// work only for the transforms t == xcd (mod 8) of the launch, from that
+// XCD's queue: pass-1 groups of transform k, then pass-2 groups of transform
+// k-1, and so on.  A pass-2 group first waits until all pass-1 groups of its
+// transform have stored Z.  Every pass-1 group is handed out before any
+// pass-2 group of the same transform and never waits, so the wait always
+// ends; it is nevertheless bounded by `wait_ticks` of the constant-rate wall
+// clock, and counted in sync[8] when exceeded.  Producer and consumer share
+// one L2 and the consumer's L1 has never held these lines (each group's rows
+// are whole 128-byte lines of its own), so completed stores plus a counter
+// in L2 are the whole handshake: no cache write-back or invalidation.  Both
+// sides touch the counter with read-modify-write atomics, which execute
+// where the producer's increments live; an atomic load would be issued
+// system-coherent and read memory behind the L2, never seeing them.
+// sync (int32, zeroed before the launch): [0, 8) next item per XCD, [8]
+// overruns, [9, 9 + rows) pass-1 groups done per transform.
+template <int LL1, int LE1, int LC1, int LL2, int LE2, int LC2, int DIR>
+__global__ __launch_bounds__((ColCfg<LL1, LE1, LC1>::WG)) void fourstep_fused_kernel(
+    const float2* src, float2* dst, const float2* __restrict__ tw1, const float2* __restrict__ tw2,
+    const float2* __restrict__ tw_lo, const float2* __restrict__ tw_hi, int tw_h, float scale, int rows,
+    int* sync, long long wait_ticks) {
+    using A = ColCfg<LL1, LE1, LC1>;
+    using B = ColCfg<LL2, LE2, LC2>;
+    static_assert(A::WG == B::WG, "both passes run with the same block size");
+    constexpr int LDS_N = A::LDS_FLOAT2 > B::LDS_FLOAT2 ? A::LDS_FLOAT2 : B::LDS_FLOAT2;
+    __shared__ float2 lds[LDS_N];
+    __shared__ int item_s;
+    constexpr int LOGN = LL1 + LL2;
+    constexpr int G1 = (1 << LL2) >> LC1;  // pass-1 column groups per transform (columns n2)
+    constexpr int G2 = (1 << LL1) >> LC2;  // pass-2 column groups per transform (columns k1)
+    const int tid = threadIdx.x;
+    // HW_REG_XCC_ID (hwreg 20), bits [3:0]
+    const int xcd = (int)__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 7;
+    const int nt = rows > xcd ? (rows - xcd + 7) / 8 : 0;  // this XCD's transforms: t = xcd + 8k
+    const int total = nt * (G1 + G2);
+    int* done = sync + 9;
+    for (;;) {
+        if (tid == 0) item_s = atomicAdd(sync + xcd, 1);
+        __syncthreads();
+        const int it = item_s;
+        __syncthreads();  // every thread has read item_s before it is written again
+        if (it >= total) break;
+        // queue order: P1(0) | P1(1) P2(0) | P1(2) P2(1) | ... | P2(nt-1)
+        int k, g;
+        bool second;
+        if (it < G1) {
+            k = 0, g = it, second = false;
+        } else {
+            const int u = it - G1, blk = u / (G1 + G2), r = u - blk * (G1 + G2);
+            if (blk < nt - 1 && r < G1) k = blk + 1, g = r, second = false;
+            else k = blk, g = blk < nt - 1 ? r - G1 : r, second = true;
+        }
+        const int t = xcd + 8 * k;
+        const int64_t base = (int64_t)t << LOGN;
+        // the lane index, hidden from the optimizer per item, so lane
+        // addresses are recomputed per item instead of held across the loop
+        const int tl = opaque(tid);
+        if (!second) {
+            const int c = tl & (A::C - 1), j = tl >> LC1, c0 = g << LC1;
+            float2 v[A::E];
+            col_load<A>(v, src + base + c0, c, j, LL2);
+            col_passes<A, DIR, 0, true>(v, lds, tw1, c, j, [&] {
+                BigTw<A> f;
+                big_tw_load<A>(f, tw_lo, tw_hi, tw_h, (uint32_t)(c0 + c), j);
+                return f;
+            });
+            col_store<A, 0>(v, dst + base + ((int64_t)c0 << LL1), lds, tl, c, j, LL2, 1.0f);
+            __builtin_amdgcn_s_waitcnt(0);  // this thread's Z stores have reached L2
+            __syncthreads();
+            if (tid == 0) atomicAdd(done + t, 1);
+        } else {
+            if (tid == 0) {
+                // an add of an opaque zero: a literal 0 would be turned into
+                // an (L2-bypassing) atomic load by the compiler
+                const int zero = opaque(0);
+                const long long t_start = wall_clock64();
+                while (atomicAdd(done + t, zero) < G1) {
+                    if (wall_clock64() - t_start > wait_ticks) {
+                        atomicAdd(sync + 8, 1);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+            }
+            __syncthreads();
+            const int c = tl & (B::C - 1), j = tl >> LC2, c0 = g << LC2;
+            float2 v[B::E];
+            col_load<B>(v, dst + base + c0, c, j, LL1);
+            col_passes<B, DIR, 1, true>(v, lds, tw2, c, j, [&] { return BigTw<B>{}; });
+            col_store<B, 1>(v, dst + base + c0, lds, tl, c, j, LL1, scale);
+        }
+    }
+}
+
+// clears a fused launch's counters: sync[0, 8) and sync[9, n); sync[8]
+// (wait overruns) accumulates over the plan's launches
+__global__ void zero_sync(int* sync, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n && i != 8) sync[i] = 0;
+}
+
 // Blocks of the persistent kernel one CU holds at once (occupancy query,
 // made once per kernel).
 template <int LOGL, int LOGE, int LOGC, int DIR, int KIND>
@@ -443,7 +546,7 @@ hipError_t launch_pass(const float2* src, float2* dst, const mfft_plan* p, int64
     const int64_t groups = ((int64_t)1 << log_s) >> LOGC;
     const int64_t tiles = rows * groups;
     const float2* tw = KIND == 0 ? p->tw_n1 : p->tw_n2;
-    if (p->persistent) {
+    if (p->schedule == 1) {
         // a multiple of the column groups (fixed c0 per block) and of 16
         // (whole XCD-pairing groups), at most one resident wave of blocks
         const int64_t unit = groups > 16 ? groups : 16;
@@ -489,6 +592,53 @@ void fourstep_default_split(int log2n, int* log2n1, int* log2n2) {
     *log2n2 = log2n - *log2n1;
 }
 
+namespace {
+
+template <int L1, int L2, int DIR>
+hipError_t launch_fused_one(const float2* src, float2* dst, const mfft_plan* p, int64_t rows, float scale,
+                            hipStream_t stream) {
+    constexpr int E1 = col_loge(L1), C1 = col_logc(L1), E2 = col_loge(L2), C2 = col_logc(L2);
+    using A = ColCfg<L1, E1, C1>;
+    const int nsync = 9 + (int)rows;
+    zero_sync<<<(nsync + 255) / 256, 256, 0, stream>>>(p->sync, nsync);
+    mark(stream);
+    static const int per_cu = [] {
+        int b = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fourstep_fused_kernel<L1, E1, C1, L2, E2, C2, DIR>,
+                                                         A::WG, 0) != hipSuccess) {
+            (void)hipGetLastError();
+            b = 1;
+        }
+        return b > 0 ? b : 1;
+    }();
+    // one resident wave of blocks, a multiple of the 8 XCDs
+    const int grid = ((per_cu * p->num_cus) / 8) * 8 > 0 ? ((per_cu * p->num_cus) / 8) * 8 : 8;
+    fourstep_fused_kernel<L1, E1, C1, L2, E2, C2, DIR><<<grid, A::WG, 0, stream>>>(
+        src, dst, p->tw_n1, p->tw_n2, p->tw_lo, p->tw_hi, p->tw_h, scale, (int)rows, p->sync,
+        (long long)kFusedWaitMs * p->clock_khz);
+    mark(stream);
+    return hipGetLastError();
+}
+
+hipError_t launch_fused(int dir, const float2* src, float2* dst, const mfft_plan* p, int64_t rows, float scale,
+                        hipStream_t stream) {
+    const int l1 = ilog2((int)p->n1), l2 = ilog2((int)p->n2);
+#define MFFT_FUSED_CASE(A, B)                                                                  \
+    if (l1 == A && l2 == B)                                                                    \
+        return dir < 0 ? launch_fused_one<A, B, -1>(src, dst, p, rows, scale, stream)          \
+                       : launch_fused_one<A, B, 1>(src, dst, p, rows, scale, stream);
+    MFFT_FUSED_CASE(7, 7) MFFT_FUSED_CASE(7, 8) MFFT_FUSED_CASE(8, 7) MFFT_FUSED_CASE(8, 8)
+    MFFT_FUSED_CASE(8, 9) MFFT_FUSED_CASE(9, 8) MFFT_FUSED_CASE(9, 9)
+#undef MFFT_FUSED_CASE
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool fourstep_fused_supported(int l1, int l2) {
+    return l1 >= 7 && l1 <= 9 && l2 >= 7 && l2 <= 9 && l1 - l2 <= 1 && l2 - l1 <= 1;
+}
+
 hipError_t launch_fourstep(int dir, const float2* src, float2* dst, const mfft_plan* p, int64_t rows,
                            float scale, hipStream_t stream, int* launches) {
     const int l1 = ilog2((int)p->n1), l2 = ilog2((int)p->n2);
@@ -500,6 +650,12 @@ hipError_t launch_fourstep(int dir, const float2* src, float2* dst, const mfft_p
         const float2* s = src + r0 * n;
         float2* d = dst + r0 * n;
         hipError_t e;
+        if (p->schedule == 2) {
+            e = launch_fused(dir, s, d, p, rc, scale, stream);
+            if (e != hipSuccess) return e;
+            count += 2;
+            continue;
+        }
         e = dir < 0 ? dispatch_len<-1, 0>(l1, s, d, p, rc, l2, 1.0f, stream)
                     : dispatch_len<1, 0>(l1, s, d, p, rc, l2, 1.0f, stream);
         if (e != hipSuccess) return e;

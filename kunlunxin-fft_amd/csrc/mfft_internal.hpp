@@ -19,8 +19,9 @@ struct mfft_plan {
     int elems = 16;      // LDS_FUSED: elements per thread
     int launches = 0;
     int64_t n1 = 0, n2 = 0, chunk_rows = 0;
-    int persistent = 0;  // FOUR_STEP: persistent blocks that prefetch their next column group
-    int num_cus = 0;     // compute units of `device` (persistent grid size)
+    int schedule = 0;    // FOUR_STEP: 0 one column group per block, 1 persistent, 2 fused (one launch)
+    int num_cus = 0;     // compute units of `device` (persistent / fused grid size)
+    int clock_khz = 0;   // constant wall-clock rate of `device` (fused schedule wait bound)
     bool r2c_fused = false, c2r_fused = false;
 
     // device memory owned by the plan
@@ -33,6 +34,7 @@ struct mfft_plan {
     float2* tw_real = nullptr;  // exp(-2*pi*i*k/n), k in [0, n/2]  (r2c stitch / c2r pre)
     float2* ws_a = nullptr;     // core-sized scratch (real flows: core output / input)
     float2* ws_b = nullptr;     // core-sized scratch (stage-flow ping-pong)
+    int* sync = nullptr;        // fused four-step: [0,8) work counters, [8] wait overruns, then one per row
     int64_t ws_bytes = 0, table_bytes = 0;
 };
 
@@ -87,6 +89,9 @@ hipError_t launch_lds(int mode, int dir, int log2l, int elems, const void* src, 
 
 // ---- fourstep_kernels.hip: two-pass column/row FFT -----------------------
 bool fourstep_supported(int log2n1, int log2n2);
+bool fourstep_fused_supported(int log2n1, int log2n2);  // schedule 2: n1, n2 in [128, 512], within 2x
+constexpr int kFusedWaitMs = 20;  // longest pass-2 wait of the fused schedule before it gives up
+constexpr bool kFusedScheduleEnabled = false;  // fused schedule switched off (it did not finish on the GPU)
 int fourstep_col_loge(int logl);  // log2 elements per thread of a pass of length 2^logl
 void fourstep_default_split(int log2n, int* log2n1, int* log2n2);
 hipError_t launch_fourstep(int dir, const float2* src, float2* dst, const mfft_plan* p,

@@ -37,7 +37,7 @@ MAX_PARAMS = 4
 EXPORTS = (
     "mfft_plan_create", "mfft_execute", "mfft_execute_timed", "mfft_plan_destroy", "mfft_plan_query",
     "mfft_bit_reverse_permute", "mfft_device_props_get", "mfft_last_error",
-    "mfft_abi_version",
+    "mfft_abi_version", "mfft_plan_sync_overruns",
 )
 
 
@@ -101,6 +101,8 @@ def load() -> ctypes.CDLL:
         lib.mfft_plan_destroy.restype = i32
         lib.mfft_plan_query.argtypes = [vp, ctypes.POINTER(PlanInfo)]
         lib.mfft_plan_query.restype = i32
+        lib.mfft_plan_sync_overruns.argtypes = [vp, ctypes.POINTER(ctypes.c_int64)]
+        lib.mfft_plan_sync_overruns.restype = i32
         lib.mfft_bit_reverse_permute.argtypes = [vp, vp, i64, i64, vp]
         lib.mfft_bit_reverse_permute.restype = i32
         lib.mfft_device_props_get.argtypes = [i32, ctypes.POINTER(DeviceProps)]
@@ -166,6 +168,13 @@ class NativePlan:
         check(_lib.mfft_execute_timed(self._h, ctypes.c_void_p(in_ptr), ctypes.c_void_p(out_ptr),
                                       ctypes.c_void_p(stream_ptr), ms, cap, ctypes.byref(k)))
         return [float(ms[i]) for i in range(k.value)]
+
+    def sync_overruns(self) -> int:
+        """Fused four-step schedule: pass-2 waits that hit their poll limit
+        over this plan's launches so far (0 unless something is wrong)."""
+        k = ctypes.c_int64(0)
+        check(_lib.mfft_plan_sync_overruns(self._h, ctypes.byref(k)))
+        return int(k.value)
 
     @property
     def flow_name(self) -> str:

@@ -12,7 +12,7 @@ fft_dif, fft_dif_batch (runner.py:165, 839)  RADIX2_DIF (M0, bitrev fold)    blo
 fft_dit_radix4(_batch) (runner.py:1399,1112) RADIX4_DIT (M5, digit-rev fold) block
 fft_dif_radix4(_batch) (runner.py:1473,1193) RADIX4_DIF (M5)                 block
 fft_lds_fused(_batch)                        LDS_FUSED (single pass)         elems
-fft_four_step(_batch)                        FOUR_STEP (two passes)          n1, chunk_rows, persistent
+fft_four_step(_batch)                        FOUR_STEP (two passes)          n1, chunk_rows, schedule
 fft_dit_fused (runner.py:209)                LDS_FUSED / FOUR_STEP (auto)    --
 fft_{dit,dif}_matrix(_batch) (runner.py:379) LDS_FUSED / FOUR_STEP (auto)    --
 fft_{dit,dif}_grouped (runner.py:505)        LDS_FUSED / FOUR_STEP (auto)    --
@@ -100,7 +100,13 @@ def flow_params(executed: str, n: int, transform_type: str, block, params: dict)
             return native.FLOW_AUTO, ()
         if n1 and (core % n1 or not 16 <= core // n1 <= 1024 or not 16 <= n1 <= 1024):
             n1 = 0
-        return flow, (n1, int(params.get("chunk_rows", 0)), 1 if params.get("persistent", 0) else 0)
+        sched = int(params.get("schedule", 0))
+        if sched == 2:
+            l1 = (n1 or (1 << ((core.bit_length() - 1) // 2))).bit_length() - 1
+            l2 = core.bit_length() - 1 - l1
+            if not (7 <= l1 <= 9 and 7 <= l2 <= 9 and abs(l1 - l2) <= 1):
+                sched = 0  # a real flow's half-length core outside the fused range
+        return flow, (n1, int(params.get("chunk_rows", 0)), sched)
     if kind == "block":
         # a stage flow needs at least one stage (radix-4: one radix-4 stage);
         # shorter cores (N=1 c2c, N=2 real) run in the single-pass kernel
@@ -250,14 +256,14 @@ def fft_lds_fused_batch(x, elems: int = 0):
     return _batched("fft_lds_fused_batch", x, None, {"elems": elems})
 
 
-def fft_four_step(x, n1: int = 0, chunk_rows: int = 0, persistent: int = 0):
+def fft_four_step(x, n1: int = 0, chunk_rows: int = 0, schedule: int = 0):
     """Two-pass four-step FFT (column pass + twiddle, in-place row pass)."""
-    return _single("fft_four_step", x, None, {"n1": n1, "chunk_rows": chunk_rows, "persistent": persistent})
+    return _single("fft_four_step", x, None, {"n1": n1, "chunk_rows": chunk_rows, "schedule": schedule})
 
 
-def fft_four_step_batch(x, n1: int = 0, chunk_rows: int = 0, persistent: int = 0):
+def fft_four_step_batch(x, n1: int = 0, chunk_rows: int = 0, schedule: int = 0):
     return _batched("fft_four_step_batch", x, None,
-                    {"n1": n1, "chunk_rows": chunk_rows, "persistent": persistent})
+                    {"n1": n1, "chunk_rows": chunk_rows, "schedule": schedule})
 
 
 def fft_dit_fused(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64):

@@ -114,9 +114,9 @@ def entry_contract_violations(entry: dict) -> list[str]:
         ch = params.get("chunk_rows", 0)
         if ch not in sp.fourstep_chunk_rows:
             bad.append(f"chunk_rows {ch!r} not in {sp.fourstep_chunk_rows}")
-        pers = params.get("persistent", 0)
-        if pers not in sp.fourstep_persistent:
-            bad.append(f"persistent {pers!r} not in {sp.fourstep_persistent}")
+        sched = params.get("schedule", 0)
+        if sched not in sp.fourstep_schedule:
+            bad.append(f"schedule {sched!r} not in {sp.fourstep_schedule}")
         if isinstance(n, int) and n < sp.fourstep_min_n:
             bad.append(f"N={n} below the four-step minimum {sp.fourstep_min_n}")
     if "variant" in params and params["variant"] not in sp.batch_variants:
