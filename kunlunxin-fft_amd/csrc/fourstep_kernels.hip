@@ -458,7 +458,9 @@ __global__ __launch_bounds__((ColCfg<LL1, LE1, LC1>::WG)) void fourstep_fused_ke
     for (;;) {
         if (tid == 0) item_s = atomicAdd(sync + xcd, 1);
         __syncthreads();
-        const int it = item_s;
+        // block-uniform, and read into a scalar register so that every branch
+        // on it (around the barriers below) is a scalar branch
+        const int it = __builtin_amdgcn_readfirstlane(item_s);
         __syncthreads();  // every thread has read item_s before it is written again
         if (it >= total) break;
         // queue order: P1(0) | P1(1) P2(0) | P1(2) P2(1) | ... | P2(nt-1)
@@ -622,15 +624,21 @@ hipError_t launch_fused_one(const float2* src, float2* dst, const mfft_plan* p, 
 
 hipError_t launch_fused(int dir, const float2* src, float2* dst, const mfft_plan* p, int64_t rows, float scale,
                         hipStream_t stream) {
-    const int l1 = ilog2((int)p->n1), l2 = ilog2((int)p->n2);
+    if constexpr (!kFusedScheduleEnabled) {
+        // switched off (plan creation rejects schedule 2); not instantiated
+        (void)dir, (void)src, (void)dst, (void)p, (void)rows, (void)scale, (void)stream;
+        return hipErrorNotSupported;
+    } else {
+        const int l1 = ilog2((int)p->n1), l2 = ilog2((int)p->n2);
 #define MFFT_FUSED_CASE(A, B)                                                                  \
-    if (l1 == A && l2 == B)                                                                    \
-        return dir < 0 ? launch_fused_one<A, B, -1>(src, dst, p, rows, scale, stream)          \
-                       : launch_fused_one<A, B, 1>(src, dst, p, rows, scale, stream);
-    MFFT_FUSED_CASE(7, 7) MFFT_FUSED_CASE(7, 8) MFFT_FUSED_CASE(8, 7) MFFT_FUSED_CASE(8, 8)
-    MFFT_FUSED_CASE(8, 9) MFFT_FUSED_CASE(9, 8) MFFT_FUSED_CASE(9, 9)
+        if (l1 == A && l2 == B)                                                                \
+            return dir < 0 ? launch_fused_one<A, B, -1>(src, dst, p, rows, scale, stream)      \
+                           : launch_fused_one<A, B, 1>(src, dst, p, rows, scale, stream);
+        MFFT_FUSED_CASE(7, 7) MFFT_FUSED_CASE(7, 8) MFFT_FUSED_CASE(8, 7) MFFT_FUSED_CASE(8, 8)
+        MFFT_FUSED_CASE(8, 9) MFFT_FUSED_CASE(9, 8) MFFT_FUSED_CASE(9, 9)
 #undef MFFT_FUSED_CASE
-    return hipErrorInvalidValue;
+        return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace
