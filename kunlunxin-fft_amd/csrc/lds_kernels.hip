@@ -35,7 +35,11 @@
 namespace mfft {
 namespace {
 
-template <int LOGL, int LOGE>
+// Shortest transform whose 16-element exchange goes through LDS one
+// component at a time (split), halving its LDS so more blocks share a CU.
+constexpr int kSplit16MinLog = 13;
+
+template <int LOGL, int LOGE, int MODE = 0>
 struct LdsCfg {
     static constexpr int L = 1 << LOGL;
     static constexpr int LE = sched_le(LOGL, LOGE);  // log2 elements per thread
@@ -44,20 +48,23 @@ struct LdsCfg {
     static constexpr int WG = T >= 256 ? T : 256;          // threads per block
     static constexpr int TPB = WG / T;                     // transforms per block
     static constexpr int P = sched_passes(LOGL, LE);       // passes
-    // Exchange padding: one slot per 16 elements in float2 rows (pad; a
-    // half-wave's stride-16 writes then tile the 64 banks), one per 32 in the
-    // split exchange's float rows (pad32), so the stride-32 writes of a
-    // radix-32 pass land 33 floats apart, one bank each, and the two 32-lane
-    // transforms of a wave sit half a bank row apart (1056 == 32 mod 64).
+    // Real and imaginary parts exchanged separately through a float array:
+    // half the LDS, twice the barriers.  Always with 32 elements per thread;
+    // with 16 from kSplit16MinLog points (never for the r2c stitch, which
+    // reads whole complex values out of LDS).
+    static constexpr bool SPLIT = LE == 5 || (LE == 4 && LOGL >= kSplit16MinLog && MODE != 1);
+    // Exchange padding: one slot per 16 elements in float2 rows and in the
+    // split rows of 16-element threads (pad; a half-wave's stride-16 writes
+    // then tile the 64 banks), one per 32 in the split rows of 32-element
+    // threads (pad32), so the stride-32 writes of a radix-32 pass land 33
+    // floats apart, one bank each, and the two 32-lane transforms of a wave
+    // sit half a bank row apart (1056 == 32 mod 64).
+    static constexpr int FSH = LE == 5 ? 5 : 4;
     static constexpr int PITCH = LE == 5 ? L + (L >> 5) : L + (L >> 4) + 1;
-    // 32 elements per thread exchange real and imaginary parts separately
-    // through a float array: half the LDS, twice the barriers.
-    static constexpr bool SPLIT = LE == 5;
     static constexpr int LDS_FLOATS = TPB * PITCH * (SPLIT ? 1 : 2);
     // Waves per SIMD the register allocation must allow.  A split-exchange
     // block uses at most 70 KB of LDS, so up to 16 waves of it fit a CU when
-    // each wave stays within 128 VGPRs; left to itself the compiler takes up
-    // to 167 for 32 elements and the CU then holds one block fewer.
+    // each wave stays within 128 VGPRs.
     static constexpr int MIN_WAVES = SPLIT ? 4 : 1;
     static constexpr int logr(int p) { return sched_logr(LOGL, LE, p); }
     static constexpr int lns(int p) { return sched_lns(LE, p); }
@@ -72,19 +79,20 @@ __device__ __forceinline__ int pad_add(int pi, int i) {
     if constexpr (K % 16 == 0) return pi + K + K / 16;
     else return pad(i + K);
 }
-// the same with one slot per 32 elements (split exchange)
-__device__ __forceinline__ int pad32(int i) { return i + (i >> 5); }
-template <int K>
-__device__ __forceinline__ int pad32_add(int pi, int i) {
-    if constexpr (K % 32 == 0) return pi + K + K / 32;
-    else return pad32(i + K);
+// the same with one slot per 2^SH elements (split exchange rows)
+template <int SH>
+__device__ __forceinline__ int padf(int i) { return i + (i >> SH); }
+template <int SH, int K>
+__device__ __forceinline__ int padf_add(int pi, int i) {
+    if constexpr (K % (1 << SH) == 0) return pi + K + (K >> SH);
+    else return padf<SH>(i + K);
 }
 
 template <int LOGL, int LOGE, int DIR, int MODE>
-__global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG), (LdsCfg<LOGL, LOGE>::MIN_WAVES)) void lds_fft_kernel(
+__global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE, MODE>::MIN_WAVES)) void lds_fft_kernel(
     const void* __restrict__ src_v, void* __restrict__ dst_v, const float2* __restrict__ tw,
     const float2* __restrict__ tw_real, int64_t rows, float scale) {
-    using C = LdsCfg<LOGL, LOGE>;
+    using C = LdsCfg<LOGL, LOGE, MODE>;
     constexpr int L = C::L, E = C::E, T = C::T, P = C::P;
     constexpr bool NEED_LDS = (P > 1) || (MODE == 1);
     static_assert(!(C::SPLIT && MODE == 1), "the r2c stitch needs whole complex values in LDS");
@@ -147,7 +155,7 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG), (LdsCfg<LOGL, LOGE>::MIN_
         constexpr int NB = E / R;
         constexpr int LNS = C::lns(p);
         constexpr int NS = 1 << LNS;
-        const int pj = pad(j), pj32 = pad32(j);
+        const int pj = pad(j), pjf = padf<C::FSH>(j);
         if constexpr (p > 0 && !C::SPLIT) {
             static_for<0, NB>([&](auto m) {
                 static_for<0, R>([&](auto q) {
@@ -186,16 +194,16 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE>::WG), (LdsCfg<LOGL, LOGE>::MIN_
                 static_for<0, NB>([&](auto m) {
                     const int b = j + m.value * T;
                     const int base = ((b >> LNS) << (LNS + LR)) + (b & (NS - 1));
-                    const int pb = pad32(base);
+                    const int pb = padf<C::FSH>(base);
                     static_for<0, R>([&](auto q) {
                         const float2 x = v[m.value * R + q.value];
-                        ltf[pad32_add<q.value * NS>(pb, base)] = comp.value == 0 ? x.x : x.y;
+                        ltf[padf_add<C::FSH, q.value * NS>(pb, base)] = comp.value == 0 ? x.x : x.y;
                     });
                 });
                 __syncthreads();
                 static_for<0, NB1>([&](auto m) {
                     static_for<0, R1>([&](auto q) {
-                        const float x = ltf[pad32_add<m.value * T + q.value * (L / R1)>(pj32, j)];
+                        const float x = ltf[padf_add<C::FSH, m.value * T + q.value * (L / R1)>(pjf, j)];
                         if constexpr (comp.value == 0) v[m.value * R1 + q.value].x = x;
                         else v[m.value * R1 + q.value].y = x;
                     });
