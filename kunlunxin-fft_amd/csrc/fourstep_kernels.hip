@@ -455,11 +455,19 @@ __global__ __launch_bounds__((ColCfg<LL1, LE1, LC1>::WG)) void fourstep_fused_ke
     const int nt = rows > xcd ? (rows - xcd + 7) / 8 : 0;  // this XCD's transforms: t = xcd + 8k
     const int total = nt * (G1 + G2);
     int* done = sync + 9;
+    // Every branch in this loop is wave-uniform (a scalar branch).  A
+    // per-thread `if (tid == 0)` next to the barriers lets the compiler
+    // thread the paths of thread 0 and of the others apart: the loop is then
+    // compiled as an inner loop around the barriers whose exit is taken by
+    // thread 0 alone, the other lanes of its wave run the barriers again
+    // without it, and the block re-reads a stale item forever.  So wave 0
+    // runs the queue and counter atomics with all of its lanes (lane 0 adds
+    // 1, the others 0) and only scalar-register values steer control flow.
+    const bool lead = __builtin_amdgcn_readfirstlane(tid) < 64;  // wave 0
+    const int one = tid == 0 ? 1 : 0;
     for (;;) {
-        if (tid == 0) item_s = atomicAdd(sync + xcd, 1);
+        if (lead) item_s = __builtin_amdgcn_readfirstlane(atomicAdd(sync + xcd, one));
         __syncthreads();
-        // block-uniform, and read into a scalar register so that every branch
-        // on it (around the barriers below) is a scalar branch
         const int it = __builtin_amdgcn_readfirstlane(item_s);
         __syncthreads();  // every thread has read item_s before it is written again
         if (it >= total) break;
@@ -490,16 +498,16 @@ __global__ __launch_bounds__((ColCfg<LL1, LE1, LC1>::WG)) void fourstep_fused_ke
             col_store<A, 0>(v, dst + base + ((int64_t)c0 << LL1), lds, tl, c, j, LL2, 1.0f);
             __builtin_amdgcn_s_waitcnt(0);  // this thread's Z stores have reached L2
             __syncthreads();
-            if (tid == 0) atomicAdd(done + t, 1);
+            if (lead) atomicAdd(done + t, one);
         } else {
-            if (tid == 0) {
+            if (lead) {
                 // an add of an opaque zero: a literal 0 would be turned into
                 // an (L2-bypassing) atomic load by the compiler
                 const int zero = opaque(0);
                 const long long t_start = wall_clock64();
-                while (atomicAdd(done + t, zero) < G1) {
+                while (__builtin_amdgcn_readfirstlane(atomicAdd(done + t, zero)) < G1) {
                     if (wall_clock64() - t_start > wait_ticks) {
-                        atomicAdd(sync + 8, 1);
+                        atomicAdd(sync + 8, one);
                         break;
                     }
                     __builtin_amdgcn_s_sleep(2);
