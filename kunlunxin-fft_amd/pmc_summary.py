@@ -16,13 +16,13 @@ Writes
     -> HBM bytes per launch``, which bench.py reports as ``roofline.traffic``;
   * a Markdown table (algorithmic bytes, measured bytes, their ratio).
 
-``stats``: the per-kernel duration table of ``rocprofv3 --kernel-trace
---stats`` (its kernel_stats.csv) as Markdown.
+``stats``: kernel durations per launch shape (kernel, grid) from the
+kernel_trace.csv of ``rocprofv3 --kernel-trace``, as Markdown.
 
 Usage:
     python kunlunxin-fft_amd/pmc_summary.py traffic --fetch DIR --write DIR --detail bench_detail.json \
         --json profiles/pmc_traffic.json --md profiles/<name>.md [--command TEXT]
-    python kunlunxin-fft_amd/pmc_summary.py stats --dir DIR --md profiles/<name>.md [--command TEXT]
+    python kunlunxin-fft_amd/pmc_summary.py stats --dir DIR --md profiles/<name>.md [--detail bench_detail.json] [--command TEXT]
 """
 from __future__ import annotations
 
@@ -74,16 +74,53 @@ def per_kernel(d: str, counter: str):
     return {k: sum(v) / len(v) for k, v in acc.items()}
 
 
+def bench_keys(name: str, grid: int, sizes) -> list:
+    """bench.py kernel keys ("<kernel>|N=<n>|rows=<rows per launch>") that a
+    dispatch of ``name`` over ``grid`` threads serves; a dispatch of grid
+    threads with 2^LOGE elements per thread covers grid * 2^LOGE points.
+    Two sizes can share one (kernel, grid), e.g. pass 2 of 2^19 and 2^20
+    points.  Persistent kernels are not matched: their grid is the resident
+    wave, not the work."""
+    t = _template_args(name)
+    if t is None or not name.startswith(("fourstep_pass_kernel", "lds_fft_kernel")):
+        return []
+    logl, loge = t[0], t[1]
+    points = grid << loge
+    keys = []
+    for s in sizes:
+        n = s["n"]
+        if name.startswith("lds_fft_kernel") and s["flow"] == "lds-fused" and n == (1 << logl):
+            if points == n * s["batch"]:  # one launch per execute covers the batch
+                keys.append(f"lds_fft_kernel|N={n}|rows={points // n}")
+        elif name.startswith("fourstep") and s["flow"] == "four-step" and s.get("split"):
+            n1, n2, rows = s["split"]
+            kind = t[4]
+            if rows * n == points and (n1 if kind == 0 else n2) == (1 << logl):
+                keys.append(f"fourstep_pass_kernel pass {kind + 1} (n{kind + 1}={1 << logl})"
+                            f"|N={n}|rows={rows}")
+    return keys
+
+
 SQ_COUNTERS = ("SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_INSTS_LDS", "SQ_INSTS_VALU")
 
 
-def calibration(vals: dict) -> float:
-    """Counter KiB per KiB actually moved, from the largest copy dispatch."""
-    cands = [(g, v) for (n, g), v in vals.items() if n.startswith(COPY_KERNEL)]
-    if not cands:
-        raise SystemExit("the run holds no device copy to calibrate against")
-    g, v = max(cands)
-    return v / (COPY_BYTES / 1024)
+def calibration(d: str, counter: str) -> float:
+    """Counter KiB per KiB actually moved, from bench.py's 256 MiB copies.
+
+    Those are the device copies dispatched before the first other kernel of
+    the run; later copies (inputs, vendor comparisons) have other sizes.
+    """
+    rows = sorted((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"]))
+                  for r in _counter_rows(d) if r.get("Counter_Name") == counter)
+    vals = []
+    for _, name, v in rows:
+        if not name.startswith(COPY_KERNEL):
+            break
+        vals.append(v)
+    if not vals:
+        raise SystemExit(f"the {counter} run starts with no device copy to calibrate against")
+    vals.sort()
+    return vals[len(vals) // 2] / (COPY_BYTES / 1024)
 
 
 def _commands(f, command: str) -> None:
@@ -95,22 +132,32 @@ def _commands(f, command: str) -> None:
 
 
 def stats(args) -> int:
-    files = glob.glob(os.path.join(args.dir, "**", "*kernel_stats.csv"), recursive=True)
+    """Per (kernel, grid) durations from kernel_trace.csv: one kernel name
+    covers several launch shapes (sizes, chunks), which kernel_stats.csv
+    averages together."""
+    files = glob.glob(os.path.join(args.dir, "**", "*kernel_trace.csv"), recursive=True)
     if not files:
-        raise SystemExit(f"no *kernel_stats.csv under {args.dir}")
+        raise SystemExit(f"no *kernel_trace.csv under {args.dir}")
+    durs = collections.defaultdict(list)
     with open(files[0], newline="") as f:
-        rows = list(csv.DictReader(f))
+        for r in csv.DictReader(f):
+            grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+            durs[(_short(r["Kernel_Name"]), grid)].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    sizes = json.load(open(args.detail))["per_size"] if args.detail else []
+    total = sum(sum(v) for v in durs.values())
+    order = sorted(durs.items(), key=lambda kv: -sum(kv[1]))[: args.top]
     with open(args.md, "w") as f:
-        f.write("# Kernel durations (rocprofv3 --kernel-trace --stats)\n\n")
+        f.write("# Kernel durations per launch shape (rocprofv3 --kernel-trace)\n\n")
         _commands(f, args.command)
-        f.write("| kernel | calls | total ms | average us | min us | max us | share |\n")
-        f.write("|---|---:|---:|---:|---:|---:|---:|\n")
-        for r in rows:
-            name = _short(r["Name"])
-            f.write(f"| {name} | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.3f} | "
-                    f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
-                    f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.1f}% |\n")
-    print(f"wrote {args.md} ({len(rows)} kernels)")
+        f.write("Rows are (kernel, grid threads) from kernel_trace.csv, the largest total first; "
+                "`bench key` names the bench.py size a launch shape serves.\n\n")
+        f.write("| kernel | grid | bench key | calls | total ms | average us | min us | max us | share |\n")
+        f.write("|---|---:|---|---:|---:|---:|---:|---:|---:|\n")
+        for (name, grid), v in order:
+            keys = ", ".join(k.split("|", 1)[1] for k in bench_keys(name, grid, sizes)) or "-"
+            f.write(f"| {name} | {grid} | {keys} | {len(v)} | {sum(v) / 1e6:.3f} | {sum(v) / len(v) / 1e3:.2f} | "
+                    f"{min(v) / 1e3:.2f} | {max(v) / 1e3:.2f} | {100.0 * sum(v) / total:.1f}% |\n")
+    print(f"wrote {args.md} ({len(order)} launch shapes)")
     return 0
 
 
@@ -128,6 +175,8 @@ def main() -> int:
     st = sub.add_parser("stats")
     st.add_argument("--dir", required=True, help="output dir of the --kernel-trace --stats run")
     st.add_argument("--md", required=True)
+    st.add_argument("--detail", default="", help="bench_detail.json of the same command (labels the rows)")
+    st.add_argument("--top", type=int, default=40, help="launch shapes listed")
     st.add_argument("--command", default="")
     args = ap.parse_args()
     if args.cmd == "stats":
@@ -135,32 +184,16 @@ def main() -> int:
 
     fetch = per_kernel(args.fetch, "FETCH_SIZE")
     write = per_kernel(args.write, "WRITE_SIZE")
-    f_cal, w_cal = calibration(fetch), calibration(write)
+    f_cal, w_cal = calibration(args.fetch, "FETCH_SIZE"), calibration(args.write, "WRITE_SIZE")
     sq = {c: per_kernel(args.sq, c) for c in SQ_COUNTERS} if args.sq else {}
     sizes = json.load(open(args.detail))["per_size"]
 
     rows_out, traffic = [], {}
     for (name, grid) in sorted(set(fetch) | set(write)):
-        t = _template_args(name)
-        if t is None or not name.startswith(("fourstep_pass_kernel", "fourstep_persist_kernel", "lds_fft_kernel")):
+        keys = bench_keys(name, grid, sizes)
+        if not keys:
             continue
-        logl, loge = t[0], t[1]
-        if name.startswith("fourstep_persist_kernel"):
-            continue  # grid is the resident wave, not the work: not matched by size
-        points = grid << loge
-        # every bench size this dispatch shape serves (two sizes can share
-        # one (kernel, grid), e.g. pass 2 of 2^19 and 2^20 points)
-        keys = []
-        for s in sizes:
-            n = s["n"]
-            if name.startswith("lds_fft_kernel") and s["flow"] == "lds-fused" and n == (1 << logl):
-                keys.append(f"lds_fft_kernel|N={n}|rows={points // n}")
-            elif name.startswith("fourstep") and s["flow"] == "four-step" and s.get("split"):
-                n1, n2, rows = s["split"]
-                kind = t[4]
-                if rows * n == points and (n1 if kind == 0 else n2) == (1 << logl):
-                    keys.append(f"fourstep_pass_kernel pass {kind + 1} (n{kind + 1}={1 << logl})"
-                                f"|N={n}|rows={rows}")
+        points = grid << _template_args(name)[1]
         fb = fetch.get((name, grid), float("nan")) * 1024 / f_cal
         wb = write.get((name, grid), float("nan")) * 1024 / w_cal
         alg = 16 * points
