@@ -20,7 +20,9 @@ Also reported (on the same JSON line):
   device sync per trial, pooled p50, scripts/issue10_wp3_holdout.py:176-190)
   for execute_fft_plan, plus the kernel-only event p50;
 * ``config2``: latency and GB/s of the reference's small-batch configuration (N in {1024, 2048}, B in
-  {16, 64}); ``config4``: the same for N=2^20 B=1 and N=2^16 B=256;
+  {16, 64}); ``config3``: the same for inverse C2C, R2C and C2R at N in {256, 4096}, B in {1, 64}
+  (real transforms count 4N + 8(N/2+1) bytes per row); ``config4``: the same for N=2^20 B=1 and
+  N=2^16 B=256;
 * ``per_size[].vendor_*``: torch.fft.fft (rocFFT) on the same inputs, a
   comparison column only;
 * ``cpu_baseline``: the reference's own CPU FFT (butterfly::fft_dit built
@@ -217,11 +219,18 @@ def main() -> int:
     log(f"dominant kernel: {roofline}")
 
     # ---- latency at N=2048 B=1 (reference protocol) and config 2
-    def latency(n, b):
+    def latency(n, b, ttype="c2c", tdir=None):
         rng = np.random.default_rng(102026 + 10 * n + b)
-        h = (rng.standard_normal((b, n)) + 1j * rng.standard_normal((b, n))).astype(np.complex64)
+        m = n // 2 + 1 if ttype == "c2r" else n
+        if ttype == "r2c":
+            h = rng.standard_normal((b, n)).astype(np.float32)
+            nbytes = b * (4 * n + 8 * (n // 2 + 1))
+        else:
+            h = (rng.standard_normal((b, m)) + 1j * rng.standard_normal((b, m))).astype(np.complex64)
+            nbytes = b * (4 * n + 8 * (n // 2 + 1)) if ttype == "c2r" else 16 * n * b
         x = torch.from_numpy(h[0] if b == 1 else h).to(dev)
-        plan = pkg.plan_fft("dit", n, batch=b, profile_hash=prof)
+        plan = pkg.plan_fft("dit", n, batch=b, profile_hash=prof, transform_type=ttype,
+                            transform_direction=tdir)
         for _ in range(5):
             pkg.execute_fft_plan(plan, x)
         torch.cuda.synchronize()
@@ -245,18 +254,24 @@ def main() -> int:
         torch.cuda.synchronize()
         ev = statistics.median(s.elapsed_time(e) for s, e in evs)
         p50 = statistics.median(wall)
-        return {"n": n, "batch": b, "executed": plan.executed, "api_wall_p50_ms": round(p50, 5),
+        return {"n": n, "batch": b, "transform": f"{ttype} {plan.transform_direction}",
+                "executed": plan.executed, "api_wall_p50_ms": round(p50, 5),
                 "kernel_event_p50_ms": round(ev, 5),
-                "api_gbps": round(16 * n * b / (p50 * 1e-3) / 1e9, 3),
-                "kernel_gbps": round(16 * n * b / (ev * 1e-3) / 1e9, 1)}
+                "api_gbps": round(nbytes / (p50 * 1e-3) / 1e9, 3),
+                "kernel_gbps": round(nbytes / (ev * 1e-3) / 1e9, 1)}
 
-    lat, cfg2, cfg4 = None, [], []
+    lat, cfg2, cfg3, cfg4 = None, [], [], []
     if not args.no_latency:
         lat = latency(2048, 1)
         log(f"latency N=2048 B=1: {lat}")
         cfg2 = [latency(n, b) for n in (1024, 2048) for b in (16, 64)]
         for c in cfg2:
             log(f"config2: {c}")
+        # config 3: inverse C2C and the real pair at N in {256, 4096}, B in {1, 64}
+        cfg3 = [latency(n, b, t, d) for n in (256, 4096) for b in (1, 64)
+                for t, d in (("c2c", "inverse"), ("r2c", "forward"), ("c2r", "inverse"))]
+        for c in cfg3:
+            log(f"config3: {c}")
         cfg4 = [latency(1 << 20, 1), latency(1 << 16, 256)]
         for c in cfg4:
             log(f"config4: {c}")
@@ -326,6 +341,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "latency_n2048_b1": lat,
         "config2": cfg2,
+        "config3": cfg3,
         "config4": cfg4,
         "per_size": per_size,
     }

@@ -30,6 +30,7 @@ import math
 import weakref
 from dataclasses import dataclass, field
 
+from . import ledger as _ledger
 from .composition import composition_select
 from .config import NORMALIZATIONS, TRANSFORM_DIRECTIONS, TRANSFORM_TYPES
 from .selector import Selection, find_entry, load_table, select
@@ -308,12 +309,35 @@ def _resolve(plan: ExecutionPlan, device_index: int):
     return nplan, spec
 
 
+# Per-plan fast-path record, filled by the first checked execute on a device:
+# (plan weakref, device, input dtype, input shape, native plan, output shape,
+# output dtype).  Evicted when the plan dies.
+_FAST: dict = {}
+
+
 def execute_fft_plan(plan: ExecutionPlan, x):
     """Execute a resolved plan without re-querying the table (plan reuse).
 
     ``x`` must be a contiguous GPU tensor of the plan's shape and dtype; the
     result is a newly allocated tensor on the same device and stream.
+
+    A call whose input matches what the plan's last checked call on the same
+    device saw exactly (tensor type, device, dtype, shape, contiguity) skips
+    re-deriving the contract; any other input takes the full checks, which
+    raise the reference's errors.
     """
+    hit = _FAST.get(id(plan))
+    if hit is not None and _ledger._active is None and hit[0]() is plan and type(x) is _fast_mods[0].Tensor:
+        if x.get_device() == hit[1] and x.dtype is hit[2] and x.shape == hit[3] and x.is_contiguous():
+            torch, launch = _fast_mods
+            return launch(hit[4], x, torch.empty(hit[5], dtype=hit[6], device=x.device))
+    return _execute_checked(plan, x)
+
+
+_fast_mods: list = []  # [torch, runner.launch] once the first execute imported them
+
+
+def _execute_checked(plan: ExecutionPlan, x):
     import torch
 
     from .ledger import phase
@@ -340,7 +364,13 @@ def execute_fft_plan(plan: ExecutionPlan, x):
         out = torch.empty(shape, dtype=dt, device=x.device)
         from .runner import launch
 
-        return launch(nplan, x, out)
+        y = launch(nplan, x, out)
+    if not _fast_mods:
+        _fast_mods[:] = [torch, launch]
+    key = id(plan)
+    ref = weakref.ref(plan, lambda _r, k=key: _FAST.pop(k, None))
+    _FAST[key] = (ref, dev, x.dtype, tuple(x.shape), nplan, shape, dt)
+    return y
 
 
 def run_fft(x, direction: str, *, batch: int | None = None, precision: str = "fp32",

@@ -157,8 +157,10 @@ class NativePlan:
         self.info = info
 
     def execute(self, in_ptr: int, out_ptr: int, stream_ptr: int) -> None:
-        check(_lib.mfft_execute(self._h, ctypes.c_void_p(in_ptr), ctypes.c_void_p(out_ptr),
-                                ctypes.c_void_p(stream_ptr)))
+        # plain ints convert through the c_void_p argtypes
+        rc = _lib.mfft_execute(self._h, in_ptr, out_ptr, stream_ptr)
+        if rc:
+            check(rc)
 
     def execute_timed(self, in_ptr: int, out_ptr: int, stream_ptr: int, cap: int = 64) -> list:
         """Execute once and return each kernel launch's duration in ms (HIP

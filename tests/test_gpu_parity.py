@@ -436,6 +436,36 @@ def test_runs_on_a_side_stream(gpu):
     check(y.cpu().numpy(), oracle.fft_dit(seeded_c64(n, b)), "side stream")
 
 
+def test_plan_reuse_checks_every_call(gpu):
+    """Repeat executes of one plan (the cached per-plan fast path) give the
+    checked first call's result, follow the current stream, and still raise
+    the reference's errors for any input that does not match the plan."""
+    n, b = 2048, 4
+    h = seeded_c64(n, b)
+    x = torch.from_numpy(h).to(gpu)
+    plan = plan_fft("dit", n, batch=b, profile_hash=DeviceProfile.load().hash())
+    y0 = execute_fft_plan(plan, x).cpu().numpy()
+    y1 = execute_fft_plan(plan, x).cpu().numpy()
+    assert np.array_equal(y0, y1)
+    check(y1, oracle.fft_dit(h), "plan reuse")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        y2 = execute_fft_plan(plan, x)
+    s.synchronize()
+    assert np.array_equal(y2.cpu().numpy(), y0)
+    with pytest.raises(ValueError, match="shape"):
+        execute_fft_plan(plan, x[:2])
+    with pytest.raises(TypeError):
+        execute_fft_plan(plan, x.to(torch.complex128))
+    with pytest.raises(ValueError, match="contiguous"):
+        execute_fft_plan(plan, torch.from_numpy(np.ascontiguousarray(h.T)).to(gpu).T)
+    with pytest.raises(ValueError, match="GPU"):
+        execute_fft_plan(plan, torch.from_numpy(h))
+    with pytest.raises(TypeError):
+        execute_fft_plan(plan, h)
+    assert np.array_equal(execute_fft_plan(plan, x).cpu().numpy(), y0)
+
+
 def test_plan_info_reports_flows(gpu):
     assert native.NativePlan(4096, 4).flow_name == "lds-fused"
     fs = native.NativePlan(1 << 16, 4)
