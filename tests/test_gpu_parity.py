@@ -105,13 +105,34 @@ def test_c2c_all_norms(gpu, name, norm, td):
     check(y, oracle.c2c(x, td, norm), f"{name} {td} {norm}")
 
 
-@pytest.mark.parametrize("elems,n", [(e, n) for e in (4, 8, 16) for n in (32, 256, 2048, 4096)]
+@pytest.mark.parametrize("elems,n", [(e, n) for e in (4, 8) for n in (8, 16, 32, 64, 128, 256, 512, 1024, 2048,
+                                                                    4096, 8192)]
+                         + [(16, n) for n in (32, 256, 2048, 4096)]
                          + [(32, n) for n in (1024, 2048, 4096, 8192, 16384, 32768)] + [(16, 16384)])
 def test_lds_elems_axis_neutral(gpu, elems, n):
     x = seeded_c64(n, 7)
     y = execute_fft_plan(mkplan("fft_lds_fused_batch", n, 7, params={"elems": elems}),
                          torch.from_numpy(x).to(gpu)).cpu().numpy()
     check(y, oracle.fft_dit(x), f"lds elems={elems} N={n}")
+
+
+@pytest.mark.parametrize("elems", [4, 8])
+@pytest.mark.parametrize("n", [64, 2048])
+@pytest.mark.parametrize("b", [1, 5])
+def test_lds_small_elems_inverse_and_real(gpu, elems, n, b):
+    """The latency kernels (4 and 8 elements per thread) in the inverse
+    direction (conjugated roots) and in the fused R2C/C2R modes."""
+    x = seeded_c64(n, b, session=3)
+    sfx = "_batch" if b > 1 else ""
+    p = {"elems": elems}
+    y = execute_fft_plan(mkplan("fft_lds_fused" + sfx, n, b, td="inverse", norm="ortho", params=p),
+                         torch.from_numpy(x).to(gpu)).cpu().numpy()
+    check(y, oracle.c2c(x, "inverse", "ortho"), f"lds elems={elems} N={n} B={b} inverse")
+    r = seeded_f32(n, b, session=3)
+    z = execute_fft_plan(mkplan("fft_lds_fused" + sfx, n, b, tt="r2c", params=p), torch.from_numpy(r).to(gpu))
+    check(z.cpu().numpy(), np.fft.rfft(r.astype(np.float64)), f"lds elems={elems} N={n} B={b} r2c")
+    back = execute_fft_plan(mkplan("fft_lds_fused" + sfx, n, b, tt="c2r", td="inverse", params=p), z)
+    check(back.cpu().numpy(), r.astype(np.float64), f"lds elems={elems} N={n} B={b} c2r round trip")
 
 
 @pytest.mark.parametrize("n,n1", [(256, 16), (512, 32), (1 << 12, 16), (1 << 12, 256), (1 << 16, 64),
