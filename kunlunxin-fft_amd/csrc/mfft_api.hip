@@ -180,6 +180,11 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
     if (transform_type != MFFT_C2C && n < 2)
         return fail(MFFT_ERR_VALUE, "real transforms need n >= 2, got %lld", (long long)n);
     if (batch < 1) return fail(MFFT_ERR_VALUE, "batch must be >= 1, got %lld", (long long)batch);
+    // at most 2^40 bytes of complex64 rows (above any GPU's memory): keeps
+    // every byte count in range and every grid below 2^31 blocks
+    if (batch > ((int64_t)1 << 37) / n)
+        return fail(MFFT_ERR_VALUE, "batch=%lld of n=%lld exceeds 2^40 bytes of complex64 rows", (long long)batch,
+                    (long long)n);
     if (nparams < 0 || nparams > MFFT_MAX_PARAMS || (nparams > 0 && !params))
         return fail(MFFT_ERR_VALUE, "bad params (nparams=%d)", nparams);
     int32_t prm[MFFT_MAX_PARAMS] = {0, 0, 0, 0};

@@ -436,6 +436,15 @@ def test_input_validation_raises_before_launch(gpu):
         fft_dit(torch.ones(12, dtype=torch.complex64, device=gpu))
 
 
+def test_native_rejects_oversized_batch(gpu):
+    """Plans cover at most 2^40 bytes of complex64 rows (no byte count or
+    grid can overflow); the largest legal batch still plans."""
+    for n in (1, 1024, 1 << 20):
+        with pytest.raises(ValueError, match="2\\^40"):
+            native.NativePlan(n, ((1 << 37) // n) + 1)
+    assert native.NativePlan(1024, (1 << 37) // 1024, flow=native.FLOW_LDS_FUSED).info.batch == 1 << 27
+
+
 def test_native_rejects_overlap_and_misalignment(gpu):
     np_ = native.NativePlan(64, 2, flow=native.FLOW_LDS_FUSED)
     buf = torch.zeros(4 * 64, dtype=torch.complex64, device=gpu)

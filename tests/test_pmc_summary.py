@@ -1,0 +1,73 @@
+"""Host logic of kunlunxin-fft_amd/pmc_summary.py on synthetic rocprofv3 CSVs:
+copy calibration, (kernel, grid) -> bench-size matching, traffic bytes and
+the per-launch-shape duration table."""
+import csv
+import json
+import os
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+SCRIPT = os.path.join(ROOT, "kunlunxin-fft_amd", "pmc_summary.py")
+LDS = "void mfft::(anonymous namespace)::lds_fft_kernel<10, 4, -1, 0>(void const*, void*, float)"
+P1 = "void mfft::(anonymous namespace)::fourstep_pass_kernel<10, 5, 4, -1, 0>(float2 const*, int)"
+COPY = "__amd_rocclr_copyBuffer"
+MIB = 1024  # counter values are KiB
+
+
+def _counters(path, counter, rows):
+    os.makedirs(path, exist_ok=True)
+    with open(os.path.join(path, "run_counter_collection.csv"), "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Dispatch_Id", "Grid_Size", "Kernel_Name", "Counter_Name", "Counter_Value"])
+        for i, (name, grid, kib) in enumerate(rows, 1):
+            w.writerow([i, grid, name, counter, kib])
+
+
+def _detail(path):
+    sizes = [{"n": 1024, "batch": 32768, "flow": "lds-fused", "split": None},
+             {"n": 1 << 20, "batch": 64, "flow": "four-step", "split": [1024, 1024, 16]}]
+    with open(path, "w") as f:
+        json.dump({"per_size": sizes}, f)
+
+
+def test_traffic_calibrates_on_leading_copies(tmp_path):
+    # the counters read half (fetch) and all (write) of the bytes moved;
+    # a later, larger copy must not change the calibration
+    lds_grid, p1_grid = 2097152, 524288  # 2^25 and 2^24 points
+    fetch = [(COPY, 131072, 128 * MIB), (COPY, 131072, 128 * MIB), (LDS, lds_grid, 128 * MIB),
+             (P1, p1_grid, 64.5 * MIB), (COPY, 131072, 300 * MIB)]
+    write = [(COPY, 131072, 256 * MIB), (COPY, 131072, 256 * MIB), (LDS, lds_grid, 256 * MIB),
+             (P1, p1_grid, 128 * MIB), (COPY, 131072, 600 * MIB)]
+    _counters(tmp_path / "f", "FETCH_SIZE", fetch)
+    _counters(tmp_path / "w", "WRITE_SIZE", write)
+    _detail(tmp_path / "d.json")
+    out = tmp_path / "t.json"
+    subprocess.run([sys.executable, SCRIPT, "traffic", "--fetch", str(tmp_path / "f"), "--write",
+                    str(tmp_path / "w"), "--detail", str(tmp_path / "d.json"), "--json", str(out),
+                    "--md", str(tmp_path / "t.md")], check=True, capture_output=True)
+    t = json.load(open(out))
+    assert t["lds_fft_kernel|N=1024|rows=32768"] == 512 << 20
+    assert t["fourstep_pass_kernel pass 1 (n1=1024)|N=1048576|rows=16"] == (129 + 128) << 20
+    assert "scaled by 2.000" in open(tmp_path / "t.md").read()
+
+
+def test_stats_one_row_per_launch_shape(tmp_path):
+    d = tmp_path / "trace"
+    d.mkdir()
+    rows = [(LDS, 2097152, 100_000), (LDS, 2097152, 102_000), (LDS, 2048, 4_000), (P1, 524288, 64_000)]
+    with open(d / "run_kernel_trace.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Kernel_Name", "Start_Timestamp", "End_Timestamp", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z"])
+        t = 0
+        for name, grid, ns in rows:
+            w.writerow([name, t, t + ns, grid, 1, 1])
+            t += ns + 1000
+    _detail(tmp_path / "d.json")
+    md = tmp_path / "s.md"
+    subprocess.run([sys.executable, SCRIPT, "stats", "--dir", str(d), "--detail", str(tmp_path / "d.json"),
+                    "--md", str(md)], check=True, capture_output=True)
+    text = open(md).read()
+    assert "| lds_fft_kernel<10, 4, -1, 0> | 2097152 | N=1024|rows=32768 | 2 | 0.202 | 101.00 |" in text
+    assert "| lds_fft_kernel<10, 4, -1, 0> | 2048 | - | 1 |" in text
+    assert "| fourstep_pass_kernel<10, 5, 4, -1, 0> | 524288 | N=1048576|rows=16 | 1 |" in text
