@@ -105,6 +105,7 @@ class DesignSpace:
     stage_blocks: tuple
     lds_elems: tuple
     lds_max_n: int
+    lds_stagger: tuple
     fourstep_n1: tuple
     fourstep_chunk_rows: tuple
     fourstep_min_n: int
@@ -126,6 +127,9 @@ class DesignSpace:
         lds = p.get("lds_fused", {})
         _require(_pow2_list(lds.get("elems")), "butterfly_space.json: P.lds_fused.elems must be powers of two")
         _require(isinstance(lds.get("max_n"), int) and lds["max_n"] > 0, "butterfly_space.json: P.lds_fused.max_n required")
+        stag = lds.get("stagger", [0])
+        _require(isinstance(stag, list) and stag and all(isinstance(v, int) and 0 <= v <= 16 for v in stag),
+                 "butterfly_space.json: P.lds_fused.stagger must be ints in [0, 16]")
         fs = p.get("four_step", {})
         _require(_pow2_list(fs.get("n1")), "butterfly_space.json: P.four_step.n1 must be powers of two")
         ch = fs.get("chunk_rows")
@@ -146,6 +150,7 @@ class DesignSpace:
         return DesignSpace(
             space_id=d["space_id"], target=d["target"], radix=tuple(p["radix"]),
             stage_blocks=tuple(st["blocks"]), lds_elems=tuple(lds["elems"]), lds_max_n=lds["max_n"],
+            lds_stagger=tuple(stag),
             fourstep_n1=tuple(fs["n1"]), fourstep_chunk_rows=tuple(ch), fourstep_min_n=fs["min_n"],
             fourstep_schedule=tuple(sched),
             batch_candidates=tuple(b["candidates"]), batch_variants=tuple(variants),

@@ -91,7 +91,7 @@ __device__ __forceinline__ int padf_add(int pi, int i) {
 template <int LOGL, int LOGE, int DIR, int MODE>
 __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE, MODE>::MIN_WAVES)) void lds_fft_kernel(
     const void* __restrict__ src_v, void* __restrict__ dst_v, const float2* __restrict__ tw,
-    const float2* __restrict__ tw_real, int64_t rows, float scale) {
+    const float2* __restrict__ tw_real, int64_t rows, float scale, int stag_wave, int stag_cus, int stag_n) {
     using C = LdsCfg<LOGL, LOGE, MODE>;
     constexpr int L = C::L, E = C::E, T = C::T, P = C::P;
     constexpr bool NEED_LDS = (P > 1) || (MODE == 1);
@@ -100,6 +100,17 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
     float2* const lds = lds_raw;
     float* const ldsf = reinterpret_cast<float*>(lds_raw);
 
+    // Start stagger (block-uniform): the blocks of the first wave (the first
+    // stag_wave in dispatch order) that land on the upper half of the
+    // stag_cus CUs of their XCD (blocks go round-robin over the 8 XCDs, so
+    // block b is the (b / 8)-th of its XCD) sleep stag_n x 8128 clocks before
+    // loading.  With few blocks per CU every CU otherwise loads, computes and
+    // stores in lockstep, round after round, and HBM idles through the common
+    // compute phase; offsetting half of every XCD's CUs by about half a
+    // block period makes one half load and store while the other computes.
+    if (stag_n > 0 && (int)blockIdx.x < stag_wave && (int)((blockIdx.x >> 3) % stag_cus) >= (stag_cus >> 1)) {
+        for (int q = 0; q < stag_n; ++q) __builtin_amdgcn_s_sleep(127);
+    }
     const int tid = threadIdx.x;
     const int tl = tid / T;
     const int j = tid & (T - 1);
@@ -246,50 +257,70 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
     }
 }
 
+// Arguments of one LDS launch, passed down the template dispatch.
+struct LdsArgs {
+    const void* src;
+    void* dst;
+    const float2* tw;
+    const float2* tw_real;
+    int64_t rows;
+    float scale;
+    hipStream_t stream;
+    int num_cus;  // compute units of the device (start stagger)
+    int stagger;  // start stagger, s_sleep(127) units (0 = off)
+};
+
 template <int LOGL, int LOGE, int DIR, int MODE>
-hipError_t launch_one(const void* src, void* dst, const float2* tw, const float2* tw_real,
-                      int64_t rows, float scale, hipStream_t stream) {
+hipError_t launch_one(const LdsArgs& a) {
     using C = LdsCfg<LOGL, LOGE>;
-    const int64_t blocks = (rows + C::TPB - 1) / C::TPB;
+    const int64_t blocks = (a.rows + C::TPB - 1) / C::TPB;
     if (blocks <= 0) return hipSuccess;
-    lds_fft_kernel<LOGL, LOGE, DIR, MODE><<<(unsigned)blocks, C::WG, 0, stream>>>(src, dst, tw, tw_real, rows, scale);
-    mark(stream);
+    int wave_blocks = 0, n = 0;
+    if (a.stagger > 0 && a.num_cus >= 16) {
+        // blocks one wave of the grid holds (occupancy query, once per kernel)
+        static const int per_cu = [] {
+            int b = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, lds_fft_kernel<LOGL, LOGE, DIR, MODE>, C::WG, 0) !=
+                hipSuccess) {
+                (void)hipGetLastError();
+                b = 0;
+            }
+            return b;
+        }();
+        const int64_t wave = (int64_t)per_cu * a.num_cus;
+        // only when the launch runs at least two waves of blocks
+        if (wave > 0 && blocks >= 2 * wave) wave_blocks = (int)wave, n = a.stagger;
+    }
+    lds_fft_kernel<LOGL, LOGE, DIR, MODE><<<(unsigned)blocks, C::WG, 0, a.stream>>>(
+        a.src, a.dst, a.tw, a.tw_real, a.rows, a.scale, wave_blocks, a.num_cus / 8, n);
+    mark(a.stream);
     return hipGetLastError();
 }
 
 template <int LOGL, int LOGE>
-hipError_t dispatch_mode(int mode, int dir, const void* src, void* dst, const float2* tw,
-                         const float2* tw_real, int64_t rows, float scale, hipStream_t stream) {
-    if (mode == 0) {
-        return dir < 0 ? launch_one<LOGL, LOGE, -1, 0>(src, dst, tw, tw_real, rows, scale, stream)
-                       : launch_one<LOGL, LOGE, 1, 0>(src, dst, tw, tw_real, rows, scale, stream);
-    }
-    if (mode == 1) return launch_one<LOGL, LOGE, -1, 1>(src, dst, tw, tw_real, rows, scale, stream);
-    return launch_one<LOGL, LOGE, 1, 2>(src, dst, tw, tw_real, rows, scale, stream);
+hipError_t dispatch_mode(int mode, int dir, const LdsArgs& a) {
+    if (mode == 0) return dir < 0 ? launch_one<LOGL, LOGE, -1, 0>(a) : launch_one<LOGL, LOGE, 1, 0>(a);
+    if (mode == 1) return launch_one<LOGL, LOGE, -1, 1>(a);
+    return launch_one<LOGL, LOGE, 1, 2>(a);
 }
 
 // 32 elements per thread (split exchange): c2c and c2r only
 template <int LOGL>
-hipError_t dispatch_split(int mode, int dir, const void* src, void* dst, const float2* tw,
-                          const float2* tw_real, int64_t rows, float scale, hipStream_t stream) {
-    if (mode == 0) {
-        return dir < 0 ? launch_one<LOGL, 5, -1, 0>(src, dst, tw, tw_real, rows, scale, stream)
-                       : launch_one<LOGL, 5, 1, 0>(src, dst, tw, tw_real, rows, scale, stream);
-    }
-    if (mode == 2) return launch_one<LOGL, 5, 1, 2>(src, dst, tw, tw_real, rows, scale, stream);
+hipError_t dispatch_split(int mode, int dir, const LdsArgs& a) {
+    if (mode == 0) return dir < 0 ? launch_one<LOGL, 5, -1, 0>(a) : launch_one<LOGL, 5, 1, 0>(a);
+    if (mode == 2) return launch_one<LOGL, 5, 1, 2>(a);
     return hipErrorInvalidValue;
 }
 
 template <int LOGL>
-hipError_t dispatch_elems(int loge, int mode, int dir, const void* src, void* dst, const float2* tw,
-                          const float2* tw_real, int64_t rows, float scale, hipStream_t stream) {
+hipError_t dispatch_elems(int loge, int mode, int dir, const LdsArgs& a) {
     if constexpr (LOGL >= 10) {
-        if (loge == 5) return dispatch_split<LOGL>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        if (loge == 5) return dispatch_split<LOGL>(mode, dir, a);
     }
     switch (loge) {
-        case 2: return dispatch_mode<LOGL, 2>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 3: return dispatch_mode<LOGL, 3>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        default: return dispatch_mode<LOGL, 4>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 2: return dispatch_mode<LOGL, 2>(mode, dir, a);
+        case 3: return dispatch_mode<LOGL, 3>(mode, dir, a);
+        default: return dispatch_mode<LOGL, 4>(mode, dir, a);
     }
 }
 
@@ -322,25 +353,26 @@ int lds_threads_per_block(int log2l, int elems) {
 
 hipError_t launch_lds(int mode, int dir, int log2l, int elems, const void* src, void* dst,
                       const float2* tw, const float2* tw_real, int64_t rows, float scale,
-                      hipStream_t stream) {
+                      hipStream_t stream, int num_cus, int stagger) {
     const int loge = ilog2(elems);
+    const LdsArgs a{src, dst, tw, tw_real, rows, scale, stream, num_cus, stagger};
     switch (log2l) {
-        case 0: return dispatch_elems<0>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 1: return dispatch_elems<1>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 2: return dispatch_elems<2>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 3: return dispatch_elems<3>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 4: return dispatch_elems<4>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 5: return dispatch_elems<5>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 6: return dispatch_elems<6>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 7: return dispatch_elems<7>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 8: return dispatch_elems<8>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 9: return dispatch_elems<9>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 10: return dispatch_elems<10>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 11: return dispatch_elems<11>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 12: return dispatch_elems<12>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 13: return dispatch_elems<13>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 14: return dispatch_elems<14>(loge, mode, dir, src, dst, tw, tw_real, rows, scale, stream);
-        case 15: return dispatch_split<15>(mode, dir, src, dst, tw, tw_real, rows, scale, stream);
+        case 0: return dispatch_elems<0>(loge, mode, dir, a);
+        case 1: return dispatch_elems<1>(loge, mode, dir, a);
+        case 2: return dispatch_elems<2>(loge, mode, dir, a);
+        case 3: return dispatch_elems<3>(loge, mode, dir, a);
+        case 4: return dispatch_elems<4>(loge, mode, dir, a);
+        case 5: return dispatch_elems<5>(loge, mode, dir, a);
+        case 6: return dispatch_elems<6>(loge, mode, dir, a);
+        case 7: return dispatch_elems<7>(loge, mode, dir, a);
+        case 8: return dispatch_elems<8>(loge, mode, dir, a);
+        case 9: return dispatch_elems<9>(loge, mode, dir, a);
+        case 10: return dispatch_elems<10>(loge, mode, dir, a);
+        case 11: return dispatch_elems<11>(loge, mode, dir, a);
+        case 12: return dispatch_elems<12>(loge, mode, dir, a);
+        case 13: return dispatch_elems<13>(loge, mode, dir, a);
+        case 14: return dispatch_elems<14>(loge, mode, dir, a);
+        case 15: return dispatch_split<15>(mode, dir, a);
         default: return hipErrorInvalidValue;
     }
 }

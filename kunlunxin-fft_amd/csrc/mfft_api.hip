@@ -139,7 +139,7 @@ int run_core(const mfft_plan* p, const float2* src, float2* dst, int dir, float 
             break;
         case MFFT_FLOW_LDS_FUSED:
             e = mfft::launch_lds(0, dir, mfft::ilog2((int)p->core_n), p->elems, src, dst, p->tw, nullptr,
-                                 p->batch, scale, stream);
+                                 p->batch, scale, stream, p->num_cus, p->stagger);
             break;
         case MFFT_FLOW_FOUR_STEP:
             e = mfft::launch_fourstep(dir, src, dst, p, p->batch, scale, stream, &launches);
@@ -202,7 +202,7 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
     const int lds_mode = transform_type == MFFT_R2C ? 1 : (transform_type == MFFT_C2R ? 2 : 0);
     if (flow == MFFT_FLOW_AUTO)
         flow = mfft::lds_supported(logc, 0, lds_mode) ? MFFT_FLOW_LDS_FUSED : MFFT_FLOW_FOUR_STEP;
-    int block = 256, elems = 0;
+    int block = 256, elems = 0, stagger = 0;
     int64_t n1 = 0, n2 = 0, chunk = 0;
     int schedule = 0;
     switch (flow) {
@@ -231,6 +231,10 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
                             mfft::kMaxLdsLog2, (long long)core_n, prm[0]);
             elems = prm[0] ? prm[0] : mfft::lds_default_elems(logc);
             block = mfft::lds_threads_per_block(logc, elems);
+            if (prm[1] > mfft::kMaxStagger)
+                return fail(MFFT_ERR_VALUE, "LDS_FUSED start stagger params[1]=%d exceeds %d", prm[1],
+                            mfft::kMaxStagger);
+            stagger = prm[1];
             break;
         case MFFT_FLOW_FOUR_STEP: {
             int l1, l2;
@@ -290,6 +294,7 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
     p->device = dev;
     p->block = block;
     p->elems = elems;
+    p->stagger = stagger;
     p->n1 = n1;
     p->n2 = n2;
     p->chunk_rows = chunk;
@@ -411,7 +416,8 @@ int mfft_execute(const mfft_plan* p, const void* in, void* out, void* stream_v) 
     const int logc = mfft::ilog2((int)p->core_n);
     if (p->transform_type == MFFT_R2C) {
         if (p->r2c_fused) {
-            he = mfft::launch_lds(1, -1, logc, p->elems, in, out, p->tw, p->tw_real, p->batch, p->scale, stream);
+            he = mfft::launch_lds(1, -1, logc, p->elems, in, out, p->tw, p->tw_real, p->batch, p->scale, stream,
+                                  p->num_cus, p->stagger);
             return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
         }
         int rc = run_core(p, (const float2*)in, p->ws_a, -1, 1.0f, stream);
@@ -421,7 +427,8 @@ int mfft_execute(const mfft_plan* p, const void* in, void* out, void* stream_v) 
     }
     // c2r
     if (p->c2r_fused) {
-        he = mfft::launch_lds(2, 1, logc, p->elems, in, out, p->tw, p->tw_real, p->batch, p->scale, stream);
+        he = mfft::launch_lds(2, 1, logc, p->elems, in, out, p->tw, p->tw_real, p->batch, p->scale, stream,
+                              p->num_cus, p->stagger);
         return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
     }
     he = mfft::launch_c2r_pre((const float2*)in, p->ws_a, p->tw_real, p->n, p->batch, stream);

@@ -17,6 +17,7 @@ struct mfft_plan {
     float scale = 1.0f;  // applied by the final store of the core (c2c, c2r) or the stitch (r2c)
     int block = 256;     // stage flows: threads per block
     int elems = 16;      // LDS_FUSED: elements per thread
+    int stagger = 0;     // LDS_FUSED: start stagger of half the first wave, s_sleep(127) units
     int launches = 0;
     int64_t n1 = 0, n2 = 0, chunk_rows = 0;
     int schedule = 0;    // FOUR_STEP: 0 one column group per block, 1 persistent, 2 fused (one launch)
@@ -85,11 +86,12 @@ int lds_default_elems(int log2l);
 int lds_threads_per_block(int log2l, int elems);
 hipError_t launch_lds(int mode, int dir, int log2l, int elems, const void* src, void* dst,
                       const float2* tw, const float2* tw_real, int64_t rows, float scale,
-                      hipStream_t stream);
+                      hipStream_t stream, int num_cus = 0, int stagger = 0);
 
 // ---- fourstep_kernels.hip: two-pass column/row FFT -----------------------
 bool fourstep_supported(int log2n1, int log2n2);
 bool fourstep_fused_supported(int log2n1, int log2n2);  // schedule 2: n1, n2 in [128, 512], within 2x
+constexpr int kMaxStagger = 16;  // LDS_FUSED start stagger limit (16 x 8128 clocks)
 constexpr int kFusedWaitMs = 20;  // longest pass-2 wait of the fused schedule before it gives up
 constexpr bool kFusedScheduleEnabled = false;  // fused schedule switched off (it did not finish on the GPU)
 int fourstep_col_loge(int logl);  // log2 elements per thread of a pass of length 2^logl

@@ -93,7 +93,7 @@ def flow_params(executed: str, n: int, transform_type: str, block, params: dict)
             e = 0
         if logc == 15:
             e = 0
-        return flow, (e,)
+        return flow, (e, int(params.get("stagger", 0)))
     if kind == "fourstep":
         n1 = int(params.get("n1", 0))
         if core < 256:

@@ -105,6 +105,9 @@ def entry_contract_violations(entry: dict) -> list[str]:
         e = params.get("elems", 0)
         if e not in (0,) + sp.lds_elems:
             bad.append(f"elems {e!r} not in {sp.lds_elems}")
+        stg = params.get("stagger", 0)
+        if stg not in (0,) + sp.lds_stagger:
+            bad.append(f"stagger {stg!r} not in {sp.lds_stagger}")
         if isinstance(n, int) and n > 2 * sp.lds_max_n:
             bad.append(f"N={n} exceeds the LDS kernel's range ({sp.lds_max_n} complex core)")
     if real == "four-step":

@@ -5,7 +5,8 @@ MI355X counterpart of the reference's table builder
 For every cell (N, batch, direction) it times the M0 incumbent (fft_dit /
 fft_dif and their batch forms) and every legal challenger of the published
 design space (config/butterfly_space.json): the radix-4 global-stage flow,
-the single-pass LDS kernel at each elements-per-thread setting, and the
+the single-pass LDS kernel at each elements-per-thread setting (and start
+stagger, where it can act), and the
 four-step at each split, chunking and schedule (one column group per
 workgroup, persistent workgroups, or both passes fused per XCD).  The fastest challenger is promoted
 only when it beats the incumbent by at least GUARD_PCT percent (M0 closure);
@@ -75,8 +76,14 @@ def candidates(n: int, b: int, direction: str, space):
                 continue
             if n <= 16 and e != 16:
                 continue
-            out.append((f"lds_e{e}", "fft_lds_fused" + sfx, 256, {"elems": e},
-                        ("lds-resident", "stockham-radix16", "lds-stockham-single-pass")))
+            # the start stagger acts on launches of two or more waves of
+            # workgroups with at most four workgroups per CU: 2^13..2^15 points
+            # at 16 or 32 elements per thread, in large batches
+            stags = [s for s in space.lds_stagger if s == 0 or (e >= 16 and logn >= 13 and n * b >= (1 << 24))]
+            for stg in stags:
+                params = {"elems": e} if stg == 0 else {"elems": e, "stagger": stg}
+                out.append((f"lds_e{e}" + (f"_s{stg}" if stg else ""), "fft_lds_fused" + sfx, 256, params,
+                            ("lds-resident", "stockham-radix16", "lds-stockham-single-pass")))
     if space.fourstep_min_n <= n <= (1 << 20):
         for n1 in space.fourstep_n1:
             n2 = n // n1

@@ -135,6 +135,27 @@ def test_lds_small_elems_inverse_and_real(gpu, elems, n, b):
     check(back.cpu().numpy(), r.astype(np.float64), f"lds elems={elems} N={n} B={b} c2r round trip")
 
 
+@pytest.mark.parametrize("n,b,stg", [(1 << 15, 600, 4), (1 << 14, 1100, 2), (1 << 15, 300, 4)])
+def test_lds_start_stagger_neutral(gpu, n, b, stg):
+    """The start stagger only delays workgroups: results equal the
+    unstaggered kernel's bit for bit (B=600 and 1100 run it over two or more
+    waves of workgroups; B=300 leaves it off)."""
+    x = torch.from_numpy(seeded_c64(n, b, session=5)).to(gpu)
+    y0 = execute_fft_plan(mkplan("fft_lds_fused_batch", n, b, params={"elems": 32}), x)
+    y1 = execute_fft_plan(mkplan("fft_lds_fused_batch", n, b, params={"elems": 32, "stagger": stg}), x)
+    assert torch.equal(y0, y1)
+    rows = [0, b // 2, b - 1]
+    check(y1[rows].cpu().numpy(), np.fft.fft(x[rows].cpu().numpy().astype(np.complex128)), f"stagger N={n} B={b}")
+    # c2r with a 2^15-point core (the fused pre-twiddle mode)
+    if n == 1 << 15 and b == 600:
+        h = torch.from_numpy(seeded_c64(n + 1, b, session=6)).to(gpu)  # n + 1 bins of a 2n-point c2r
+        r0 = execute_fft_plan(mkplan("fft_lds_fused_batch", 2 * n, b, tt="c2r", td="inverse",
+                                     params={"elems": 32}), h)
+        r1 = execute_fft_plan(mkplan("fft_lds_fused_batch", 2 * n, b, tt="c2r", td="inverse",
+                                     params={"elems": 32, "stagger": stg}), h)
+        assert torch.equal(r0, r1)
+
+
 @pytest.mark.parametrize("n,n1", [(256, 16), (512, 32), (1 << 12, 16), (1 << 12, 256), (1 << 16, 64),
                                   (1 << 16, 1024), (1 << 20, 1024), (1 << 14, 512)])
 @pytest.mark.parametrize("chunk", [0, 2])
