@@ -7,9 +7,9 @@ values in KiB per dispatch, ``--output-format csv``), averages them per
 (kernel, grid), scales each counter by what it reads for the device copy of
 known size that bench.py performs first (256 MiB read + 256 MiB written,
 kernel ``__amd_rocclr_copyBuffer``), and matches every FFT kernel to the
-bench.py size it belongs to using ``gpurun_out/bench_detail.json`` of the same
-command: a dispatch of ``grid`` threads with 2^LOGE elements per thread covers
-grid * 2^LOGE complex points.
+bench.py size it belongs to using the ``bench_detail.json`` that the same
+bench.py command writes: a dispatch of ``grid`` threads with 2^LOGE elements
+per thread covers grid * 2^LOGE complex points.
 
 Writes
   * a JSON map ``"<kernel as bench.py names it>|N=<n>|rows=<rows per launch>"
