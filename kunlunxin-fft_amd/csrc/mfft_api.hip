@@ -261,8 +261,10 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
                             "(got 2^%d x 2^%d)",
                             l1, l2);
             // The fused schedule did not finish on the MI355X (its first launch, N=2^14 B=1, ran
-            // past a 60 s limit twice, the second time with every pass-2 wait bounded by the wall
-            // clock); its cause is not found, so the schedule is switched off.
+            // past a 60 s limit twice).  Its work loop had been compiled into an inner loop around
+            // the barriers that only thread 0 could leave, so the other lanes redid a stale item
+            // forever; the loop now branches on wave-uniform values only, which has not yet run on
+            // the GPU, so the schedule stays switched off.
             if (schedule == 2 && !mfft::kFusedScheduleEnabled)
                 return fail(MFFT_ERR_UNSUPPORTED,
                             "the fused FOUR_STEP schedule (params[2] = 2) is disabled in this build");

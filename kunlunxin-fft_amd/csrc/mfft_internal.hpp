@@ -93,7 +93,7 @@ bool fourstep_supported(int log2n1, int log2n2);
 bool fourstep_fused_supported(int log2n1, int log2n2);  // schedule 2: n1, n2 in [128, 512], within 2x
 constexpr int kMaxStagger = 16;  // LDS_FUSED start stagger limit (16 x 8128 clocks)
 constexpr int kFusedWaitMs = 20;  // longest pass-2 wait of the fused schedule before it gives up
-constexpr bool kFusedScheduleEnabled = false;  // fused schedule switched off (it did not finish on the GPU)
+constexpr bool kFusedScheduleEnabled = false;  // fused schedule switched off until its fixed loop has run on the GPU
 int fourstep_col_loge(int logl);  // log2 elements per thread of a pass of length 2^logl
 void fourstep_default_split(int log2n, int* log2n1, int* log2n2);
 hipError_t launch_fourstep(int dir, const float2* src, float2* dst, const mfft_plan* p,

@@ -191,7 +191,8 @@ FUSED_SPLITS = [(1 << 14, 128), (1 << 15, 128), (1 << 15, 256), (1 << 16, 256), 
 
 
 FUSED_OFF = ("the fused four-step schedule is switched off: its first GPU launch (N=2^14, B=1) did not "
-             "finish twice, the cause is not found, and plan creation now rejects schedule 2")
+             "finish twice (its loop compiled into an inner barrier loop only thread 0 could leave); the "
+             "fixed loop has not run on the GPU yet, and plan creation rejects schedule 2")
 
 
 @pytest.mark.skip(reason=FUSED_OFF)
