@@ -21,7 +21,7 @@ kernel_trace.csv of ``rocprofv3 --kernel-trace``, as Markdown.
 
 Usage:
     python kunlunxin-fft_amd/pmc_summary.py traffic --fetch DIR --write DIR --detail bench_detail.json \
-        --json profiles/pmc_traffic.json --md profiles/<name>.md [--command TEXT]
+        --json profiles/pmc_traffic.json --md profiles/<name>.md [--sq DIR] [--trace DIR] [--command TEXT]
     python kunlunxin-fft_amd/pmc_summary.py stats --dir DIR --md profiles/<name>.md [--detail bench_detail.json] [--command TEXT]
 """
 from __future__ import annotations
@@ -131,18 +131,25 @@ def _commands(f, command: str) -> None:
         f.write("\n")
 
 
-def stats(args) -> int:
-    """Per (kernel, grid) durations from kernel_trace.csv: one kernel name
-    covers several launch shapes (sizes, chunks), which kernel_stats.csv
-    averages together."""
-    files = glob.glob(os.path.join(args.dir, "**", "*kernel_trace.csv"), recursive=True)
+def trace_durations(d: str) -> dict:
+    """(kernel, grid threads) -> list of dispatch durations in ns, from the
+    kernel_trace.csv of a ``rocprofv3 --kernel-trace`` run."""
+    files = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
     if not files:
-        raise SystemExit(f"no *kernel_trace.csv under {args.dir}")
+        raise SystemExit(f"no *kernel_trace.csv under {d}")
     durs = collections.defaultdict(list)
     with open(files[0], newline="") as f:
         for r in csv.DictReader(f):
             grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
             durs[(_short(r["Kernel_Name"]), grid)].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    return durs
+
+
+def stats(args) -> int:
+    """Per (kernel, grid) durations from kernel_trace.csv: one kernel name
+    covers several launch shapes (sizes, chunks), which kernel_stats.csv
+    averages together."""
+    durs = trace_durations(args.dir)
     sizes = json.load(open(args.detail))["per_size"] if args.detail else []
     total = sum(sum(v) for v in durs.values())
     order = sorted(durs.items(), key=lambda kv: -sum(kv[1]))[: args.top]
@@ -172,6 +179,7 @@ def main() -> int:
     t.add_argument("--md", required=True)
     t.add_argument("--command", default="", help="commands that made the input, quoted in the Markdown")
     t.add_argument("--sq", default="", help="output dir of an SQ counter run (" + " ".join(SQ_COUNTERS) + ")")
+    t.add_argument("--trace", default="", help="output dir of a --kernel-trace run of the same command (rates)")
     st = sub.add_parser("stats")
     st.add_argument("--dir", required=True, help="output dir of the --kernel-trace --stats run")
     st.add_argument("--md", required=True)
@@ -186,6 +194,7 @@ def main() -> int:
     write = per_kernel(args.write, "WRITE_SIZE")
     f_cal, w_cal = calibration(args.fetch, "FETCH_SIZE"), calibration(args.write, "WRITE_SIZE")
     sq = {c: per_kernel(args.sq, c) for c in SQ_COUNTERS} if args.sq else {}
+    durs = trace_durations(args.trace) if args.trace else {}
     sizes = json.load(open(args.detail))["per_size"]
 
     rows_out, traffic = [], {}
@@ -213,9 +222,14 @@ def main() -> int:
         if sq:
             f.write("SQ columns (a third run): LDS bank-conflict cycles per LDS-active cycle "
                     "(SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE) and LDS per VALU instructions.\n\n")
+        if durs:
+            f.write("Rate columns (the kernel-trace run of the same bench command): the measured bytes over the "
+                    "average rocprofv3 duration of the same launch shape, and that rate against 8 TB/s.\n\n")
         f.write("| bench kernel key | kernel | grid | algorithmic MiB | fetch MiB | write MiB | traffic / algorithmic |"
-                + (" LDS conflict / active | LDS / VALU insts |" if sq else "") + "\n")
-        f.write("|---|---|---:|---:|---:|---:|---:|" + ("---:|---:|" if sq else "") + "\n")
+                + (" LDS conflict / active | LDS / VALU insts |" if sq else "")
+                + (" rocprof avg us | HBM GB/s | % of 8 TB/s |" if durs else "") + "\n")
+        f.write("|---|---|---:|---:|---:|---:|---:|" + ("---:|---:|" if sq else "") + ("---:|---:|---:|" if durs else "")
+                + "\n")
         for key, name, grid, alg, fb, wb in rows_out:
             extra = ""
             if sq:
@@ -223,6 +237,14 @@ def main() -> int:
                 bc, act, li, vi = (g(c) for c in SQ_COUNTERS)
                 extra = (f" {bc / act:.3f} |" if bc is not None and act else " - |") + \
                         (f" {li / vi:.3f} |" if li is not None and vi else " - |")
+            if durs:
+                v = durs.get((name, grid))
+                if v:
+                    us = sum(v) / len(v) / 1e3
+                    gbs = (fb + wb) / (us * 1e-6) / 1e9
+                    extra += f" {us:.2f} | {gbs:.0f} | {gbs / 8000:.1%} |"
+                else:
+                    extra += " - | - | - |"
             f.write(f"| {key} | {name} | {grid} | {alg / 2**20:.1f} | {fb / 2**20:.1f} | {wb / 2**20:.1f} | "
                     f"{(fb + wb) / alg:.3f} |{extra}\n")
     print(f"wrote {args.json} ({len(traffic)} kernels) and {args.md}")
