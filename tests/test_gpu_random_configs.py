@@ -1,0 +1,90 @@
+"""Seeded random configurations through the plan API, against numpy float64.
+
+Each case draws a runner (M0, M5, LDS, four-step), a transform type and
+direction, a norm, N, a ragged batch, and the runner's parameters (threads
+per block, elements per thread, start stagger, n1, chunk rows, schedule) from
+their published ranges (N <= 2^20), then checks the GPU result to the north-star gate
+(rel-L2 and peak-normalised worst element <= 1e-5).  Sizes stay small enough
+(N * B <= 2^21) that the whole set runs in seconds.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from kunlunxin_fft_amd import ExecutionPlan, execute_fft_plan
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+NORMS = ("none", "forward", "backward", "ortho")
+# runner, smallest and largest log2 of the complex core
+FLOWS = (("fft_dit", 1, 16), ("fft_dif", 1, 16), ("fft_dit_radix4", 2, 16), ("fft_dif_radix4", 2, 16),
+         ("fft_lds_fused", 0, 15), ("fft_four_step", 8, 20))
+
+
+def _cases(count=160, seed=20261202):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        name, lo, hi = FLOWS[int(rng.integers(len(FLOWS)))]
+        tt = ("c2c", "c2c", "r2c", "c2r")[int(rng.integers(4))]
+        real = tt != "c2c"
+        logc = int(rng.integers(lo, min(hi, 19 if real else 20) + 1))  # N <= 2^20
+        logn = logc + (1 if real else 0)
+        b = int(rng.integers(1, min(40, max(1, (1 << 21) >> logn)) + 1))
+        td = "forward" if tt == "r2c" else ("inverse" if tt == "c2r" else ("forward", "inverse")[int(rng.integers(2))])
+        norm = NORMS[int(rng.integers(4))]
+        block, params = 256, {}
+        if name in ("fft_dit", "fft_dif", "fft_dit_radix4", "fft_dif_radix4"):
+            block = (64, 128, 256, 512, 1024)[int(rng.integers(5))]
+        elif name == "fft_lds_fused":
+            params = {"elems": (0, 4, 8, 16, 32)[int(rng.integers(5))], "stagger": (0, 0, 1, 3)[int(rng.integers(4))]}
+        else:
+            params = {"n1": (0, 16, 32, 64, 128, 256, 512, 1024)[int(rng.integers(8))],
+                      "chunk_rows": (0, 0, 1, 2, 3, 5)[int(rng.integers(6))], "schedule": int(rng.integers(2))}
+        out.append(pytest.param(i, name, tt, td, norm, 1 << logn, b, block, params,
+                                id=f"{i}-{name}-{tt}-{td}-{norm}-N{1 << logn}-B{b}"))
+    return out
+
+
+def _reference(x, tt, td, norm, n):
+    if tt == "c2c":
+        return oracle.c2c(x, td, norm) if n <= 4096 else _np_c2c(x, td, norm)
+    np_norm = {"none": "backward" if tt == "r2c" else "forward", "forward": "forward", "backward": "backward",
+               "ortho": "ortho"}[norm]
+    if tt == "r2c":
+        return np.fft.rfft(x.astype(np.float64), norm=np_norm)
+    return np.fft.irfft(x.astype(np.complex128), n=n, norm=np_norm)
+
+
+def _np_c2c(x, td, norm):
+    x = x.astype(np.complex128)
+    n = x.shape[-1]
+    if td == "forward":
+        return np.fft.fft(x, norm="backward" if norm == "none" else norm)
+    if norm in ("none", "forward"):
+        return np.fft.ifft(x, norm="backward") * n
+    return np.fft.ifft(x, norm=norm)
+
+
+@pytest.mark.parametrize("case,name,tt,td,norm,n,b,block,params", _cases())
+def test_random_configuration(gpu, case, name, tt, td, norm, n, b, block, params):
+    rng = np.random.default_rng(7000 + case)
+    m = n // 2 + 1 if tt == "c2r" else n
+    if tt == "r2c":
+        h = rng.standard_normal((b, n)).astype(np.float32)
+    else:
+        h = (rng.standard_normal((b, m)) + 1j * rng.standard_normal((b, m))).astype(np.complex64)
+    if b == 1:
+        h = h[0]
+    plan = ExecutionPlan(n=n, batch=b, direction="dit", precision="fp32", selection_source="table",
+                         reason="random configuration", fallback=False,
+                         executed=name + ("_batch" if b > 1 else ""), block=block, flow_id="test",
+                         flow_realization="test", processing_unit="test", params=params, transform_type=tt,
+                         transform_direction=td, norm=norm)
+    y = execute_fft_plan(plan, torch.from_numpy(h).to(gpu)).cpu().numpy()
+    ref = _reference(h, tt, td, norm, n)
+    l2 = oracle.rel_l2(y, ref)
+    mx = oracle.max_rel_error(y, ref)
+    assert l2 <= TOL and mx <= TOL, f"rel_l2={l2:.3e} max_rel={mx:.3e}"
