@@ -102,7 +102,11 @@ enum {
  *                                    the XCD whose L2 holds its pass-1 output
  *                                    (n1, n2 in [128, 512] within 2x; one
  *                                    execute of such a plan at a time: its
- *                                    counters live in the plan) */
+ *                                    counters live in the plan),
+ *                        params[3] = pass-2 row order: 0 = forward; 1 =
+ *                                    reverse, so the batch rows pass 1 wrote
+ *                                    last (the most likely still in the
+ *                                    MALL) are read first (schedules 0, 1) */
 #define MFFT_MAX_PARAMS 4
 
 typedef struct mfft_plan mfft_plan;

@@ -110,6 +110,7 @@ class DesignSpace:
     fourstep_chunk_rows: tuple
     fourstep_min_n: int
     fourstep_schedule: tuple
+    fourstep_pass2_order: tuple
     batch_candidates: tuple
     batch_variants: tuple
     layout_in: str
@@ -139,6 +140,9 @@ class DesignSpace:
         sched = fs.get("schedule", [0])
         _require(isinstance(sched, list) and sched and all(v in (0, 1, 2) for v in sched),
                  "butterfly_space.json: P.four_step.schedule must be a list of 0/1/2")
+        order = fs.get("pass2_order", [0])
+        _require(isinstance(order, list) and order and all(v in (0, 1) for v in order),
+                 "butterfly_space.json: P.four_step.pass2_order must be a list of 0/1")
         b = p.get("batch_expansion", {})
         _require(_pow2_list(b.get("candidates")), "butterfly_space.json: P.batch_expansion.candidates must be powers of two")
         variants = b.get("variants", [])
@@ -152,7 +156,7 @@ class DesignSpace:
             stage_blocks=tuple(st["blocks"]), lds_elems=tuple(lds["elems"]), lds_max_n=lds["max_n"],
             lds_stagger=tuple(stag),
             fourstep_n1=tuple(fs["n1"]), fourstep_chunk_rows=tuple(ch), fourstep_min_n=fs["min_n"],
-            fourstep_schedule=tuple(sched),
+            fourstep_schedule=tuple(sched), fourstep_pass2_order=tuple(order),
             batch_candidates=tuple(b["candidates"]), batch_variants=tuple(variants),
             layout_in=lay["in"][0], layout_out=lay["out"][0],
         )

@@ -336,13 +336,16 @@ template <int LOGL, int LOGE, int LOGC, int DIR, int KIND>
 __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_pass_kernel(
     const float2* src, float2* dst, const float2* __restrict__ tw,
     const float2* __restrict__ tw_lo, const float2* __restrict__ tw_hi, int tw_h, int logn,
-    int log_s, float scale) {
+    int log_s, float scale, int rev) {
     using C = ColCfg<LOGL, LOGE, LOGC>;
     __shared__ float2 lds[C::LDS_FLOAT2];
     const int groups = (1 << log_s) >> LOGC;  // column groups per transform
     const int bid = xcd_pair_block((int)blockIdx.x, (int)gridDim.x);
-    const int64_t row = bid / groups;
-    const int c0 = (bid - (int)(row * groups)) << LOGC;
+    const int64_t row0 = bid / groups;
+    const int c0 = (bid - (int)(row0 * groups)) << LOGC;
+    // pass 2 in reverse row order (rev): the rows pass 1 wrote last, whose Z
+    // is the most likely to be still in the MALL, go first
+    const int64_t row = (KIND == 1 && rev) ? (int64_t)((int)gridDim.x / groups) - 1 - row0 : row0;
     const int tid = threadIdx.x;
     const int c = tid & (C::C - 1);
     const int j = tid >> LOGC;
@@ -371,7 +374,7 @@ template <int LOGL, int LOGE, int LOGC, int DIR, int KIND>
 __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG), 4) void fourstep_persist_kernel(
     const float2* src, float2* dst, const float2* __restrict__ tw,
     const float2* __restrict__ tw_lo, const float2* __restrict__ tw_hi, int tw_h, int logn,
-    int log_s, float scale, int64_t tiles) {
+    int log_s, float scale, int64_t tiles, int rev) {
     using C = ColCfg<LOGL, LOGE, LOGC>;
     __shared__ float2 lds[C::LDS_FLOAT2];
     __shared__ float2 lds_tw[C::TW_SIZE > 0 ? C::TW_SIZE : 1];
@@ -382,12 +385,15 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG), 4) void fourstep_pe
     const int64_t stride = gridDim.x;
     const int64_t t0 = xcd_pair_block((int)blockIdx.x, (int)gridDim.x);
     const int c0 = (int)(t0 & ((1 << log_groups) - 1)) << LOGC;
+    // batch row of tile t; pass 2 walks the rows in reverse order with rev
+    const int64_t last_row = (tiles >> log_groups) - 1;
+    auto row_of = [&](int64_t t) { return (KIND == 1 && rev) ? last_row - (t >> log_groups) : (t >> log_groups); };
 
     for (int i = tid; i < C::TW_SIZE; i += C::WG) lds_tw[i] = tw[i];
     BigTw<C> f;
     if constexpr (KIND == 0) big_tw_load<C>(f, tw_lo, tw_hi, tw_h, (uint32_t)(c0 + c), j);
     float2 v[C::E];
-    col_load<C>(v, src + ((t0 >> log_groups) << logn) + c0, c, j, log_s);
+    col_load<C>(v, src + (row_of(t0) << logn) + c0, c, j, log_s);
     __syncthreads();  // lds_tw complete
 
     // one column group: transform v (group t) and store it.  Per-call copies
@@ -402,15 +408,14 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG), 4) void fourstep_pe
             static_for<0, C::LR_LAST>([&](auto i) { fl.sp[i.value] = opaque(f.sp[i.value]); });
             return fl;
         });
-        const int64_t base = (t >> log_groups) << logn;
+        const int64_t base = row_of(t) << logn;
         col_store<C, KIND>(v, dst + opaque_uniform(KIND == 0 ? base + ((int64_t)c0 << LOGL) : base + c0), lds, tl, cl,
                            jl, log_s, scale);
     };
     int64_t t = t0;
     for (; t + stride < tiles; t += stride) {
         float2 vn[C::E];
-        col_load<C>(vn, src + opaque_uniform((((t + stride) >> log_groups) << logn) + c0), opaque(c), opaque(j),
-                    log_s);
+        col_load<C>(vn, src + opaque_uniform((row_of(t + stride) << logn) + c0), opaque(c), opaque(j), log_s);
         process(t);
         static_for<0, C::E>([&](auto r) { v[r.value] = vn[r.value]; });
     }
@@ -565,10 +570,10 @@ hipError_t launch_pass(const float2* src, float2* dst, const mfft_plan* p, int64
         if (g < unit) g = unit;
         if (g > tiles) g = tiles;
         fourstep_persist_kernel<LOGL, LOGE, LOGC, DIR, KIND><<<(unsigned)g, C::WG, 0, stream>>>(
-            src, dst, tw, p->tw_lo, p->tw_hi, p->tw_h, logn, log_s, scale, tiles);
+            src, dst, tw, p->tw_lo, p->tw_hi, p->tw_h, logn, log_s, scale, tiles, p->pass2_rev);
     } else {
         fourstep_pass_kernel<LOGL, LOGE, LOGC, DIR, KIND><<<(unsigned)tiles, C::WG, 0, stream>>>(
-            src, dst, tw, p->tw_lo, p->tw_hi, p->tw_h, logn, log_s, scale);
+            src, dst, tw, p->tw_lo, p->tw_hi, p->tw_h, logn, log_s, scale, p->pass2_rev);
     }
     mark(stream);
     return hipGetLastError();

@@ -21,6 +21,7 @@ struct mfft_plan {
     int launches = 0;
     int64_t n1 = 0, n2 = 0, chunk_rows = 0;
     int schedule = 0;    // FOUR_STEP: 0 one column group per block, 1 persistent, 2 fused (one launch)
+    int pass2_rev = 0;   // FOUR_STEP: pass 2 walks the batch rows in reverse order
     int num_cus = 0;     // compute units of `device` (persistent / fused grid size)
     int clock_khz = 0;   // constant wall-clock rate of `device` (fused schedule wait bound)
     bool r2c_fused = false, c2r_fused = false;

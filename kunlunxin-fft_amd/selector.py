@@ -120,6 +120,9 @@ def entry_contract_violations(entry: dict) -> list[str]:
         sched = params.get("schedule", 0)
         if sched not in sp.fourstep_schedule:
             bad.append(f"schedule {sched!r} not in {sp.fourstep_schedule}")
+        order = params.get("pass2_order", 0)
+        if order not in sp.fourstep_pass2_order:
+            bad.append(f"pass2_order {order!r} not in {sp.fourstep_pass2_order}")
         if isinstance(n, int) and n < sp.fourstep_min_n:
             bad.append(f"N={n} below the four-step minimum {sp.fourstep_min_n}")
     if "variant" in params and params["variant"] not in sp.batch_variants:

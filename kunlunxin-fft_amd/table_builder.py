@@ -6,9 +6,9 @@ For every cell (N, batch, direction) it times the M0 incumbent (fft_dit /
 fft_dif and their batch forms) and every legal challenger of the published
 design space (config/butterfly_space.json): the radix-4 global-stage flow,
 the single-pass LDS kernel at each elements-per-thread setting (and start
-stagger, where it can act), and the
-four-step at each split, chunking and schedule (one column group per
-workgroup, persistent workgroups, or both passes fused per XCD).  The fastest challenger is promoted
+stagger, where it can act), and the four-step at each split, chunking,
+schedule (one column group per workgroup, persistent workgroups, or both
+passes fused per XCD) and pass-2 row order.  The fastest challenger is promoted
 only when it beats the incumbent by at least GUARD_PCT percent (M0 closure);
 otherwise the cell keeps M0.  The table is bound to the device profile hash
 and the live environment fingerprint, so it selects only on the stack it was
@@ -95,17 +95,22 @@ def candidates(n: int, b: int, direction: str, space):
             chunks = [0]
             if b >= 16 and n >= (1 << 14):
                 chunks += [c for c in space.fourstep_chunk_rows if c and c < b and n * c * 8 >= (16 << 20)
-                           and n * c * 8 <= (128 << 20)]
+                           and n * c * 8 <= (256 << 20)]
             l1, l2 = int(math.log2(n1)), int(math.log2(n2))
             for ch in chunks:
                 for sched in space.fourstep_schedule:
                     if sched == 2 and not (7 <= l1 <= 9 and 7 <= l2 <= 9 and abs(l1 - l2) <= 1):
                         continue
-                    params = {"n1": n1, "chunk_rows": ch}
-                    if sched:
-                        params["schedule"] = sched
-                    out.append((f"{('fs', 'fsp', 'fsf')[sched]}_n1_{n1}_c{ch}", "fft_four_step" + sfx, 256, params,
-                                ("four-step", "stockham-radix16", "four-step-two-pass")))
+                    # the reverse pass-2 row order only matters with more than one row
+                    for order in (space.fourstep_pass2_order if b > 1 and sched != 2 else (0,)):
+                        params = {"n1": n1, "chunk_rows": ch}
+                        if sched:
+                            params["schedule"] = sched
+                        if order:
+                            params["pass2_order"] = order
+                        out.append((f"{('fs', 'fsp', 'fsf')[sched]}_n1_{n1}_c{ch}" + ("_r" if order else ""),
+                                    "fft_four_step" + sfx, 256, params,
+                                    ("four-step", "stockham-radix16", "four-step-two-pass")))
     return out
 
 

@@ -167,6 +167,24 @@ def test_four_step_split_and_chunk_neutral(gpu, n, n1, chunk):
     check(y, np.fft.fft(x.astype(np.complex128)), f"four-step N={n} n1={n1} chunk={chunk}")
 
 
+@pytest.mark.parametrize("n,n1", [(1 << 12, 64), (1 << 16, 256), (1 << 18, 512), (1 << 20, 1024)])
+@pytest.mark.parametrize("chunk,sched", [(0, 0), (2, 0), (0, 1), (3, 1)])
+def test_four_step_reverse_pass2_order(gpu, n, n1, chunk, sched):
+    """pass2_order 1 (pass 2 walks the batch rows last-written first) only
+    reorders whole rows between workgroups: results equal the forward
+    order's bit for bit, chunked or not, per-group or persistent."""
+    b = 7 if n <= (1 << 16) else 3
+    x = torch.from_numpy(seeded_c64(n, b, session=7)).to(gpu)
+    base = {"n1": n1, "chunk_rows": chunk, "schedule": sched}
+    y0 = execute_fft_plan(mkplan("fft_four_step_batch", n, b, params=base), x)
+    y1 = execute_fft_plan(mkplan("fft_four_step_batch", n, b, params={**base, "pass2_order": 1}), x)
+    assert torch.equal(y0, y1)
+    check(y1.cpu().numpy(), np.fft.fft(x.cpu().numpy().astype(np.complex128)), f"reverse N={n} chunk={chunk}")
+    yi = execute_fft_plan(mkplan("fft_four_step_batch", n, b, td="inverse", norm="ortho",
+                                 params={**base, "pass2_order": 1}), x)
+    check(yi.cpu().numpy(), np_ref(x.cpu().numpy(), "inverse", "ortho"), f"reverse inverse N={n}")
+
+
 @pytest.mark.parametrize("n,n1", [(256, 16), (1 << 10, 32), (1 << 12, 64), (1 << 14, 128), (1 << 15, 128),
                                   (1 << 15, 256), (1 << 16, 256), (1 << 17, 256), (1 << 17, 512),
                                   (1 << 18, 512), (1 << 19, 512), (1 << 19, 1024), (1 << 20, 1024)])
