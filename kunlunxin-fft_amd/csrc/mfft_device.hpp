@@ -161,6 +161,20 @@ constexpr int sched_tw_size(int logl, int le) { return sched_tw_off(logl, le, sc
 // highest power of two <= q (q >= 1)
 constexpr int high_bit(int q) { return q <= 1 ? 1 : 2 * high_bit(q >> 1); }
 
+// Non-temporal (streaming) global access of one complex64: the `nt` form
+// of the load/store, whose lines are not kept in the caches on a miss.  Data
+// read exactly once uses it so that it does not evict what a later pass
+// still reads (the four-step's intermediate in the 256 MB MALL).
+typedef float nt_float2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float2 load_nt(const float2* p) {
+    const nt_float2 v = __builtin_nontemporal_load(reinterpret_cast<const nt_float2*>(p));
+    return make_float2(v.x, v.y);
+}
+__device__ __forceinline__ void store_nt(float2* p, float2 x) {
+    const nt_float2 v = {x.x, x.y};
+    __builtin_nontemporal_store(v, reinterpret_cast<nt_float2*>(p));
+}
+
 // Multiply v[OFF + q] (q = 1..R-1) by W^(q*k) of a pass whose table rows
 // `tp[i*NS + k]` hold W^(2^i * k): loads the log2(R) power-of-two roots
 // (coalesced across lanes) and composes the rest, w_q = w_(q - hb) * w_hb,
