@@ -2,10 +2,10 @@
 
 Each case draws a runner (M0, M5, LDS, four-step), a transform type and
 direction, a norm, N, a ragged batch, and the runner's parameters (threads
-per block, elements per thread, start stagger, n1, chunk rows, schedule) from
-their published ranges (N <= 2^20), then checks the GPU result to the north-star gate
-(rel-L2 and peak-normalised worst element <= 1e-5).  Sizes stay small enough
-(N * B <= 2^21) that the whole set runs in seconds.
+per block, elements per thread, start stagger, n1, chunk rows, schedule, pass-2
+row order) from their published ranges (N <= 2^20), then checks the GPU result
+to the north-star gate (rel-L2 and peak-normalised worst element <= 1e-5).
+Sizes stay small enough (N * B <= 2^21) that the whole set runs in seconds.
 """
 import numpy as np
 import pytest
@@ -42,7 +42,8 @@ def _cases(count=160, seed=20261202):
             params = {"elems": (0, 4, 8, 16, 32)[int(rng.integers(5))], "stagger": (0, 0, 1, 3)[int(rng.integers(4))]}
         else:
             params = {"n1": (0, 16, 32, 64, 128, 256, 512, 1024)[int(rng.integers(8))],
-                      "chunk_rows": (0, 0, 1, 2, 3, 5)[int(rng.integers(6))], "schedule": int(rng.integers(2))}
+                      "chunk_rows": (0, 0, 1, 2, 3, 5)[int(rng.integers(6))], "schedule": int(rng.integers(2)),
+                      "pass2_order": int(rng.integers(2))}
         out.append(pytest.param(i, name, tt, td, norm, 1 << logn, b, block, params,
                                 id=f"{i}-{name}-{tt}-{td}-{norm}-N{1 << logn}-B{b}"))
     return out
