@@ -77,9 +77,9 @@ def candidates(n: int, b: int, direction: str, space):
             if n <= 16 and e != 16:
                 continue
             # the start stagger acts on launches of two or more waves of
-            # workgroups with at most four workgroups per CU: 2^13..2^15 points
-            # at 16 or 32 elements per thread, in large batches
-            stags = [s for s in space.lds_stagger if s == 0 or (e >= 16 and logn >= 13 and n * b >= (1 << 24))]
+            # workgroups with at most four workgroups per CU: 16 or 32
+            # elements per thread, in large batches
+            stags = [s for s in space.lds_stagger if s == 0 or (e >= 16 and logn >= 10 and n * b >= (1 << 24))]
             for stg in stags:
                 params = {"elems": e} if stg == 0 else {"elems": e, "stagger": stg}
                 out.append((f"lds_e{e}" + (f"_s{stg}" if stg else ""), "fft_lds_fused" + sfx, 256, params,
