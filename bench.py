@@ -4,7 +4,8 @@ p50 latency at N=2048 B=1 (the reference's headline metric), on one MI355X.
 One step = one forward C2C complex64 transform (through the public plan API:
 ``plan_fft`` with the device profile -> ``execute_fft_plan``) of every size
 N = 2^10 .. 2^20 at B = max(64, 2^25 / N) rows -- 256 MiB in and 256 MiB out
-per size, larger than the 256 MB Infinity Cache.  Inputs are synthetic
+per size (512 MiB each way at 2^20, where B = 64), no less than the 256 MB
+Infinity Cache.  Inputs are synthetic
 (iid N(0,1) real/imag parts from a fixed device-side seed) and resident in
 HBM before the timed region.  ``value`` = algorithmic bytes of all K steps
 (16*N*B per transform) / timed wall time, in GB/s.
@@ -333,7 +334,7 @@ def main() -> int:
         "data": "synthetic: iid N(0,1) real/imag parts, fixed device seed, resident in HBM",
         "config": {"workload": "forward C2C complex64 via plan_fft/execute_fft_plan, "
                                "N=2^10..2^20, B=max(64, 2^25/N) per N (256 MiB in + 256 MiB out "
-                               "per N); one step = all 11 sizes",
+                               "per N, 512 MiB each way at 2^20); one step = all 11 sizes",
                    "frac_hbm_of_value": round(value / PEAK_GBPS, 4),
                    "d2d_copy_gbps": round(copy_gbps, 1),
                    "frac_of_d2d_copy": round(value / copy_gbps, 4)},
