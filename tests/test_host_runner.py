@@ -1,0 +1,98 @@
+"""Host logic between the plan and the C ABI: runner parameters -> native
+flow parameters, the selector's design-space contract for them, and the
+table builder's candidate set.  No GPU needed."""
+import json
+import os
+
+import pytest
+
+from kunlunxin_fft_amd import native
+from kunlunxin_fft_amd.config import DesignSpace
+from kunlunxin_fft_amd.runner import flow_params
+from kunlunxin_fft_amd.selector import entry_contract_violations
+from kunlunxin_fft_amd.table_builder import candidates
+
+
+def test_lds_params_map_to_elems_and_stagger():
+    assert flow_params("fft_lds_fused_batch", 4096, "c2c", 256, {"elems": 16, "stagger": 2}) == \
+        (native.FLOW_LDS_FUSED, (16, 2))
+    # 32 elements need >= 1024 points; 2^13..2^14 take 16 or 32; 2^15 only 32
+    assert flow_params("fft_lds_fused", 512, "c2c", 256, {"elems": 32})[1] == (0, 0)
+    assert flow_params("fft_lds_fused", 8192, "c2c", 256, {"elems": 8})[1] == (0, 0)
+    assert flow_params("fft_lds_fused", 32768, "c2c", 256, {"elems": 16, "stagger": 3})[1] == (0, 3)
+    # a real transform's core is n/2; r2c cores stop at 16384 and never take 32
+    assert flow_params("fft_lds_fused", 2048, "r2c", 256, {"elems": 32})[1] == (0, 0)
+    assert flow_params("fft_lds_fused", 1 << 16, "r2c", 256, {})[0] == native.FLOW_AUTO
+    assert flow_params("fft_lds_fused", 1 << 16, "c2r", 256, {})[0] == native.FLOW_LDS_FUSED
+
+
+def test_four_step_params_map_to_split_chunk_schedule_order():
+    p = {"n1": 512, "chunk_rows": 32, "schedule": 1, "pass2_order": 1}
+    assert flow_params("fft_four_step_batch", 1 << 18, "c2c", 256, p) == (native.FLOW_FOUR_STEP, (512, 32, 1, 1))
+    # an n1 that leaves n2 outside [16, 1024] falls back to the library's split
+    assert flow_params("fft_four_step", 1 << 20, "c2c", 256, {"n1": 256})[1][0] == 0
+    # the fused schedule only where both factors are 2^7..2^9 within 2x
+    assert flow_params("fft_four_step", 1 << 20, "c2c", 256, {"n1": 1024, "schedule": 2})[1][2] == 0
+    assert flow_params("fft_four_step", 1 << 16, "c2c", 256, {"n1": 256, "schedule": 2})[1][2] == 2
+    # cores below 256 points leave the flow to the library
+    assert flow_params("fft_four_step", 256, "r2c", 256, {})[0] == native.FLOW_AUTO
+
+
+def test_stage_flows_validate_the_block():
+    assert flow_params("fft_dit_batch", 1024, "c2c", 512, {}) == (native.FLOW_RADIX2_DIT, (512,))
+    with pytest.raises(ValueError):
+        flow_params("fft_dit", 1024, "c2c", 32, {})
+    with pytest.raises(ValueError):
+        flow_params("fft_dit", 1024, "c2c", 96, {})
+    with pytest.raises(ValueError):
+        flow_params("no_such_runner", 1024, "c2c", 256, {})
+
+
+def _entry(params, real="lds-resident", unit="stockham-radix16", n=1 << 14, b=2048, executed="fft_lds_fused_batch"):
+    return {"N": n, "batch": b, "direction": "dit", "block": 256, "flow_id": "x", "flow_realization": real,
+            "processing_unit": unit, "params": dict(params, variant="folded"), "executed": executed,
+            "incumbent_ms": 1.0, "challenger_ms": 0.5, "reason": "test"}
+
+
+def test_contract_accepts_published_params_and_refuses_others():
+    sp = DesignSpace.load()
+    ok = _entry({"elems": 32, "stagger": max(sp.lds_stagger)})
+    assert not [v for v in entry_contract_violations(ok) if "stagger" in v]
+    bad = _entry({"elems": 32, "stagger": 7})
+    assert any("stagger" in v for v in entry_contract_violations(bad))
+    fs = _entry({"n1": 512, "chunk_rows": 0, "pass2_order": 1}, real="four-step", n=1 << 18, b=128,
+                executed="fft_four_step_batch")
+    assert not [v for v in entry_contract_violations(fs) if "pass2_order" in v]
+    fs_bad = _entry({"n1": 512, "chunk_rows": 0, "pass2_order": 2}, real="four-step", n=1 << 18, b=128,
+                    executed="fft_four_step_batch")
+    assert any("pass2_order" in v for v in entry_contract_violations(fs_bad))
+
+
+def test_builder_offers_stagger_and_row_order_only_where_they_act():
+    sp = DesignSpace.load()
+    big = [c for c in candidates(1 << 15, 1024, "dit", sp) if c[1].startswith("fft_lds")]
+    assert {c[3].get("stagger", 0) for c in big} == set(sp.lds_stagger)
+    small = [c for c in candidates(1 << 15, 16, "dit", sp) if c[1].startswith("fft_lds")]
+    assert {c[3].get("stagger", 0) for c in small} == {0}
+    fs_batch = [c for c in candidates(1 << 18, 128, "dit", sp) if c[1].startswith("fft_four_step")]
+    assert {c[3].get("pass2_order", 0) for c in fs_batch} == set(sp.fourstep_pass2_order)
+    assert all(c[3].get("schedule", 0) in sp.fourstep_schedule for c in fs_batch)
+    fs_one = [c for c in candidates(1 << 18, 1, "dit", sp) if c[1].startswith("fft_four_step")]
+    assert {c[3].get("pass2_order", 0) for c in fs_one} == {0}
+    # every candidate's parameters pass the loader's own contract
+    for c in big + fs_batch:
+        label, name, block, params, (real, unit, flow_id) = c
+        e = _entry(params, real=real, unit=unit, n=1 << (15 if name.startswith("fft_lds") else 18),
+                   b=1024 if name.startswith("fft_lds") else 128, executed=name)
+        assert not entry_contract_violations(e), (label, entry_contract_violations(e))
+
+
+def test_shipped_table_uses_only_published_params():
+    sp = DesignSpace.load()
+    path = os.path.join(os.path.dirname(__file__), "..", "kunlunxin-fft_amd", "config", "selector_table.json")
+    t = json.load(open(path))
+    for e in t["entries"]:
+        p = e["params"]
+        assert p.get("stagger", 0) in (0,) + sp.lds_stagger
+        assert p.get("pass2_order", 0) in sp.fourstep_pass2_order
+        assert p.get("schedule", 0) in sp.fourstep_schedule
