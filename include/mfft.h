@@ -37,8 +37,8 @@
  * device that was current at plan creation, which must be current at
  * execute.  `in` and `out` must not overlap; `in` is never written.
  * Executes of one plan that overlap in time (two streams or two host threads)
- * share the plan's workspace and race: serialise them, or create one plan per
- * stream.
+ * share the plan's workspace and race: serialise them, give each its own
+ * workspace (mfft_execute_ws), or create one plan per stream.
  */
 #ifndef MFFT_H_
 #define MFFT_H_
@@ -153,6 +153,35 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
 
 /* Enqueue one transform of all `batch` rows.  No allocation, no host sync. */
 int mfft_execute(const mfft_plan* plan, const void* in, void* out, void* stream);
+
+/* Caller-owned workspace.  The reference exposes neither a stream nor a
+ * workspace (its execute_fft_plan, src/xpu/entry.py:501-628, allocates per
+ * call on the framework's stream); these entry points close that gap for
+ * callers that manage device memory themselves.  A plan needs workspace only
+ * for the stage flows (RADIX2/RADIX4: one batch x core_n complex64 buffer)
+ * and for real transforms whose core is not fused into the LDS kernel (one
+ * more such buffer); LDS_FUSED and FOUR_STEP C2C need none.
+ *
+ * mfft_plan_create_ex: mfft_plan_create with `flags`; with
+ * MFFT_PLAN_CALLER_WORKSPACE the plan allocates only its twiddle tables (and
+ * the fused four-step's counters), and every execute of a plan that needs
+ * workspace must go through mfft_execute_ws (mfft_execute refuses it). */
+#define MFFT_PLAN_CALLER_WORKSPACE 1
+int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform_type,
+                        int transform_direction, int norm, int flow,
+                        const int32_t* params, int nparams, int flags);
+
+/* Bytes of workspace an execute of this plan needs (0: none). */
+int mfft_plan_workspace_size(const mfft_plan* plan, int64_t* bytes);
+
+/* mfft_execute with the caller's workspace instead of the plan's own:
+ * `workspace` is device memory on the plan's device, 256-byte aligned, of at
+ * least mfft_plan_workspace_size bytes, overlapping neither `in` nor `out`
+ * (it may be NULL when that size is 0).  The library only uses it for the
+ * duration of the enqueued work, so executes of one plan on different
+ * streams with different workspaces do not race. */
+int mfft_execute_ws(const mfft_plan* plan, const void* in, void* out, void* workspace,
+                    int64_t workspace_bytes, void* stream);
 
 /* mfft_execute with a HIP event recorded on `stream` before the first and
  * after every kernel launch (the profiling counterpart of the reference's

@@ -121,20 +121,30 @@ bool is_stage_flow(int f) {
            f == MFFT_FLOW_RADIX4_DIF;
 }
 
+// Alignment of a caller workspace and of the ws_b offset inside it.
+constexpr int64_t kWorkAlign = 256;
+
+// The scratch of one execute: the plan's own, or carved out of a caller's
+// workspace.
+struct Work {
+    float2* a;  // core-sized: the core output (r2c) or input (c2r) of a non-fused real flow
+    float2* b;  // core-sized: stage-flow ping-pong
+};
+
 // Enqueue the complex core of length p->core_n over `rows` rows.
-int run_core(const mfft_plan* p, const float2* src, float2* dst, int dir, float scale,
+int run_core(const mfft_plan* p, const float2* src, float2* dst, int dir, float scale, const Work& w,
              hipStream_t stream) {
     hipError_t e = hipSuccess;
     int launches = 0;
     switch (p->flow) {
         case MFFT_FLOW_RADIX2_DIT:
         case MFFT_FLOW_RADIX2_DIF:
-            e = mfft::launch_radix2(p->flow == MFFT_FLOW_RADIX2_DIF, dir, src, dst, p->ws_b, p->tw,
+            e = mfft::launch_radix2(p->flow == MFFT_FLOW_RADIX2_DIF, dir, src, dst, w.b, p->tw,
                                     p->core_n, p->batch, scale, p->block, stream, &launches);
             break;
         case MFFT_FLOW_RADIX4_DIT:
         case MFFT_FLOW_RADIX4_DIF:
-            e = mfft::launch_radix4(p->flow == MFFT_FLOW_RADIX4_DIF, dir, src, dst, p->ws_b, p->tw,
+            e = mfft::launch_radix4(p->flow == MFFT_FLOW_RADIX4_DIF, dir, src, dst, w.b, p->tw,
                                     p->core_n, p->batch, scale, p->block, stream, &launches);
             break;
         case MFFT_FLOW_LDS_FUSED:
@@ -151,6 +161,65 @@ int run_core(const mfft_plan* p, const float2* src, float2* dst, int dir, float 
     return MFFT_OK;
 }
 
+// One execute with the scratch `w`; ws/ws_bytes: the caller's workspace
+// (checked against in and out), or NULL for the plan's own.
+int execute_impl(const mfft_plan* p, const void* in, void* out, const Work& w, void* stream_v,
+                 const void* ws = nullptr, int64_t ws_bytes = 0) {
+    if (!in || !out) return fail(MFFT_ERR_VALUE, "in and out must not be NULL");
+    const size_t in_bytes = (size_t)p->batch *
+        (p->transform_type == MFFT_R2C ? (size_t)p->n * 4
+         : p->transform_type == MFFT_C2R ? (size_t)(p->n / 2 + 1) * 8 : (size_t)p->n * 8);
+    const size_t out_bytes = (size_t)p->batch *
+        (p->transform_type == MFFT_R2C ? (size_t)(p->n / 2 + 1) * 8
+         : p->transform_type == MFFT_C2R ? (size_t)p->n * 4 : (size_t)p->n * 8);
+    const char* ib = (const char*)in;
+    const char* ob = (const char*)out;
+    if (ib < ob + out_bytes && ob < ib + in_bytes)
+        return fail(MFFT_ERR_VALUE, "in and out must not overlap");
+    if (ws) {
+        const char* wb = (const char*)ws;
+        if ((wb < ib + in_bytes && ib < wb + ws_bytes) || (wb < ob + out_bytes && ob < wb + ws_bytes))
+            return fail(MFFT_ERR_VALUE, "the workspace must not overlap in or out");
+    }
+    if ((((uintptr_t)in) & 7) && p->transform_type != MFFT_R2C)
+        return fail(MFFT_ERR_VALUE, "complex input must be 8-byte aligned");
+    if ((((uintptr_t)in) & 7) && p->transform_type == MFFT_R2C)
+        return fail(MFFT_ERR_VALUE, "r2c input must be 8-byte aligned (pairs are read as complex)");
+    if (((uintptr_t)out) & 7) return fail(MFFT_ERR_VALUE, "output must be 8-byte aligned");
+    int dev = -1;
+    hipError_t he = hipGetDevice(&dev);
+    if (he != hipSuccess) return hip_fail(he, "hipGetDevice");
+    if (dev != p->device)
+        return fail(MFFT_ERR_RUNTIME, "plan was created on device %d but device %d is current", p->device, dev);
+    hipStream_t stream = (hipStream_t)stream_v;
+    const int dir = p->transform_direction == MFFT_FORWARD ? -1 : 1;
+
+    if (p->transform_type == MFFT_C2C)
+        return run_core(p, (const float2*)in, (float2*)out, dir, p->scale, w, stream);
+
+    const int logc = mfft::ilog2((int)p->core_n);
+    if (p->transform_type == MFFT_R2C) {
+        if (p->r2c_fused) {
+            he = mfft::launch_lds(1, -1, logc, p->elems, in, out, p->tw, p->tw_real, p->batch, p->scale, stream,
+                                  p->num_cus, p->stagger);
+            return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
+        }
+        int rc = run_core(p, (const float2*)in, w.a, -1, 1.0f, w, stream);
+        if (rc != MFFT_OK) return rc;
+        he = mfft::launch_r2c_stitch(w.a, (float2*)out, p->tw_real, p->n, p->batch, p->scale, stream);
+        return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
+    }
+    // c2r
+    if (p->c2r_fused) {
+        he = mfft::launch_lds(2, 1, logc, p->elems, in, out, p->tw, p->tw_real, p->batch, p->scale, stream,
+                              p->num_cus, p->stagger);
+        return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
+    }
+    he = mfft::launch_c2r_pre((const float2*)in, w.a, p->tw_real, p->n, p->batch, stream);
+    if (he != hipSuccess) return hip_fail(he, "kernel launch");
+    return run_core(p, w.a, (float2*)out, 1, p->scale, w, stream);
+}
+
 }  // namespace
 
 extern "C" {
@@ -161,9 +230,15 @@ const char* mfft_last_error(void) { return g_err.c_str(); }
 
 int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_type,
                      int transform_direction, int norm, int flow, const int32_t* params, int nparams) {
+    return mfft_plan_create_ex(out, n, batch, transform_type, transform_direction, norm, flow, params, nparams, 0);
+}
+
+int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform_type, int transform_direction,
+                        int norm, int flow, const int32_t* params, int nparams, int flags) {
     g_err.clear();
     if (!out) return fail(MFFT_ERR_VALUE, "out must not be NULL");
     *out = nullptr;
+    if (flags & ~MFFT_PLAN_CALLER_WORKSPACE) return fail(MFFT_ERR_VALUE, "unknown plan flags 0x%x", flags);
     if (transform_type < MFFT_C2C || transform_type > MFFT_C2R)
         return fail(MFFT_ERR_VALUE, "unsupported transform_type %d", transform_type);
     if (transform_direction != MFFT_FORWARD && transform_direction != MFFT_INVERSE)
@@ -338,12 +413,18 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
     const size_t core_bytes = (size_t)batch * (size_t)core_n * sizeof(float2);
     const bool need_a = real && !(p->r2c_fused || p->c2r_fused);
     const bool need_b = is_stage_flow(flow);
-    if (rc == MFFT_OK && need_a) {
+    p->need_a = need_a;
+    p->need_b = need_b;
+    p->core_bytes = (int64_t)core_bytes;
+    p->work_b_off = need_a ? (p->core_bytes + kWorkAlign - 1) / kWorkAlign * kWorkAlign : 0;
+    p->work_bytes = need_b ? p->work_b_off + p->core_bytes : (need_a ? p->core_bytes : 0);
+    p->caller_ws = (flags & MFFT_PLAN_CALLER_WORKSPACE) != 0;
+    if (rc == MFFT_OK && need_a && !p->caller_ws) {
         he = hipMalloc((void**)&p->ws_a, core_bytes);
         if (he != hipSuccess) rc = hip_fail(he, "hipMalloc(workspace)");
         else p->ws_bytes += (int64_t)core_bytes;
     }
-    if (rc == MFFT_OK && need_b) {
+    if (rc == MFFT_OK && need_b && !p->caller_ws) {
         he = hipMalloc((void**)&p->ws_b, core_bytes);
         if (he != hipSuccess) rc = hip_fail(he, "hipMalloc(workspace)");
         else p->ws_bytes += (int64_t)core_bytes;
@@ -392,54 +473,37 @@ int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_ty
 int mfft_execute(const mfft_plan* p, const void* in, void* out, void* stream_v) {
     g_err.clear();
     if (!p) return fail(MFFT_ERR_VALUE, "plan must not be NULL");
-    if (!in || !out) return fail(MFFT_ERR_VALUE, "in and out must not be NULL");
-    const size_t in_bytes = (size_t)p->batch *
-        (p->transform_type == MFFT_R2C ? (size_t)p->n * 4
-         : p->transform_type == MFFT_C2R ? (size_t)(p->n / 2 + 1) * 8 : (size_t)p->n * 8);
-    const size_t out_bytes = (size_t)p->batch *
-        (p->transform_type == MFFT_R2C ? (size_t)(p->n / 2 + 1) * 8
-         : p->transform_type == MFFT_C2R ? (size_t)p->n * 4 : (size_t)p->n * 8);
-    const char* ib = (const char*)in;
-    const char* ob = (const char*)out;
-    if (ib < ob + out_bytes && ob < ib + in_bytes)
-        return fail(MFFT_ERR_VALUE, "in and out must not overlap");
-    if ((((uintptr_t)in) & 7) && p->transform_type != MFFT_R2C)
-        return fail(MFFT_ERR_VALUE, "complex input must be 8-byte aligned");
-    if ((((uintptr_t)in) & 7) && p->transform_type == MFFT_R2C)
-        return fail(MFFT_ERR_VALUE, "r2c input must be 8-byte aligned (pairs are read as complex)");
-    if (((uintptr_t)out) & 7) return fail(MFFT_ERR_VALUE, "output must be 8-byte aligned");
-    int dev = -1;
-    hipError_t he = hipGetDevice(&dev);
-    if (he != hipSuccess) return hip_fail(he, "hipGetDevice");
-    if (dev != p->device)
-        return fail(MFFT_ERR_RUNTIME, "plan was created on device %d but device %d is current", p->device, dev);
-    hipStream_t stream = (hipStream_t)stream_v;
-    const int dir = p->transform_direction == MFFT_FORWARD ? -1 : 1;
+    if (p->caller_ws && p->work_bytes > 0)
+        return fail(MFFT_ERR_VALUE,
+                    "the plan was created with MFFT_PLAN_CALLER_WORKSPACE and needs %lld bytes of workspace: "
+                    "use mfft_execute_ws",
+                    (long long)p->work_bytes);
+    return execute_impl(p, in, out, Work{p->ws_a, p->ws_b}, stream_v);
+}
 
-    if (p->transform_type == MFFT_C2C)
-        return run_core(p, (const float2*)in, (float2*)out, dir, p->scale, stream);
+int mfft_plan_workspace_size(const mfft_plan* p, int64_t* bytes) {
+    g_err.clear();
+    if (!p || !bytes) return fail(MFFT_ERR_VALUE, "plan and bytes must not be NULL");
+    *bytes = p->work_bytes;
+    return MFFT_OK;
+}
 
-    const int logc = mfft::ilog2((int)p->core_n);
-    if (p->transform_type == MFFT_R2C) {
-        if (p->r2c_fused) {
-            he = mfft::launch_lds(1, -1, logc, p->elems, in, out, p->tw, p->tw_real, p->batch, p->scale, stream,
-                                  p->num_cus, p->stagger);
-            return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
-        }
-        int rc = run_core(p, (const float2*)in, p->ws_a, -1, 1.0f, stream);
-        if (rc != MFFT_OK) return rc;
-        he = mfft::launch_r2c_stitch(p->ws_a, (float2*)out, p->tw_real, p->n, p->batch, p->scale, stream);
-        return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
-    }
-    // c2r
-    if (p->c2r_fused) {
-        he = mfft::launch_lds(2, 1, logc, p->elems, in, out, p->tw, p->tw_real, p->batch, p->scale, stream,
-                              p->num_cus, p->stagger);
-        return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
-    }
-    he = mfft::launch_c2r_pre((const float2*)in, p->ws_a, p->tw_real, p->n, p->batch, stream);
-    if (he != hipSuccess) return hip_fail(he, "kernel launch");
-    return run_core(p, p->ws_a, (float2*)out, 1, p->scale, stream);
+int mfft_execute_ws(const mfft_plan* p, const void* in, void* out, void* workspace, int64_t workspace_bytes,
+                    void* stream_v) {
+    g_err.clear();
+    if (!p) return fail(MFFT_ERR_VALUE, "plan must not be NULL");
+    if (workspace_bytes < 0) return fail(MFFT_ERR_VALUE, "workspace_bytes must be >= 0");
+    if (p->work_bytes == 0) return execute_impl(p, in, out, Work{nullptr, nullptr}, stream_v);
+    if (!workspace) return fail(MFFT_ERR_VALUE, "this plan needs %lld bytes of workspace", (long long)p->work_bytes);
+    if (workspace_bytes < p->work_bytes)
+        return fail(MFFT_ERR_VALUE, "workspace of %lld bytes is smaller than the plan's %lld",
+                    (long long)workspace_bytes, (long long)p->work_bytes);
+    if (((uintptr_t)workspace) % kWorkAlign)
+        return fail(MFFT_ERR_VALUE, "workspace must be %d-byte aligned", (int)kWorkAlign);
+    char* w = (char*)workspace;
+    return execute_impl(p, in, out,
+                        Work{p->need_a ? (float2*)w : nullptr, p->need_b ? (float2*)(w + p->work_b_off) : nullptr},
+                        stream_v, workspace, p->work_bytes);
 }
 
 int mfft_execute_timed(const mfft_plan* p, const void* in, void* out, void* stream_v,

@@ -37,7 +37,12 @@ struct mfft_plan {
     float2* ws_a = nullptr;     // core-sized scratch (real flows: core output / input)
     float2* ws_b = nullptr;     // core-sized scratch (stage-flow ping-pong)
     int* sync = nullptr;        // fused four-step: [0,8) work counters, [8] wait overruns, then one per row
-    int64_t ws_bytes = 0, table_bytes = 0;
+    int64_t ws_bytes = 0, table_bytes = 0;  // device memory held by the plan
+    // Scratch an execute needs: ws_a and/or ws_b, each core_bytes; caller
+    // workspaces hold ws_a at offset 0 and ws_b at work_b_off.
+    bool need_a = false, need_b = false;
+    int64_t core_bytes = 0, work_b_off = 0, work_bytes = 0;
+    bool caller_ws = false;  // created with MFFT_PLAN_CALLER_WORKSPACE: holds no ws_a / ws_b
 };
 
 namespace mfft {

@@ -37,8 +37,10 @@ MAX_PARAMS = 4
 EXPORTS = (
     "mfft_plan_create", "mfft_execute", "mfft_execute_timed", "mfft_plan_destroy", "mfft_plan_query",
     "mfft_bit_reverse_permute", "mfft_device_props_get", "mfft_last_error",
-    "mfft_abi_version", "mfft_plan_sync_overruns",
+    "mfft_abi_version", "mfft_plan_sync_overruns", "mfft_plan_create_ex", "mfft_plan_workspace_size",
+    "mfft_execute_ws",
 )
+PLAN_CALLER_WORKSPACE = 1
 
 
 class PlanInfo(ctypes.Structure):
@@ -92,8 +94,15 @@ def load() -> ctypes.CDLL:
         lib.mfft_plan_create.argtypes = [ctypes.POINTER(vp), i64, i64, i32, i32, i32, i32,
                                          ctypes.POINTER(ctypes.c_int32), i32]
         lib.mfft_plan_create.restype = i32
+        lib.mfft_plan_create_ex.argtypes = [ctypes.POINTER(vp), i64, i64, i32, i32, i32, i32,
+                                            ctypes.POINTER(ctypes.c_int32), i32, i32]
+        lib.mfft_plan_create_ex.restype = i32
         lib.mfft_execute.argtypes = [vp, vp, vp, vp]
         lib.mfft_execute.restype = i32
+        lib.mfft_plan_workspace_size.argtypes = [vp, ctypes.POINTER(i64)]
+        lib.mfft_plan_workspace_size.restype = i32
+        lib.mfft_execute_ws.argtypes = [vp, vp, vp, vp, i64, vp]
+        lib.mfft_execute_ws.restype = i32
         lib.mfft_execute_timed.argtypes = [vp, vp, vp, vp, ctypes.POINTER(ctypes.c_float), i32,
                                            ctypes.POINTER(i32)]
         lib.mfft_execute_timed.restype = i32
@@ -134,7 +143,7 @@ class NativePlan:
 
     def __init__(self, n: int, batch: int, transform_type: str = "c2c",
                  transform_direction: str = "forward", norm: str = "backward",
-                 flow: int = FLOW_AUTO, params=()):
+                 flow: int = FLOW_AUTO, params=(), caller_workspace: bool = False):
         lib = load()
         if transform_type not in TYPE_IDS:
             raise ValueError(f"unsupported transform_type {transform_type!r}")
@@ -148,9 +157,9 @@ class NativePlan:
         arr = (ctypes.c_int32 * MAX_PARAMS)(*(params + [0] * (MAX_PARAMS - len(params))))
         h = ctypes.c_void_p()
         self._h = None
-        check(lib.mfft_plan_create(ctypes.byref(h), int(n), int(batch), TYPE_IDS[transform_type],
-                                   DIR_IDS[transform_direction], NORM_IDS[norm], int(flow),
-                                   arr, len(params)))
+        check(lib.mfft_plan_create_ex(ctypes.byref(h), int(n), int(batch), TYPE_IDS[transform_type],
+                                      DIR_IDS[transform_direction], NORM_IDS[norm], int(flow),
+                                      arr, len(params), PLAN_CALLER_WORKSPACE if caller_workspace else 0))
         self._h = h
         info = PlanInfo()
         check(lib.mfft_plan_query(self._h, ctypes.byref(info)))
@@ -161,6 +170,17 @@ class NativePlan:
         rc = _lib.mfft_execute(self._h, in_ptr, out_ptr, stream_ptr)
         if rc:
             check(rc)
+
+    def workspace_size(self) -> int:
+        """Bytes of workspace an execute of this plan needs (0: none)."""
+        k = ctypes.c_int64(0)
+        check(_lib.mfft_plan_workspace_size(self._h, ctypes.byref(k)))
+        return int(k.value)
+
+    def execute_ws(self, in_ptr: int, out_ptr: int, ws_ptr: int, ws_bytes: int, stream_ptr: int) -> None:
+        """Execute with the caller's workspace (256-byte aligned device memory
+        of at least workspace_size() bytes) instead of the plan's own."""
+        check(_lib.mfft_execute_ws(self._h, in_ptr, out_ptr, ws_ptr, int(ws_bytes), stream_ptr))
 
     def execute_timed(self, in_ptr: int, out_ptr: int, stream_ptr: int, cap: int = 64) -> list:
         """Execute once and return each kernel launch's duration in ms (HIP

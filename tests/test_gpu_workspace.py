@@ -1,0 +1,134 @@
+"""Caller-owned workspace through the C ABI: mfft_plan_create_ex with
+MFFT_PLAN_CALLER_WORKSPACE, mfft_plan_workspace_size and mfft_execute_ws.
+
+The same kernels run with the plan's own scratch or with the caller's, so the
+results must be bit-identical, whatever the workspace held before; both are
+also checked against numpy float64 to the north-star gate.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from kunlunxin_fft_amd import native
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+ALIGN = 256
+
+# n, batch, transform, direction, flow, params, (needs the real-flow buffer, needs the stage ping-pong)
+CASES = [
+    (4096, 3, "c2c", "forward", native.FLOW_RADIX2_DIT, (256,), (False, True)),
+    (2048, 5, "c2c", "inverse", native.FLOW_RADIX4_DIF, (), (False, True)),
+    (1 << 16, 3, "r2c", "forward", native.FLOW_FOUR_STEP, (256,), (True, False)),
+    (1024, 4, "c2r", "inverse", native.FLOW_RADIX2_DIT, (), (True, True)),
+    (4096, 2, "r2c", "forward", native.FLOW_LDS_FUSED, (), (False, False)),
+    (1 << 18, 2, "c2c", "forward", native.FLOW_FOUR_STEP, (512,), (False, False)),
+]
+
+
+def _ids(c):
+    return f"{c[2]}-{c[3]}-N{c[0]}-B{c[1]}-flow{c[4]}"
+
+
+def _inputs(n, b, tt, gpu, seed):
+    rng = np.random.default_rng(seed)
+    if tt == "r2c":
+        h = rng.standard_normal((b, n)).astype(np.float32)
+    else:
+        m = n // 2 + 1 if tt == "c2r" else n
+        h = (rng.standard_normal((b, m)) + 1j * rng.standard_normal((b, m))).astype(np.complex64)
+    return h, torch.from_numpy(h).to(gpu)
+
+
+def _out(n, b, tt, gpu):
+    if tt == "r2c":
+        return torch.empty((b, n // 2 + 1), dtype=torch.complex64, device=gpu)
+    if tt == "c2r":
+        return torch.empty((b, n), dtype=torch.float32, device=gpu)
+    return torch.empty((b, n), dtype=torch.complex64, device=gpu)
+
+
+def _reference(h, n, tt, td):
+    if tt == "r2c":
+        return np.fft.rfft(h.astype(np.float64))
+    if tt == "c2r":
+        return np.fft.irfft(h.astype(np.complex128), n=n)
+    x = h.astype(np.complex128)
+    return np.fft.fft(x) if td == "forward" else np.fft.ifft(x)
+
+
+def _workspace(nbytes, gpu, fill=float("nan")):
+    # float32 storage rounded up; torch's caching allocator hands out
+    # 512-byte aligned blocks
+    w = torch.full(((max(nbytes, 4) + 3) // 4,), fill, dtype=torch.float32, device=gpu)
+    assert w.data_ptr() % ALIGN == 0
+    return w
+
+
+@pytest.mark.parametrize("case", CASES, ids=_ids)
+def test_caller_workspace_matches_plan_workspace(gpu, case):
+    n, b, tt, td, flow, params, (need_a, need_b) = case
+    st = torch.cuda.current_stream(gpu).cuda_stream
+    own = native.NativePlan(n, b, tt, td, "backward", flow, params)
+    cw = native.NativePlan(n, b, tt, td, "backward", flow, params, caller_workspace=True)
+    core = b * (n // 2 if tt != "c2c" else n) * 8
+    a_end = -(-core // ALIGN) * ALIGN if need_a else 0
+    expect = (a_end + core) if need_b else (core if need_a else 0)
+    assert own.workspace_size() == expect and cw.workspace_size() == expect
+    assert own.info.workspace_bytes == expect  # held by the plan
+    assert cw.info.workspace_bytes == 0         # held by nobody but the caller
+
+    h, x = _inputs(n, b, tt, gpu, seed=1000 + n + b)
+    y0 = _out(n, b, tt, gpu)
+    own.execute(x.data_ptr(), y0.data_ptr(), st)
+    ws = _workspace(expect, gpu)
+    y1 = _out(n, b, tt, gpu)
+    cw.execute_ws(x.data_ptr(), y1.data_ptr(), ws.data_ptr() if expect else 0, ws.numel() * 4, st)
+    y2 = _out(n, b, tt, gpu)
+    own.execute_ws(x.data_ptr(), y2.data_ptr(), ws.data_ptr() if expect else 0, ws.numel() * 4, st)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1) and torch.equal(y0, y2)
+    ref = _reference(h, n, tt, td)
+    got = y1.cpu().numpy()
+    assert oracle.rel_l2(got, ref) <= TOL and oracle.max_rel_error(got, ref) <= TOL
+
+    if expect:
+        with pytest.raises(ValueError, match="mfft_execute_ws"):
+            cw.execute(x.data_ptr(), y1.data_ptr(), st)
+        with pytest.raises(ValueError, match="smaller"):
+            cw.execute_ws(x.data_ptr(), y1.data_ptr(), ws.data_ptr(), expect - 8, st)
+        roomy = _workspace(expect + ALIGN, gpu)
+        with pytest.raises(ValueError, match="aligned"):
+            cw.execute_ws(x.data_ptr(), y1.data_ptr(), roomy.data_ptr() + 8, roomy.numel() * 4 - 8, st)
+        with pytest.raises(ValueError, match="needs"):
+            cw.execute_ws(x.data_ptr(), y1.data_ptr(), 0, 0, st)
+        big = _workspace(expect + y1.numel() * y1.element_size() + ALIGN, gpu)
+        with pytest.raises(ValueError, match="overlap"):
+            # output placed inside the workspace
+            cw.execute_ws(x.data_ptr(), big.data_ptr() + ALIGN, big.data_ptr(), big.numel() * 4, st)
+    else:
+        cw.execute(x.data_ptr(), y1.data_ptr(), st)  # nothing to bring: the plain execute works
+
+
+def test_caller_workspace_two_streams(gpu):
+    """One plan, two streams, a workspace each: the executes may overlap in
+    time and must not disturb each other."""
+    n, b = 4096, 64
+    p = native.NativePlan(n, b, "c2c", "forward", "backward", native.FLOW_RADIX2_DIT, (256,),
+                          caller_workspace=True)
+    nb = p.workspace_size()
+    s1, s2 = torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)
+    h1, x1 = _inputs(n, b, "c2c", gpu, seed=11)
+    h2, x2 = _inputs(n, b, "c2c", gpu, seed=12)
+    w1, w2 = _workspace(nb, gpu), _workspace(nb, gpu)
+    y1, y2 = _out(n, b, "c2c", gpu), _out(n, b, "c2c", gpu)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        p.execute_ws(x1.data_ptr(), y1.data_ptr(), w1.data_ptr(), nb, s1.cuda_stream)
+        p.execute_ws(x2.data_ptr(), y2.data_ptr(), w2.data_ptr(), nb, s2.cuda_stream)
+    torch.cuda.synchronize()
+    for h, y in ((h1, y1), (h2, y2)):
+        ref = np.fft.fft(h.astype(np.complex128))
+        assert oracle.rel_l2(y.cpu().numpy(), ref) <= TOL

@@ -62,4 +62,15 @@ def test_execute_rejects_null_plan():
     lib = native.load()
     assert lib.mfft_execute(None, None, None, None) == native.ERR_VALUE
     assert b"plan" in lib.mfft_last_error()
+    assert lib.mfft_execute_ws(None, None, None, None, 0, None) == native.ERR_VALUE
+    assert lib.mfft_plan_workspace_size(None, None) == native.ERR_VALUE
     assert lib.mfft_plan_destroy(None) == 0
+
+
+def test_plan_create_ex_rejects_unknown_flags():
+    lib = native.load()
+    h = ctypes.c_void_p()
+    arr = (ctypes.c_int32 * native.MAX_PARAMS)()
+    rc = lib.mfft_plan_create_ex(ctypes.byref(h), 1024, 1, native.C2C, native.FORWARD, native.NORM_IDS["backward"],
+                                 native.FLOW_AUTO, arr, 0, 2)
+    assert rc == native.ERR_VALUE and b"flags" in lib.mfft_last_error() and not h.value
