@@ -24,6 +24,9 @@ Also reported (on the same JSON line):
   {16, 64}); ``config3``: the same for inverse C2C, R2C and C2R at N in {256, 4096}, B in {1, 64}
   (real transforms count 4N + 8(N/2+1) bytes per row); ``config4``: the same for N=2^20 B=1 and
   N=2^16 B=256;
+* ``real_per_size``: R2C forward and C2R inverse at the same N and B (the
+  selected plans), GB/s and fraction of peak from HIP events in cyclic order,
+  counting 4N + 8(N/2+1) bytes per row;
 * ``per_size[].vendor_*``: torch.fft.fft (rocFFT) on the same inputs, a
   comparison column only;
 * ``cpu_baseline``: the reference's own CPU FFT (butterfly::fft_dit built
@@ -68,6 +71,7 @@ def main() -> int:
     ap.add_argument("--no-latency", action="store_true", help="skip the latency / config-2 / config-4 legs")
     ap.add_argument("--no-vendor", action="store_true", help="skip the torch.fft (rocFFT) comparison column")
     ap.add_argument("--sizes", default="", help="comma-separated subset of N (profiling runs)")
+    ap.add_argument("--no-real", action="store_true", help="skip the R2C / C2R throughput leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every box here has one MI355X; "
@@ -290,6 +294,42 @@ def main() -> int:
         for c in cfg4:
             log(f"config4: {c}")
 
+    # ---- R2C and C2R throughput at the same sizes and batches (selected plans),
+    # timed in cyclic order like per_size; algorithmic bytes per row are
+    # 4N (real side) + 8(N/2+1) (half spectrum)
+    real_rows = []
+    if not args.no_real:
+        rwork = []
+        for n in sizes:
+            b = batch_for(n)
+            xr = torch.randn((b, n), dtype=torch.float32, device=dev, generator=gen)
+            xc = torch.randn((b, n // 2 + 1), dtype=torch.complex64, device=dev, generator=gen)
+            for tt, td, x in (("r2c", "forward", xr), ("c2r", "inverse", xc)):
+                plan = pkg.plan_fft("dit", n, batch=b, profile_hash=prof, transform_type=tt, transform_direction=td)
+                nplan, (shape, dt) = _resolve(plan, 0)
+                rwork.append((n, b, tt, x, plan, nplan, torch.empty(shape, dtype=dt, device=dev)))
+        for _, _, _, x, _, nplan, out in rwork:
+            nplan.execute(x.data_ptr(), out.data_ptr(), stream.cuda_stream)
+        revs = [[] for _ in rwork]
+        for _ in range(5):
+            for i, (_, _, _, x, _, nplan, out) in enumerate(rwork):
+                s = torch.cuda.Event(enable_timing=True)
+                e = torch.cuda.Event(enable_timing=True)
+                s.record(stream)
+                nplan.execute(x.data_ptr(), out.data_ptr(), stream.cuda_stream)
+                e.record(stream)
+                revs[i].append((s, e))
+        torch.cuda.synchronize()
+        for i, (n, b, tt, _, plan, nplan, _) in enumerate(rwork):
+            ms = statistics.median(s.elapsed_time(e) for s, e in revs[i])
+            gbps = b * (4 * n + 8 * (n // 2 + 1)) / (ms * 1e-3) / 1e9
+            real_rows.append({"n": n, "batch": b, "transform": tt, "executed": plan.executed,
+                              "flow": nplan.flow_name, "launches": int(nplan.info.launches), "ms": round(ms, 5),
+                              "gbps": round(gbps, 1), "frac_hbm": round(gbps / PEAK_GBPS, 4)})
+            log(f"{tt} N={n:>8} B={b:>6} {nplan.flow_name:>10} {ms:8.4f} ms {gbps:8.1f} GB/s "
+                f"({gbps / PEAK_GBPS:.1%}) launches={nplan.info.launches}")
+        del rwork
+
     # ---- vendor comparison column: rocFFT through torch.fft on the same inputs
     if not args.no_vendor:
         for (n, b, x, plan), row in zip(work, per_size):
@@ -358,6 +398,7 @@ def main() -> int:
         "config3": cfg3,
         "config4": cfg4,
         "per_size": per_size,
+        "real_per_size": real_rows,
     }
     print(json.dumps(line), flush=True)
     out_dir = os.path.join(ROOT, "gpurun_out")

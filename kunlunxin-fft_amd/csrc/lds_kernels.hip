@@ -125,7 +125,61 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
     {
         constexpr int R0 = 1 << C::logr(0);
         constexpr int NB0 = E / R0;
-        if constexpr (MODE == 2) {
+        if constexpr (MODE == 2 && P > 1 && C::LE < 5) {
+            // Each bin is loaded once (non-temporal); the partner bin L - i
+            // of the pre-twiddle comes from the thread that loaded it,
+            // through LDS, one component at a time (the exchange rows hold L
+            // floats): real parts first, kept in px, then imaginary parts,
+            // on which the pre-twiddle is applied.  Bin L, the partner of
+            // bin 0, is loaded by thread 0, which holds bin 0.
+            const float2* xb = (const float2*)src_v + row * (L + 1);
+            static_for<0, NB0>([&](auto m) {
+                static_for<0, R0>([&](auto q) {
+                    const int i = j + m.value * T + q.value * (L / R0);
+                    v[m.value * R0 + q.value] = active ? load_nt(xb + i) : make_float2(0.0f, 0.0f);
+                });
+            });
+            const float2 xny = (active && j == 0) ? load_nt(xb + L) : make_float2(0.0f, 0.0f);
+            const int pjf = padf<C::FSH>(j);
+            float px[E];
+            static_for<0, 2>([&](auto comp) {
+                if constexpr (comp.value > 0) __syncthreads();  // the real parts have been read
+                static_for<0, NB0>([&](auto m) {
+                    static_for<0, R0>([&](auto q) {
+                        const float2 x = v[m.value * R0 + q.value];
+                        ltf[padf_add<C::FSH, m.value * T + q.value * (L / R0)>(pjf, j)] =
+                            comp.value == 0 ? x.x : x.y;
+                    });
+                });
+                __syncthreads();
+                static_for<0, NB0>([&](auto m) {
+                    static_for<0, R0>([&](auto q) {
+                        constexpr int e = m.value * R0 + q.value;
+                        const int i = j + m.value * T + q.value * (L / R0);
+                        const float y = ltf[padf<C::FSH>((L - i) & (L - 1))];
+                        if constexpr (comp.value == 0) {
+                            px[e] = y;
+                        } else {
+                            float2 xk = v[e];
+                            float2 xj = make_float2(px[e], y);
+                            if (e == 0 && j == 0) {  // bin 0 pairs with bin L; both imaginary parts ignored
+                                xj = xny;
+                                xk.y = 0.0f;
+                                xj.y = 0.0f;
+                            }
+                            const float ar = 0.5f * (xk.x + xj.x), ai = 0.5f * (xk.y - xj.y);
+                            const float cr = 0.5f * (xk.x - xj.x), ci = 0.5f * (xk.y + xj.y);
+                            const float2 t = tw_real[i];
+                            const float wr = t.x, wi = -t.y;
+                            v[e] = make_float2(ar - (wr * ci + wi * cr), ai + (wr * cr - wi * ci));
+                        }
+                    });
+                });
+            });
+        } else if constexpr (MODE == 2) {
+            // single-pass lengths, and 32 elements per thread (whose partner
+            // values would not fit the register budget): both bins straight
+            // from global memory
             const float2* xb = (const float2*)src_v + row * (L + 1);
             static_for<0, NB0>([&](auto m) {
                 static_for<0, R0>([&](auto q) {
@@ -185,7 +239,8 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
             dft<R, DIR, m.value * R, 1>(v);
         });
         if constexpr ((p < P - 1 || MODE == 1) && !C::SPLIT) {
-            if constexpr (p > 0) __syncthreads();  // every thread has read this pass's inputs
+            // every thread has read this pass's inputs (pass 0 of c2r: the partner bins)
+            if constexpr (p > 0 || MODE == 2) __syncthreads();
             static_for<0, NB>([&](auto m) {
                 const int b = j + m.value * T;
                 const int base = ((b >> LNS) << (LNS + LR)) + (b & (NS - 1));

@@ -89,6 +89,12 @@ def flow_params(executed: str, n: int, transform_type: str, block, params: dict)
             return native.FLOW_AUTO, ()
         if e == 32 and (logc < 10 or transform_type == "r2c"):
             e = 0
+        # c2r cores below 32768 run with 16 elements per thread: they load
+        # each bin once and pair it with its mirror bin through LDS, where the
+        # 32-element kernel (no registers to spare for the pairs) loads every
+        # bin twice (measured 1.3-1.5x slower at 2^10-2^14 points)
+        if e == 32 and transform_type == "c2r" and logc < 15:
+            e = 16
         if logc >= 13 and 0 < e < 16:
             e = 0
         if logc == 15:

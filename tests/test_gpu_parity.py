@@ -293,6 +293,26 @@ def test_r2c_c2r_match_oracle(gpu, name, n, norm):
     check(y, oracle.c2r_dedicated(Xh, n, norm), f"c2r {name} N={n} {norm}")
 
 
+@pytest.mark.parametrize("elems,n", [(e, n) for e in (4, 8, 16) for n in (16, 64, 512, 2048, 8192)]
+                         + [(16, 1 << 14), (16, 1 << 15), (32, 1 << 12), (32, 1 << 15), (32, 1 << 16)])
+@pytest.mark.parametrize("b", [1, 3, 37])
+def test_c2r_mirror_pairs(gpu, elems, n, b):
+    """Fused C2R: each bin is loaded once and meets its mirror bin n/2 - k
+    through LDS (up to 16 elements per thread; 32 load both bins), bin 0
+    pairs with bin n/2, and the DC/Nyquist imaginary parts are ignored.
+    Ragged batches leave rows of a multi-transform block inactive."""
+    if elems < 16 and n > 8192:
+        pytest.skip("16+ elements from 8192-point cores")
+    rng = np.random.default_rng(4000 + n + b + elems)
+    m = n // 2 + 1
+    h = (rng.standard_normal((b, m)) + 1j * rng.standard_normal((b, m))).astype(np.complex64)
+    ref = np.fft.irfft(h.astype(np.complex128), n=n)  # ignores the DC and Nyquist imaginary parts
+    p = mkplan("fft_lds_fused" + ("_batch" if b > 1 else ""), n, b, tt="c2r", td="inverse",
+               params={"elems": elems})
+    y = execute_fft_plan(p, torch.from_numpy(h if b > 1 else h[0]).to(gpu)).cpu().numpy()
+    check(y.reshape(b, n), ref, f"c2r elems={elems} N={n} B={b}")
+
+
 @pytest.mark.parametrize("name", ["fft_lds_fused", "fft_four_step", "fft_dit"])
 def test_c2r_ignores_dc_nyquist_imag(gpu, golden, name):
     n = 256

@@ -24,6 +24,10 @@ def test_lds_params_map_to_elems_and_stagger():
     assert flow_params("fft_lds_fused", 2048, "r2c", 256, {"elems": 32})[1] == (0, 0)
     assert flow_params("fft_lds_fused", 1 << 16, "r2c", 256, {})[0] == native.FLOW_AUTO
     assert flow_params("fft_lds_fused", 1 << 16, "c2r", 256, {})[0] == native.FLOW_LDS_FUSED
+    # c2r takes 16 elements per thread where a c2c entry says 32 (core < 32768)
+    assert flow_params("fft_lds_fused_batch", 1 << 14, "c2r", 256, {"elems": 32, "stagger": 1})[1] == (16, 1)
+    assert flow_params("fft_lds_fused_batch", 1 << 11, "c2r", 256, {"elems": 32})[1] == (16, 0)
+    assert flow_params("fft_lds_fused_batch", 1 << 14, "c2c", 256, {"elems": 32})[1] == (32, 0)
 
 
 def test_four_step_params_map_to_split_chunk_schedule_order():
