@@ -14,7 +14,12 @@ otherwise the cell keeps M0.  The table is bound to the device profile hash
 and the live environment fingerprint, so it selects only on the stack it was
 measured on.
 
-Timing: forward C2C complex64, inputs resident on the GPU.  Cells under
+The roofline rows (N = 2^10..2^20, B = max(64, 2^25/N)) are also measured
+for R2C forward and C2R inverse with the default norm, against the M0 real
+flow, and stored as exact-semantic entries: the real modes of the LDS kernel
+and the four-step around a half-length core have their own best settings.
+
+Timing: forward C2C complex64 (and the real cells), inputs resident on the GPU.  Cells under
 64 MiB: ``reps`` back-to-back executes bracketed by HIP events on the launch
 stream, median of ``rounds`` such groups (ms per execute, launch gaps
 included).  Larger cells: each execute timed alone after an untimed 256 MiB
@@ -40,6 +45,11 @@ C5_SIZES = [1 << k for k in range(4, 15)]        # the reference's size sweep: N
 C5_BATCHES = [1, 16, 64, 256]
 ROOF_SIZES = [1 << k for k in range(10, 21)]      # roofline rows: B = max(64, 2^25/N)
 EXTRA_CELLS = [(1 << k, 1) for k in range(15, 21)] + [(1 << 16, 256), (256, 1), (4096, 64)]
+# real transforms, default norm: exact-semantic entries at the roofline rows
+# (the LDS kernel's real modes and the four-step around a half-length core
+# have their own best elements, stagger and split)
+REAL_SEMANTICS = (("r2c", "forward"), ("c2r", "inverse"))
+REAL_NORM = "backward"
 
 
 def cells(quick: bool = False):
@@ -58,6 +68,53 @@ def cells(quick: bool = False):
     if quick:
         uniq = [c for c in uniq if c[0] * c[1] <= (1 << 22) or c[1] == 1]
     return uniq
+
+
+def real_candidates(n: int, b: int, transform_type: str, space):
+    """Challengers for a real transform of length n (complex core n/2): the
+    LDS kernel's fused real modes at each elements-per-thread setting it
+    runs (R2C up to a 16384-point core and 16 elements; C2R up to 32768),
+    with the start stagger in large batches, and the four-step core."""
+    sfx = "" if b == 1 else "_batch"
+    core = n // 2
+    logc = int(math.log2(core)) if core >= 1 else 0
+    out = []
+    lds_max = 16384 if transform_type == "r2c" else 32768
+    if 1 <= core <= lds_max:
+        for e in space.lds_elems:
+            if e == 32 and (transform_type == "r2c" or logc < 15):
+                continue  # r2c never 32; c2r below 32768 maps 32 to 16
+            if logc >= 13 and e < 16:
+                continue
+            if logc == 15 and e != 32:
+                continue
+            if core <= 16 and e != 16:
+                continue
+            stags = [s for s in space.lds_stagger
+                     if s == 0 or (e >= 16 and logc >= 9 and n * b >= (1 << 24))]
+            for stg in stags:
+                params = {"elems": e} if stg == 0 else {"elems": e, "stagger": stg}
+                out.append((f"lds_e{e}" + (f"_s{stg}" if stg else ""), "fft_lds_fused" + sfx, 256, params,
+                            ("lds-resident", "stockham-radix16", "lds-stockham-single-pass")))
+    if 256 <= core and core * 2 >= space.fourstep_min_n:
+        for n1 in space.fourstep_n1:
+            n2 = core // n1
+            if n2 < 16 or n2 > 1024 or core % n1:
+                continue
+            if abs(int(math.log2(n1)) - int(math.log2(n2))) > 2:
+                continue
+            chunks = [0]
+            if b >= 16 and core >= (1 << 14):
+                chunks += [c for c in space.fourstep_chunk_rows if c and c < b and core * c * 8 >= (16 << 20)
+                           and core * c * 8 <= (256 << 20)]
+            for ch in chunks:
+                for order in (space.fourstep_pass2_order if b > 1 else (0,)):
+                    params = {"n1": n1, "chunk_rows": ch}
+                    if order:
+                        params["pass2_order"] = order
+                    out.append((f"fs_n1_{n1}_c{ch}" + ("_r" if order else ""), "fft_four_step" + sfx, 256,
+                                params, ("four-step", "stockham-radix16", "four-step-two-pass")))
+    return out
 
 
 def candidates(n: int, b: int, direction: str, space):
@@ -156,14 +213,14 @@ def main() -> int:
     # timed back to back: they live in the MALL in any use.
     flush = torch.empty(1 << 26, dtype=torch.float32, device=dev)  # 256 MiB
 
-    def time_runner(name, n, b, block, params, x):
-        np_ = get_native_plan(name, n, b, "c2c", "forward", "backward", block, params, 0)
-        shape, dt = output_spec("c2c", n, b)
+    def time_runner(name, n, b, block, params, x, tt="c2c", td="forward"):
+        np_ = get_native_plan(name, n, b, tt, td, "backward", block, params, 0)
+        shape, dt = output_spec(tt, n, b)
         out = torch.empty(shape, dtype=dt, device=dev)
         for _ in range(3):
             np_.execute(x.data_ptr(), out.data_ptr(), stream.cuda_stream)
         res = []
-        if n * b * 8 >= (64 << 20):
+        if n * b * (8 if tt == "c2c" else 4) >= (64 << 20):
             for _ in range(args.rounds):
                 for _ in range(max(3, args.reps // 4)):
                     flush.fill_(1.0)
@@ -230,6 +287,41 @@ def main() -> int:
                   f"{best[0] if best else float('nan'):.4f} ms ({gain:+.1f}%) -> {entry['executed']} "
                   f"[{time.time() - t_start:.0f}s]", flush=True)
         del x
+    # ---- real transforms at the roofline rows: exact-semantic entries
+    for n in ([] if args.quick else ROOF_SIZES):
+        b = max(64, (1 << 25) // n)
+        for tt, td in REAL_SEMANTICS:
+            if tt == "r2c":
+                x = torch.randn((b, n), dtype=torch.float32, device=dev, generator=gen)
+            else:
+                x = torch.randn((b, n // 2 + 1), dtype=torch.complex64, device=dev, generator=gen)
+            inc_name = "fft_dit_batch"
+            inc_ms = time_runner(inc_name, n, b, 256, {}, x, tt, td)
+            best = None
+            row = {"N": n, "batch": b, "direction": "dit", "transform_type": tt, "m0_dit@256": round(inc_ms, 5)}
+            for label, name, block, params, fam in real_candidates(n, b, tt, space):
+                ms = time_runner(name, n, b, block, params, x, tt, td)
+                row[label] = round(ms, 5)
+                if best is None or ms < best[0]:
+                    best = (ms, label, name, block, params, fam)
+            sweep.append(row)
+            gain = (inc_ms - best[0]) / inc_ms * 100.0 if best else -1.0
+            sem = {"transform_type": tt, "transform_direction": td, "normalization": REAL_NORM}
+            if best is not None and gain >= GUARD_PCT:
+                ms, label, name, block, params, (real, unit, flow_id) = best
+                entry = {"N": n, "batch": b, "direction": "dit", **sem, "incumbent_ms": inc_ms,
+                         "incumbent_block": 256, "challenger_ms": ms,
+                         "evidence": {"incumbent": "m0_dit@256", "challenger": label, "gain_pct": round(gain, 2)},
+                         "reason": f"{tt}: challenger {label} beats M0 incumbent m0_dit@256 by "
+                                   f"{gain:.1f}% (>= {GUARD_PCT}%)",
+                         "block": block, "flow_id": flow_id, "flow_realization": real,
+                         "processing_unit": unit, "params": dict(params, variant="folded"), "executed": name}
+                entries.append(entry)
+            print(f"{tt} N={n:>8} B={b:>6}: M0 {inc_ms:.4f} ms, best {best[1] if best else '-'} "
+                  f"{best[0] if best else float('nan'):.4f} ms ({gain:+.1f}%) [{time.time() - t_start:.0f}s]",
+                  flush=True)
+            del x
+
     table = {
         "schema_version": 1, "device": DeviceProfile.load().device,
         "profile_hash": DeviceProfile.load().hash(), "env_hash": env_hash,
@@ -237,7 +329,8 @@ def main() -> int:
         "precision": "fp32", "guard_pct": GUARD_PCT,
         "selection_semantics": "median of rounds x (reps back-to-back executes / reps), HIP events; "
                                "cells of 64 MiB and more: each execute after an untimed 256 MiB write; "
-                               "forward C2C complex64; legacy entries answer every semantic",
+                               "forward C2C complex64 (legacy entries, answering every semantic), plus "
+                               "exact-semantic R2C / C2R entries (norm backward) at the roofline rows",
         "sources": ["kunlunxin-fft_amd/table_builder.py live sweep"],
         "entries": entries, "previous_fallbacks": [],
     }

@@ -10,7 +10,7 @@ from kunlunxin_fft_amd import native
 from kunlunxin_fft_amd.config import DesignSpace
 from kunlunxin_fft_amd.runner import flow_params
 from kunlunxin_fft_amd.selector import entry_contract_violations
-from kunlunxin_fft_amd.table_builder import candidates
+from kunlunxin_fft_amd.table_builder import candidates, real_candidates
 
 
 def test_lds_params_map_to_elems_and_stagger():
@@ -100,3 +100,26 @@ def test_shipped_table_uses_only_published_params():
         assert p.get("stagger", 0) in (0,) + sp.lds_stagger
         assert p.get("pass2_order", 0) in sp.fourstep_pass2_order
         assert p.get("schedule", 0) in sp.fourstep_schedule
+
+
+def test_real_candidates_respect_the_real_modes():
+    """R2C runs the LDS kernel up to a 16384-point core and never with 32
+    elements; C2R up to 32768 (32 elements only there); every candidate
+    passes the loader's contract as an exact-semantic entry."""
+    sp = DesignSpace.load()
+    for n in (1 << 10, 1 << 14, 1 << 15, 1 << 16, 1 << 20):
+        b = max(64, (1 << 25) // n)
+        for tt, td in (("r2c", "forward"), ("c2r", "inverse")):
+            cands = real_candidates(n, b, tt, sp)
+            assert cands
+            lds = [c for c in cands if c[1].startswith("fft_lds")]
+            if tt == "r2c":
+                assert all(c[3].get("elems") != 32 for c in lds)
+                assert bool(lds) == (n // 2 <= 16384)
+            else:
+                assert all(c[3].get("elems") != 32 for c in lds if n // 2 < 32768)
+                assert bool(lds) == (n // 2 <= 32768)
+            for label, name, block, params, (real, unit, flow_id) in cands:
+                e = _entry(params, real=real, unit=unit, n=n, b=b, executed=name)
+                e.update(transform_type=tt, transform_direction=td, normalization="backward")
+                assert not entry_contract_violations(e), (tt, n, label, entry_contract_violations(e))
