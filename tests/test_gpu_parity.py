@@ -412,6 +412,36 @@ def test_config5_selector_and_m0_cells(gpu, n, b):
     check(execute_fft_plan(m0, xd).cpu().numpy(), ref, f"C5 N={n} B={b} M0")
 
 
+def _real_entries():
+    import json
+    import os
+    path = os.path.join(os.path.dirname(__file__), "..", "kunlunxin-fft_amd", "config", "selector_table.json")
+    t = json.load(open(path))
+    return [(e["N"], e["batch"], e["transform_type"], e["transform_direction"], e["executed"])
+            for e in t["entries"] if "transform_type" in e]
+
+
+@pytest.mark.parametrize("n,b,tt,td,executed", _real_entries())
+def test_selector_real_entries(gpu, n, b, tt, td, executed):
+    """The exact-semantic R2C / C2R entries of the shipped table: plan_fft
+    resolves them (not the C2C entry of the same cell), and the selected
+    plan is correct on the first, a middle and the last row."""
+    plan = plan_fft("dit", n, batch=b, profile_hash=DeviceProfile.load().hash(), transform_type=tt,
+                    transform_direction=td)
+    assert plan.executed == executed and plan.transform_type == tt and not plan.fallback
+    rng = np.random.default_rng(5000 + n)
+    if tt == "r2c":
+        x = torch.randn((b, n), dtype=torch.float32, device=gpu, generator=torch.Generator(gpu).manual_seed(n))
+    else:
+        x = torch.randn((b, n // 2 + 1), dtype=torch.complex64, device=gpu,
+                        generator=torch.Generator(gpu).manual_seed(n))
+    y = execute_fft_plan(plan, x)
+    rows = [0, int(rng.integers(1, b - 1)), b - 1]
+    h = x[rows].cpu().numpy()
+    ref = np.fft.rfft(h.astype(np.float64)) if tt == "r2c" else np.fft.irfft(h.astype(np.complex128), n=n)
+    check(y[rows].cpu().numpy(), ref, f"selector {tt} N={n} B={b} ({executed})")
+
+
 # --------------------------------------------------------- properties, KATs
 @pytest.mark.parametrize("name", ["fft_lds_fused", "fft_four_step", "fft_dit_radix4"])
 def test_linearity(gpu, name):
