@@ -102,7 +102,9 @@ enum {
  *                                    the XCD whose L2 holds its pass-1 output
  *                                    (n1, n2 in [128, 512] within 2x; one
  *                                    execute of such a plan at a time: its
- *                                    counters live in the plan),
+ *                                    counters live in the plan; switched off
+ *                                    in this build: plan creation returns
+ *                                    MFFT_ERR_UNSUPPORTED),
  *                        params[3] = pass-2 row order: 0 = forward; 1 =
  *                                    reverse, so the batch rows pass 1 wrote
  *                                    last (the most likely still in the
