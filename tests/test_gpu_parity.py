@@ -455,6 +455,33 @@ def test_linearity(gpu, name):
     check(run_(mix), alpha * run_(a) + run_(c), f"linearity {name}")
 
 
+@pytest.mark.parametrize("n", [1 << k for k in range(10, 21)])
+def test_roofline_rows_full_size(gpu, n):
+    """The bench's rows at full size (B = max(64, 2^25/N), 256 MiB in and out
+    per N) through the selected plans: sampled rows against numpy float64,
+    the forward -> inverse round trip and Parseval's identity over the whole
+    batch (both size-independent)."""
+    b = max(64, (1 << 25) // n)
+    prof = DeviceProfile.load().hash()
+    g = torch.Generator(gpu).manual_seed(n)
+    x = torch.randn((b, n), dtype=torch.complex64, device=gpu, generator=g)
+    fwd = plan_fft("dit", n, batch=b, profile_hash=prof)
+    inv = plan_fft("dit", n, batch=b, profile_hash=prof, transform_direction="inverse")
+    assert not fwd.fallback and not inv.fallback
+    y = execute_fft_plan(fwd, x)
+    rows = [0, b // 2 + 1, b - 1]
+    check(y[rows].cpu().numpy(), np.fft.fft(x[rows].cpu().numpy().astype(np.complex128)),
+          f"full-size N={n} B={b} ({fwd.executed})")
+    # Parseval: sum |Y|^2 = N sum |x|^2 (float64 sums on the device)
+    ex = torch.sum(torch.abs(x.to(torch.complex128)) ** 2).item()
+    ey = torch.sum(torch.abs(y.to(torch.complex128)) ** 2).item()
+    assert abs(ey / (n * ex) - 1.0) <= 1e-5, f"Parseval N={n}: {ey / (n * ex) - 1.0:.3e}"
+    z = execute_fft_plan(inv, y)  # backward norm: the inverse carries 1/N
+    d = (torch.linalg.vector_norm((z - x).to(torch.complex128)) /
+         torch.linalg.vector_norm(x.to(torch.complex128))).item()
+    assert d <= 1e-5, f"round trip N={n}: rel L2 {d:.3e}"
+
+
 def test_known_signals(gpu, golden):
     for name in ("fft_dit", "fft_lds_fused", "fft_four_step"):
         for kin, kout in (("impulse256_in", "impulse256_out"), ("tone256_in", "tone256_out")):
