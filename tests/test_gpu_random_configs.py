@@ -23,7 +23,7 @@ FLOWS = (("fft_dit", 1, 16), ("fft_dif", 1, 16), ("fft_dit_radix4", 2, 16), ("ff
          ("fft_lds_fused", 0, 15), ("fft_four_step", 8, 20))
 
 
-def _cases(count=160, seed=20261202):
+def _cases(count=400, seed=20261202):
     rng = np.random.default_rng(seed)
     out = []
     for i in range(count):
