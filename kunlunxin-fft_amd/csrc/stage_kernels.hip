@@ -156,46 +156,64 @@ __global__ void bitrev_kernel(const float2* __restrict__ x, float2* __restrict__
 // R2C stitch (kernels.py:1127-1177 formula): X[k] = a - i*w*c with
 // a = (Z[k] + conj Z[j])/2, c = (Z[k] - conj Z[j])/2, j = (np-k) % np,
 // w = exp(-2*pi*i*k/n); imaginary parts of bins 0 and np are exactly 0.
-__global__ void r2c_stitch_kernel(const float2* __restrict__ z, float2* __restrict__ x,
-                                  const float2* __restrict__ tw_real, int64_t total, int64_t np,
-                                  float scale) {
-    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= total) return;
-    const int64_t row = g / (np + 1);
-    const int64_t k = g - row * (np + 1);
-    const float2* zr = z + row * np;
-    const float2 zk = zr[k & (np - 1)];
-    const float2 zj = zr[(np - k) & (np - 1)];
+// One thread per mirror pair (k, np-k), k in [0, np/2]: bin np-k takes the
+// same two core outputs with their roles swapped, so every core output is
+// read once (non-temporal: it is not read again).  Pair 0 also writes bin
+// np (both from Z[0]); pair np/2 is one bin.  A block covers 256 pairs of
+// one row (bpr blocks per row), so the row is a per-block quotient.
+__device__ __forceinline__ float2 stitch_bin(float2 zk, float2 zj, float2 w, float scale, bool edge) {
     const float ar = 0.5f * (zk.x + zj.x), ai = 0.5f * (zk.y - zj.y);
     const float cr = 0.5f * (zk.x - zj.x), ci = 0.5f * (zk.y + zj.y);
-    const float2 w = tw_real[k];
-    float xr = ar + (w.x * ci + w.y * cr);
-    float xi = ai - (w.x * cr - w.y * ci);
-    if (k == 0 || k == np) xi = 0.0f;
-    x[g] = make_float2(xr * scale, xi * scale);
+    const float xr = ar + (w.x * ci + w.y * cr);
+    const float xi = edge ? 0.0f : ai - (w.x * cr - w.y * ci);
+    return make_float2(xr * scale, xi * scale);
+}
+
+__global__ __launch_bounds__(256) void r2c_stitch_kernel(const float2* __restrict__ z, float2* __restrict__ x,
+                                                         const float2* __restrict__ tw_real, int64_t np, int bpr,
+                                                         float scale) {
+    const int row = (int)(blockIdx.x / (unsigned)bpr);
+    const int64_t k = (int64_t)(blockIdx.x - (unsigned)row * (unsigned)bpr) * 256 + threadIdx.x;
+    const int64_t half = np >> 1;
+    if (k > half) return;
+    const float2* zr = z + (int64_t)row * np;
+    float2* xr = x + (int64_t)row * (np + 1);
+    const int64_t j = (np - k) & (np - 1);
+    const float2 zk = load_nt(zr + k);
+    const float2 zj = load_nt(zr + j);
+    xr[k] = stitch_bin(zk, zj, tw_real[k], scale, k == 0);
+    if (k == 0) xr[np] = stitch_bin(zk, zj, tw_real[np], scale, true);
+    else if (k != half) xr[np - k] = stitch_bin(zj, zk, tw_real[np - k], scale, false);
 }
 
 // C2R pre-twiddle (kernels.py:1180-1229 formula): Z[k] = a + i*w'*c with
 // a = (X[k] + conj X[j])/2, c = (X[k] - conj X[j])/2, j = np-k,
 // w' = exp(+2*pi*i*k/n); imaginary parts of bins 0 and np are ignored.
-__global__ void c2r_pre_kernel(const float2* __restrict__ x, float2* __restrict__ z,
-                               const float2* __restrict__ tw_real, int64_t total, int64_t np) {
-    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= total) return;
-    const int64_t row = g / np;
-    const int64_t k = g - row * np;
-    const float2* xr = x + row * (np + 1);
-    float2 xk = xr[k];
-    float2 xj = xr[np - k];
+// Paired like the stitch: thread k in [0, np/2] reads X[k] and X[np-k] once
+// and writes Z[k] and Z[np-k] (pair 0 only Z[0]; pair np/2 one value).
+__device__ __forceinline__ float2 pre_bin(float2 xk, float2 xj, float2 t) {
+    const float ar = 0.5f * (xk.x + xj.x), ai = 0.5f * (xk.y - xj.y);
+    const float cr = 0.5f * (xk.x - xj.x), ci = 0.5f * (xk.y + xj.y);
+    const float wr = t.x, wi = -t.y;
+    return make_float2(ar - (wr * ci + wi * cr), ai + (wr * cr - wi * ci));
+}
+
+__global__ __launch_bounds__(256) void c2r_pre_kernel(const float2* __restrict__ x, float2* __restrict__ z,
+                                                      const float2* __restrict__ tw_real, int64_t np, int bpr) {
+    const int row = (int)(blockIdx.x / (unsigned)bpr);
+    const int64_t k = (int64_t)(blockIdx.x - (unsigned)row * (unsigned)bpr) * 256 + threadIdx.x;
+    const int64_t half = np >> 1;
+    if (k > half) return;
+    const float2* xr = x + (int64_t)row * (np + 1);
+    float2* zr = z + (int64_t)row * np;
+    float2 xk = load_nt(xr + k);
+    float2 xj = load_nt(xr + (np - k));
     if (k == 0) {
         xk.y = 0.0f;
         xj.y = 0.0f;
     }
-    const float ar = 0.5f * (xk.x + xj.x), ai = 0.5f * (xk.y - xj.y);
-    const float cr = 0.5f * (xk.x - xj.x), ci = 0.5f * (xk.y + xj.y);
-    const float2 t = tw_real[k];
-    const float wr = t.x, wi = -t.y;
-    z[g] = make_float2(ar - (wr * ci + wi * cr), ai + (wr * cr - wi * ci));
+    zr[k] = pre_bin(xk, xj, tw_real[k]);
+    if (k != 0 && k != half) zr[np - k] = pre_bin(xj, xk, tw_real[np - k]);
 }
 
 inline unsigned grid_for(int64_t total, int block) { return (unsigned)((total + block - 1) / block); }
@@ -309,8 +327,9 @@ hipError_t launch_bitrev(const float2* src, float2* dst, int64_t n, int64_t rows
 hipError_t launch_r2c_stitch(const float2* z, float2* x, const float2* tw_real, int64_t n,
                              int64_t rows, float scale, hipStream_t stream) {
     const int64_t np = n >> 1;
-    const int64_t total = rows * (np + 1);
-    r2c_stitch_kernel<<<grid_for(total, 256), 256, 0, stream>>>(z, x, tw_real, total, np, scale);
+    const int bpr = (int)(((np >> 1) + 1 + 255) / 256);  // blocks per row: pairs k in [0, np/2]
+    if ((int64_t)bpr * rows > 0x7fffffff) return hipErrorInvalidValue;
+    r2c_stitch_kernel<<<(unsigned)(bpr * rows), 256, 0, stream>>>(z, x, tw_real, np, bpr, scale);
     mark(stream);
     return hipGetLastError();
 }
@@ -318,8 +337,9 @@ hipError_t launch_r2c_stitch(const float2* z, float2* x, const float2* tw_real, 
 hipError_t launch_c2r_pre(const float2* x, float2* z, const float2* tw_real, int64_t n,
                           int64_t rows, hipStream_t stream) {
     const int64_t np = n >> 1;
-    const int64_t total = rows * np;
-    c2r_pre_kernel<<<grid_for(total, 256), 256, 0, stream>>>(x, z, tw_real, total, np);
+    const int bpr = (int)(((np >> 1) + 1 + 255) / 256);
+    if ((int64_t)bpr * rows > 0x7fffffff) return hipErrorInvalidValue;
+    c2r_pre_kernel<<<(unsigned)(bpr * rows), 256, 0, stream>>>(x, z, tw_real, np, bpr);
     mark(stream);
     return hipGetLastError();
 }
