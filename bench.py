@@ -325,7 +325,9 @@ def main() -> int:
             gbps = b * (4 * n + 8 * (n // 2 + 1)) / (ms * 1e-3) / 1e9
             real_rows.append({"n": n, "batch": b, "transform": tt, "executed": plan.executed,
                               "flow": nplan.flow_name, "launches": int(nplan.info.launches), "ms": round(ms, 5),
-                              "gbps": round(gbps, 1), "frac_hbm": round(gbps / PEAK_GBPS, 4)})
+                              "gbps": round(gbps, 1), "frac_hbm": round(gbps / PEAK_GBPS, 4),
+                              "split": ([int(nplan.info.n1), int(nplan.info.n2), int(nplan.info.chunk_rows) or b]
+                                        if nplan.info.n1 else None)})
             log(f"{tt} N={n:>8} B={b:>6} {nplan.flow_name:>10} {ms:8.4f} ms {gbps:8.1f} GB/s "
                 f"({gbps / PEAK_GBPS:.1%}) launches={nplan.info.launches}")
         del rwork

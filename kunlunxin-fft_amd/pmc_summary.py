@@ -95,9 +95,40 @@ def bench_keys(name: str, grid: int, sizes) -> list:
         elif name.startswith("fourstep") and s["flow"] == "four-step" and s.get("split"):
             n1, n2, rows = s["split"]
             kind = t[4]
-            if rows * n == points and (n1 if kind == 0 else n2) == (1 << logl):
+            # the bench's C2C rows are forward transforms (DIR -1)
+            if rows * n == points and (n1 if kind == 0 else n2) == (1 << logl) and t[3] == -1:
                 keys.append(f"fourstep_pass_kernel pass {kind + 1} (n{kind + 1}={1 << logl})"
                             f"|N={n}|rows={rows}")
+    return keys
+
+
+def real_keys(name: str, grid: int, real_sizes) -> list:
+    """Labels ("<transform> <kernel>|N=<n>|rows=<rows>") for the launches of
+    bench.py's real-transform leg (``real_per_size``): the LDS kernel's R2C
+    (mode 1) and C2R (mode 2) instances, the four-step passes over the
+    half-length core, and the standalone stitch / pre-twiddle kernels (one
+    thread per mirror pair, 256-thread blocks per row)."""
+    keys = []
+    t = _template_args(name)
+    for s in real_sizes:
+        n, b, tt = s["n"], s["batch"], s["transform"]
+        core = n // 2
+        if name.startswith("lds_fft_kernel") and t is not None and len(t) == 4 and s["flow"] == "lds-fused":
+            logl, loge, mode = t[0], t[1], t[3]
+            if (mode, tt) in ((1, "r2c"), (2, "c2r")) and core == (1 << logl) and (grid << loge) == core * b:
+                keys.append(f"{tt} lds_fft_kernel|N={n}|rows={b}")
+        elif name.startswith("fourstep_pass_kernel") and t is not None and s["flow"] == "four-step" and s.get("split"):
+            n1, n2, rows = s["split"]
+            logl, loge, kind = t[0], t[1], t[4]
+            # r2c runs a forward core (DIR -1), c2r an inverse one (DIR +1)
+            if (rows * core == (grid << loge) and (n1 if kind == 0 else n2) == (1 << logl)
+                    and t[3] == (-1 if tt == "r2c" else 1)):
+                keys.append(f"{tt} pass {kind + 1}|N={n}|rows={rows}")
+        elif name.startswith(("r2c_stitch_kernel", "c2r_pre_kernel")) and s["flow"] == "four-step":
+            want = "r2c" if name.startswith("r2c") else "c2r"
+            bpr = ((core >> 1) + 1 + 255) // 256
+            if tt == want and grid == bpr * b * 256:
+                keys.append(f"{tt} {name}|N={n}|rows={b}")
     return keys
 
 
@@ -150,7 +181,9 @@ def stats(args) -> int:
     covers several launch shapes (sizes, chunks), which kernel_stats.csv
     averages together."""
     durs = trace_durations(args.dir)
-    sizes = json.load(open(args.detail))["per_size"] if args.detail else []
+    detail = json.load(open(args.detail)) if args.detail else {}
+    sizes = detail.get("per_size", [])
+    real_sizes = detail.get("real_per_size", [])
     total = sum(sum(v) for v in durs.values())
     order = sorted(durs.items(), key=lambda kv: -sum(kv[1]))[: args.top]
     with open(args.md, "w") as f:
@@ -161,7 +194,10 @@ def stats(args) -> int:
         f.write("| kernel | grid | bench key | calls | total ms | average us | min us | max us | share |\n")
         f.write("|---|---:|---|---:|---:|---:|---:|---:|---:|\n")
         for (name, grid), v in order:
-            keys = ", ".join(k.split("|", 1)[1] for k in bench_keys(name, grid, sizes)) or "-"
+            keys = ", ".join([k.split("|", 1)[1] for k in bench_keys(name, grid, sizes)]
+                             + [k.split("|", 1)[0].split(" ", 1)[0] + " " + k.split("|", 1)[1]
+                                for k in real_keys(name, grid, real_sizes)]) or "-"
+            keys = keys.replace("|", "\\|")  # a literal pipe inside a Markdown table cell
             f.write(f"| {name} | {grid} | {keys} | {len(v)} | {sum(v) / 1e6:.3f} | {sum(v) / len(v) / 1e3:.2f} | "
                     f"{min(v) / 1e3:.2f} | {max(v) / 1e3:.2f} | {100.0 * sum(v) / total:.1f}% |\n")
     print(f"wrote {args.md} ({len(order)} launch shapes)")
@@ -245,7 +281,7 @@ def main() -> int:
                     extra += f" {us:.2f} | {gbs:.0f} | {gbs / 8000:.1%} |"
                 else:
                     extra += " - | - | - |"
-            f.write(f"| {key} | {name} | {grid} | {alg / 2**20:.1f} | {fb / 2**20:.1f} | {wb / 2**20:.1f} | "
+            f.write(f"| {key.replace('|', chr(92) + '|')} | {name} | {grid} | {alg / 2**20:.1f} | {fb / 2**20:.1f} | {wb / 2**20:.1f} | "
                     f"{(fb + wb) / alg:.3f} |{extra}\n")
     print(f"wrote {args.json} ({len(traffic)} kernels) and {args.md}")
     return 0

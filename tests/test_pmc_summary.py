@@ -68,6 +68,40 @@ def test_stats_one_row_per_launch_shape(tmp_path):
     subprocess.run([sys.executable, SCRIPT, "stats", "--dir", str(d), "--detail", str(tmp_path / "d.json"),
                     "--md", str(md)], check=True, capture_output=True)
     text = open(md).read()
-    assert "| lds_fft_kernel<10, 4, -1, 0> | 2097152 | N=1024|rows=32768 | 2 | 0.202 | 101.00 |" in text
+    assert "| lds_fft_kernel<10, 4, -1, 0> | 2097152 | N=1024\\|rows=32768 | 2 | 0.202 | 101.00 |" in text
     assert "| lds_fft_kernel<10, 4, -1, 0> | 2048 | - | 1 |" in text
-    assert "| fourstep_pass_kernel<10, 5, 4, -1, 0> | 524288 | N=1048576|rows=16 | 1 |" in text
+    assert "| fourstep_pass_kernel<10, 5, 4, -1, 0> | 524288 | N=1048576\\|rows=16 | 1 |" in text
+
+
+def test_stats_labels_real_transform_launches(tmp_path):
+    """The real-transform leg: LDS R2C/C2R instances, four-step passes over
+    the half-length core and the standalone stitch kernel are labelled from
+    real_per_size."""
+    d = tmp_path / "trace"
+    d.mkdir()
+    r2c = "void mfft::(anonymous namespace)::lds_fft_kernel<9, 4, -1, 1>(void const*, void*, float)"
+    p1 = "void mfft::(anonymous namespace)::fourstep_pass_kernel<8, 4, 4, -1, 0>(float2 const*, int)"
+    st = "void mfft::(anonymous namespace)::r2c_stitch_kernel(float2 const*, float2*, float2 const*, long, int, float)"
+    n_lds, b_lds = 1024, 32768           # core 512: 2^24 points, 16 per thread
+    n_fs, b_fs = 1 << 16, 512            # core 2^15 = 256 x 128
+    bpr = ((n_fs // 4) + 1 + 255) // 256
+    rows = [(r2c, (n_lds // 2) * b_lds // 16, 50_000), (p1, (n_fs // 2) * b_fs // 16, 60_000),
+            (st, bpr * b_fs * 256, 53_000)]
+    with open(d / "run_kernel_trace.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Kernel_Name", "Start_Timestamp", "End_Timestamp", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z"])
+        t = 0
+        for name, grid, ns in rows:
+            w.writerow([name, t, t + ns, grid, 1, 1])
+            t += ns + 1000
+    real = [{"n": n_lds, "batch": b_lds, "transform": "r2c", "flow": "lds-fused", "split": None},
+            {"n": n_fs, "batch": b_fs, "transform": "r2c", "flow": "four-step", "split": [256, 128, b_fs]}]
+    with open(tmp_path / "d.json", "w") as f:
+        json.dump({"per_size": [], "real_per_size": real}, f)
+    md = tmp_path / "s.md"
+    subprocess.run([sys.executable, SCRIPT, "stats", "--dir", str(d), "--detail", str(tmp_path / "d.json"),
+                    "--md", str(md)], check=True, capture_output=True)
+    text = open(md).read()
+    assert "| r2c N=1024\\|rows=32768 |" in text
+    assert "| r2c N=65536\\|rows=512 |" in text
+    assert text.count("r2c N=65536") == 2  # pass 1 and the stitch
