@@ -83,7 +83,7 @@ enum {
 /* Flow parameters (params[i], all optional, 0 = library default):
  *   RADIX2_* / RADIX4_*: params[0] = threads per block (64..1024, power of two)
  *   LDS_FUSED:           params[0] = elements per thread (4, 8, 16 or 32; 32 from 2^10,
- *                                    >= 16 from 2^13, 32 at 2^15, not 32 for r2c),
+ *                                    >= 16 from 2^13, 32 at 2^15),
  *                        params[1] = start stagger (0..16): in launches of at
  *                                    least two waves of workgroups, the first
  *                                    wave's workgroups on the upper half of

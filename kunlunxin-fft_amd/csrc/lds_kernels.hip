@@ -25,7 +25,8 @@
 //   0  c2c: core + norm scale in the final store (inverse = conjugated roots)
 //   1  r2c: the real input viewed as n/2 complex (x[2k] + i x[2k+1]) is the
 //      core input for free; the stitch of kernels.py:1127-1177 runs from LDS
-//      and writes the n/2+1 bins with the scale
+//      (32 elements per thread: from the output row) and writes the n/2+1
+//      bins with the scale
 //   2  c2r: the pre-twiddle of kernels.py:1180-1229 is applied while loading
 //      the n/2+1 bins; the inverse core writes the n real samples as n/2
 //      complex pairs with scale 2*norm_scale
@@ -95,7 +96,7 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
     using C = LdsCfg<LOGL, LOGE, MODE>;
     constexpr int L = C::L, E = C::E, T = C::T, P = C::P;
     constexpr bool NEED_LDS = (P > 1) || (MODE == 1);
-    static_assert(!(C::SPLIT && MODE == 1), "the r2c stitch needs whole complex values in LDS");
+    static_assert(!(C::SPLIT && MODE == 1 && C::LE != 5), "16-element r2c kernels exchange whole complex values");
     __shared__ float2 lds_raw[NEED_LDS ? (C::LDS_FLOATS + 1) / 2 : 1];
     float2* const lds = lds_raw;
     float* const ldsf = reinterpret_cast<float*>(lds_raw);
@@ -281,7 +282,47 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
     });
 
     // ---- epilogue
-    if constexpr (MODE == 1) {
+    if constexpr (MODE == 1 && C::SPLIT) {
+        // r2c with 32 elements per thread: the split LDS rows hold one
+        // component at a time and the registers have no room for the mirror
+        // values, so the core outputs z go to the output row itself (L of
+        // its L + 1 bins), and each thread then turns disjoint mirror pairs
+        // (k, L - k) into bins in place: it alone reads and writes those two
+        // addresses, so no thread overwrites a value another still needs.
+        // The row was last written by this block's own waves (same CU and
+        // L1), so completed stores and a barrier make them visible; the
+        // reads mostly hit L2.
+        constexpr int LR = C::logr(P - 1);
+        constexpr int R = 1 << LR;
+        constexpr int NB = E / R;
+        constexpr int NS = L / R;
+        float2* xo = (float2*)dst_v + row * (L + 1);
+        if (active) {
+            static_for<0, NB>([&](auto m) {
+                const int b = j + m.value * T;
+                static_for<0, R>([&](auto q) { xo[b + q.value * NS] = v[m.value * R + q.value]; });
+            });
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are complete
+        __syncthreads();                // ... and every other thread's
+        if (active) {
+            for (int k = j; k <= L / 2; k += T) {
+                const float2 zk = xo[k];
+                const float2 zj = xo[(L - k) & (L - 1)];
+                auto bin = [&](float2 a, float2 c, int kk, bool edge) {
+                    const float ar = 0.5f * (a.x + c.x), ai = 0.5f * (a.y - c.y);
+                    const float cr = 0.5f * (a.x - c.x), ci = 0.5f * (a.y + c.y);
+                    const float2 w = tw_real[kk];
+                    const float xr = ar + (w.x * ci + w.y * cr);
+                    const float xi = edge ? 0.0f : ai - (w.x * cr - w.y * ci);
+                    return make_float2(xr * scale, xi * scale);
+                };
+                xo[k] = bin(zk, zj, k, k == 0);
+                if (k == 0) xo[L] = bin(zk, zj, L, true);
+                else if (k != L / 2) xo[L - k] = bin(zj, zk, L - k, false);
+            }
+        }
+    } else if constexpr (MODE == 1) {
         // r2c stitch out of LDS: bins k in [0, L], X[k] = a - i*w*c
         float2* xo = (float2*)dst_v + row * (L + 1);
         if (active) {
@@ -361,10 +402,11 @@ hipError_t dispatch_mode(int mode, int dir, const LdsArgs& a) {
     return launch_one<LOGL, LOGE, 1, 2>(a);
 }
 
-// 32 elements per thread (split exchange): c2c and c2r only
+// 32 elements per thread (split exchange)
 template <int LOGL>
 hipError_t dispatch_split(int mode, int dir, const LdsArgs& a) {
     if (mode == 0) return dir < 0 ? launch_one<LOGL, 5, -1, 0>(a) : launch_one<LOGL, 5, 1, 0>(a);
+    if (mode == 1) return launch_one<LOGL, 5, -1, 1>(a);
     if (mode == 2) return launch_one<LOGL, 5, 1, 2>(a);
     return hipErrorInvalidValue;
 }
@@ -386,11 +428,12 @@ hipError_t dispatch_elems(int loge, int mode, int dir, const LdsArgs& a) {
 bool lds_supported(int log2l, int elems, int mode) {
     if (log2l < 0 || log2l > kMaxLdsLog2) return false;
     if (elems != 0 && elems != 4 && elems != 8 && elems != 16 && elems != 32) return false;
-    // 32 elements per thread (split exchange) exist for 2^10..2^15 and never
-    // for the r2c stitch; 8192 and 16384 points take 16 or 32; 32768 only 32
-    if (elems == 32 && (log2l < 10 || mode == 1)) return false;
+    // 32 elements per thread (split exchange) exist for 2^10..2^15 (the r2c
+    // stitch then runs through the output row); 8192 and 16384 points take
+    // 16 or 32; 32768 only 32
+    if (elems == 32 && log2l < 10) return false;
     if (log2l >= 13 && elems != 0 && elems < 16) return false;
-    if (log2l == 15 && (mode == 1 || (elems != 0 && elems != 32))) return false;
+    if (log2l == 15 && elems != 0 && elems != 32) return false;
     return true;
 }
 

@@ -300,7 +300,7 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
         case MFFT_FLOW_LDS_FUSED:
             if (!mfft::lds_supported(logc, prm[0], lds_mode))
                 return fail(MFFT_ERR_UNSUPPORTED,
-                            "LDS_FUSED runs core lengths up to 2^%d (r2c: 2^14) with 4, 8, 16 or 32 "
+                            "LDS_FUSED runs core lengths up to 2^%d with 4, 8, 16 or 32 "
                             "elements per thread (32 from 2^10; 2^13, 2^14: 16 or 32; 2^15: 32) "
                             "(got core length %lld, elements %d)",
                             mfft::kMaxLdsLog2, (long long)core_n, prm[0]);

@@ -81,14 +81,20 @@ def flow_params(executed: str, n: int, transform_type: str, block, params: dict)
     # r2c/c2r, whose core is n/2: keep its flow where the flow can run that
     # core, else let the library pick (LDS up to 32768, four-step above).
     if kind == "lds":
-        # LDS kernel limits: core <= 32768 (r2c: 16384); 32 elements per
-        # thread from 1024 points and never for r2c; >= 16 from 8192 points
+        # LDS kernel limits: core <= 32768; 32 elements per thread from 1024
+        # points; >= 16 from 8192 points
         e = int(params.get("elems", 0))
         logc = core.bit_length() - 1
-        if core > 32768 or (transform_type == "r2c" and core > 16384):
+        if core > 32768:
             return native.FLOW_AUTO, ()
-        if e == 32 and (logc < 10 or transform_type == "r2c"):
+        if e == 32 and logc < 10:
             e = 0
+        # r2c cores below 32768 run with 16 elements per thread: the
+        # 32-element kernel stitches through the output row (one more pass
+        # over it, measured 1.3-1.8x slower there); at 32768 it is the only
+        # single-pass form
+        if e == 32 and transform_type == "r2c" and logc < 15:
+            e = 16
         # c2r cores below 32768 run with 16 elements per thread: they load
         # each bin once and pair it with its mirror bin through LDS, where the
         # 32-element kernel (no registers to spare for the pairs) loads every

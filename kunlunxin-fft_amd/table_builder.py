@@ -72,18 +72,17 @@ def cells(quick: bool = False):
 
 def real_candidates(n: int, b: int, transform_type: str, space):
     """Challengers for a real transform of length n (complex core n/2): the
-    LDS kernel's fused real modes at each elements-per-thread setting it
-    runs (R2C up to a 16384-point core and 16 elements; C2R up to 32768),
-    with the start stagger in large batches, and the four-step core."""
+    LDS kernel's fused real modes (up to a 32768-point core; 32 elements per
+    thread only there, where the runner maps 32 to 16 below it), with the
+    start stagger in large batches, and the four-step core."""
     sfx = "" if b == 1 else "_batch"
     core = n // 2
     logc = int(math.log2(core)) if core >= 1 else 0
     out = []
-    lds_max = 16384 if transform_type == "r2c" else 32768
-    if 1 <= core <= lds_max:
+    if 1 <= core <= 32768:
         for e in space.lds_elems:
-            if e == 32 and (transform_type == "r2c" or logc < 15):
-                continue  # r2c never 32; c2r below 32768 maps 32 to 16
+            if e == 32 and logc < 15:
+                continue  # real cores below 32768 map 32 to 16
             if logc >= 13 and e < 16:
                 continue
             if logc == 15 and e != 32:

@@ -313,6 +313,22 @@ def test_c2r_mirror_pairs(gpu, elems, n, b):
     check(y.reshape(b, n), ref, f"c2r elems={elems} N={n} B={b}")
 
 
+@pytest.mark.parametrize("n", [1 << k for k in range(11, 17)])
+@pytest.mark.parametrize("b", [1, 5, 11])
+def test_r2c_32_elements_stitch_through_output(gpu, n, b):
+    """R2C with 32 elements per thread (the split exchange): the core outputs
+    go to the output row, then each thread turns disjoint mirror pairs into
+    bins in place.  Small cores put several transforms in one workgroup, so
+    ragged batches leave some of its rows inactive."""
+    rng = np.random.default_rng(6000 + n + b)
+    h = rng.standard_normal((b, n)).astype(np.float32)
+    p = native.NativePlan(n, b, "r2c", "forward", "ortho", native.FLOW_LDS_FUSED, (32,))
+    x = torch.from_numpy(h).to(gpu)
+    y = torch.full((b, n // 2 + 1), float("nan"), dtype=torch.complex64, device=gpu)
+    p.execute(x.data_ptr(), y.data_ptr(), torch.cuda.current_stream(gpu).cuda_stream)
+    check(y.cpu().numpy(), np.fft.rfft(h.astype(np.float64), norm="ortho"), f"r2c e32 N={n} B={b}")
+
+
 @pytest.mark.parametrize("name", ["fft_lds_fused", "fft_four_step", "fft_dit"])
 def test_c2r_ignores_dc_nyquist_imag(gpu, golden, name):
     n = 256

@@ -20,9 +20,12 @@ def test_lds_params_map_to_elems_and_stagger():
     assert flow_params("fft_lds_fused", 512, "c2c", 256, {"elems": 32})[1] == (0, 0)
     assert flow_params("fft_lds_fused", 8192, "c2c", 256, {"elems": 8})[1] == (0, 0)
     assert flow_params("fft_lds_fused", 32768, "c2c", 256, {"elems": 16, "stagger": 3})[1] == (0, 3)
-    # a real transform's core is n/2; r2c cores stop at 16384 and never take 32
-    assert flow_params("fft_lds_fused", 2048, "r2c", 256, {"elems": 32})[1] == (0, 0)
-    assert flow_params("fft_lds_fused", 1 << 16, "r2c", 256, {})[0] == native.FLOW_AUTO
+    # a real transform's core is n/2: up to 32768 in the LDS kernel; r2c and
+    # c2r cores below 32768 take 16 where a c2c entry says 32
+    assert flow_params("fft_lds_fused", 2048, "r2c", 256, {"elems": 32})[1] == (16, 0)
+    assert flow_params("fft_lds_fused", 1 << 16, "r2c", 256, {})[0] == native.FLOW_LDS_FUSED
+    assert flow_params("fft_lds_fused", 1 << 16, "r2c", 256, {"elems": 32, "stagger": 1})[1] == (0, 1)
+    assert flow_params("fft_lds_fused", 1 << 17, "r2c", 256, {})[0] == native.FLOW_AUTO
     assert flow_params("fft_lds_fused", 1 << 16, "c2r", 256, {})[0] == native.FLOW_LDS_FUSED
     # c2r takes 16 elements per thread where a c2c entry says 32 (core < 32768)
     assert flow_params("fft_lds_fused_batch", 1 << 14, "c2r", 256, {"elems": 32, "stagger": 1})[1] == (16, 1)
@@ -103,9 +106,9 @@ def test_shipped_table_uses_only_published_params():
 
 
 def test_real_candidates_respect_the_real_modes():
-    """R2C runs the LDS kernel up to a 16384-point core and never with 32
-    elements; C2R up to 32768 (32 elements only there); every candidate
-    passes the loader's contract as an exact-semantic entry."""
+    """Both real modes run the LDS kernel up to a 32768-point core, with 32
+    elements per thread only there; every candidate passes the loader's
+    contract as an exact-semantic entry."""
     sp = DesignSpace.load()
     for n in (1 << 10, 1 << 14, 1 << 15, 1 << 16, 1 << 20):
         b = max(64, (1 << 25) // n)
@@ -113,12 +116,8 @@ def test_real_candidates_respect_the_real_modes():
             cands = real_candidates(n, b, tt, sp)
             assert cands
             lds = [c for c in cands if c[1].startswith("fft_lds")]
-            if tt == "r2c":
-                assert all(c[3].get("elems") != 32 for c in lds)
-                assert bool(lds) == (n // 2 <= 16384)
-            else:
-                assert all(c[3].get("elems") != 32 for c in lds if n // 2 < 32768)
-                assert bool(lds) == (n // 2 <= 32768)
+            assert all(c[3].get("elems") != 32 for c in lds if n // 2 < 32768)
+            assert bool(lds) == (n // 2 <= 32768)
             for label, name, block, params, (real, unit, flow_id) in cands:
                 e = _entry(params, real=real, unit=unit, n=n, b=b, executed=name)
                 e.update(transform_type=tt, transform_direction=td, normalization="backward")

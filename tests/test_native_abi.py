@@ -46,7 +46,8 @@ def test_struct_layouts():
     (dict(n=16, batch=1, transform_type="c2r", transform_direction="forward"), "inverse"),
     (dict(n=16, batch=1, flow=native.FLOW_FOUR_STEP), "FOUR_STEP"),
     (dict(n=1 << 16, batch=1, flow=native.FLOW_LDS_FUSED), "LDS_FUSED"),
-    (dict(n=1 << 15, batch=1, transform_type="r2c", flow=native.FLOW_LDS_FUSED, params=(32,)), "LDS_FUSED"),
+    (dict(n=1 << 17, batch=1, transform_type="r2c", flow=native.FLOW_LDS_FUSED), "LDS_FUSED"),
+    (dict(n=1 << 16, batch=1, transform_type="r2c", flow=native.FLOW_LDS_FUSED, params=(16,)), "LDS_FUSED"),
     (dict(n=2, batch=1, flow=native.FLOW_RADIX4_DIT), "core length"),
     (dict(n=64, batch=1, flow=native.FLOW_RADIX2_DIT, params=(32,)), "threads per block"),
     (dict(n=64, batch=1, flow=99), "unknown flow"),
