@@ -51,8 +51,9 @@ struct LdsCfg {
     static constexpr int P = sched_passes(LOGL, LE);       // passes
     // Real and imaginary parts exchanged separately through a float array:
     // half the LDS, twice the barriers.  Always with 32 elements per thread;
-    // with 16 from kSplit16MinLog points (never for the r2c stitch, which
-    // reads whole complex values out of LDS).
+    // with 16 from kSplit16MinLog points, except for r2c, whose 16-element
+    // stitch reads whole complex values out of LDS (the 32-element r2c
+    // kernel stitches through its output row instead).
     static constexpr bool SPLIT = LE == 5 || (LE == 4 && LOGL >= kSplit16MinLog && MODE != 1);
     // Exchange padding: one slot per 16 elements in float2 rows and in the
     // split rows of 16-element threads (pad; a half-wave's stride-16 writes
