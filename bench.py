@@ -19,7 +19,8 @@ Also reported (on the same JSON line):
   per N, from HIP events;
 * ``latency_n2048_b1``: the reference protocol (warmup 5, 5 x 32 trials,
   device sync per trial, pooled p50, scripts/issue10_wp3_holdout.py:176-190)
-  for execute_fft_plan, plus the kernel-only event p50;
+  for execute_fft_plan, plus the kernel-only event p50 and the per-transform
+  time of 64 executes recorded into one HIP graph and replayed;
 * ``config2``: latency and GB/s of the reference's small-batch configuration (N in {1024, 2048}, B in
   {16, 64}); ``config3``: the same for inverse C2C, R2C and C2R at N in {256, 4096}, B in {1, 64}
   (real transforms count 4N + 8(N/2+1) bytes per row); ``config4``: the same for N=2^20 B=1 and
@@ -278,9 +279,36 @@ def main() -> int:
                 "api_gbps": round(nbytes / (p50 * 1e-3) / 1e9, 3),
                 "kernel_gbps": round(nbytes / (ev * 1e-3) / 1e9, 1)}
 
+    def graph_replay_us(n, reps_per_graph=64, replays=20):
+        """Per-transform time of N-point B=1 executes recorded into one HIP
+        graph (torch.cuda.CUDAGraph) and replayed: what a launch-bound caller
+        gets without the per-call host path."""
+        plan = pkg.plan_fft("dit", n, batch=1, profile_hash=prof)
+        x = torch.randn((n,), dtype=torch.complex64, device=dev, generator=gen)
+        pkg.execute_fft_plan(plan, x)
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            pkg.execute_fft_plan(plan, x)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=side):
+                for _ in range(reps_per_graph):
+                    pkg.execute_fft_plan(plan, x)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(replays):
+            graph.replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / (replays * reps_per_graph) * 1e6
+
     lat, cfg2, cfg3, cfg4 = None, [], [], []
     if not args.no_latency:
         lat = latency(2048, 1)
+        lat["graph_replay_us_per_transform"] = round(graph_replay_us(2048), 3)
         log(f"latency N=2048 B=1: {lat}")
         cfg2 = [latency(n, b) for n in (1024, 2048) for b in (16, 64)]
         for c in cfg2:
