@@ -309,6 +309,10 @@ def main() -> int:
     if not args.no_latency:
         lat = latency(2048, 1)
         lat["graph_replay_us_per_transform"] = round(graph_replay_us(2048), 3)
+        # the reference's published p50 for this cell on its own hardware (Kunlunxin P800,
+        # frozen selector, results/p800/issue9_v61/reports/steady_report.csv:55); context only
+        lat["reference_p800_api_p50_ms"] = 0.4036
+        lat["api_p50_speedup_vs_reference_p800"] = round(0.4036 / lat["api_wall_p50_ms"], 1)
         log(f"latency N=2048 B=1: {lat}")
         cfg2 = [latency(n, b) for n in (1024, 2048) for b in (16, 64)]
         for c in cfg2:
