@@ -32,7 +32,7 @@ Also reported (on the same JSON line):
   comparison column only;
 * ``cpu_baseline``: the reference's own CPU FFT (butterfly::fft_dit built
   into oracle/_ref; the C restatement when that build is absent) on one core,
-  on a bounded sample -- 16 transforms of each N = 2^10..2^20 -- median of 3,
+  on a bounded sample -- 16 transforms of each N = 2^10..2^20 -- median of 5,
   plus the same rows spread over up to 16 host threads (``all_cores``).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -396,17 +396,17 @@ def main() -> int:
         tot_s, tot_mt, tot_bytes, kinds = 0.0, 0.0, 0, set()
         for n in SIZES:
             h = rng.standard_normal((rows, n)) + 1j * rng.standard_normal((rows, n))
-            s, kind = oracle.time_cpu_fft(h, threads=1, reps=3)
+            s, kind = oracle.time_cpu_fft(h, threads=1, reps=5)
             kinds.add(kind)
             tot_s += s
-            s_mt, kind_mt = oracle.time_cpu_fft(h, threads=threads, reps=3)
+            s_mt, kind_mt = oracle.time_cpu_fft(h, threads=threads, reps=5)
             kinds.add(kind_mt)
             tot_mt += s_mt
             tot_bytes += 16 * n * rows
         cpu = {"value": round(tot_bytes / tot_s / 1e9, 4), "unit": "GB/s", "cores": 1,
                "kind": "reference" if kinds == {"reference"} else "port",
                "sample": f"{rows} transforms of each N = 2^10..2^20 (complex<double>, butterfly::fft_dit "
-                         f"with its per-stage twiddle rebuild), median of 3 passes, {tot_s:.1f} s per pass",
+                         f"with its per-stage twiddle rebuild), median of 5 passes, {tot_s:.1f} s per pass",
                "gpu_over_cpu": round(value / (tot_bytes / tot_s / 1e9), 1),
                "all_cores": {"value": round(tot_bytes / tot_mt / 1e9, 4), "cores": threads,
                              "sample": f"the same rows split over {threads} std::threads "
