@@ -169,11 +169,7 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
                                 xk.y = 0.0f;
                                 xj.y = 0.0f;
                             }
-                            const float ar = 0.5f * (xk.x + xj.x), ai = 0.5f * (xk.y - xj.y);
-                            const float cr = 0.5f * (xk.x - xj.x), ci = 0.5f * (xk.y + xj.y);
-                            const float2 t = tw_real[i];
-                            const float wr = t.x, wi = -t.y;
-                            v[e] = make_float2(ar - (wr * ci + wi * cr), ai + (wr * cr - wi * ci));
+                            v[e] = c2r_pre_bin(xk, xj, tw_real[i]);
                         }
                     });
                 });
@@ -194,11 +190,7 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
                             xk.y = 0.0f;
                             xj.y = 0.0f;
                         }
-                        const float ar = 0.5f * (xk.x + xj.x), ai = 0.5f * (xk.y - xj.y);
-                        const float cr = 0.5f * (xk.x - xj.x), ci = 0.5f * (xk.y + xj.y);
-                        const float2 t = tw_real[i];
-                        const float wr = t.x, wi = -t.y;
-                        z = make_float2(ar - (wr * ci + wi * cr), ai + (wr * cr - wi * ci));
+                        z = c2r_pre_bin(xk, xj, tw_real[i]);
                     }
                     v[m.value * R0 + q.value] = z;
                 });
@@ -310,17 +302,9 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
             for (int k = j; k <= L / 2; k += T) {
                 const float2 zk = xo[k];
                 const float2 zj = xo[(L - k) & (L - 1)];
-                auto bin = [&](float2 a, float2 c, int kk, bool edge) {
-                    const float ar = 0.5f * (a.x + c.x), ai = 0.5f * (a.y - c.y);
-                    const float cr = 0.5f * (a.x - c.x), ci = 0.5f * (a.y + c.y);
-                    const float2 w = tw_real[kk];
-                    const float xr = ar + (w.x * ci + w.y * cr);
-                    const float xi = edge ? 0.0f : ai - (w.x * cr - w.y * ci);
-                    return make_float2(xr * scale, xi * scale);
-                };
-                xo[k] = bin(zk, zj, k, k == 0);
-                if (k == 0) xo[L] = bin(zk, zj, L, true);
-                else if (k != L / 2) xo[L - k] = bin(zj, zk, L - k, false);
+                xo[k] = r2c_bin(zk, zj, tw_real[k], scale, k == 0);
+                if (k == 0) xo[L] = r2c_bin(zk, zj, tw_real[L], scale, true);
+                else if (k != L / 2) xo[L - k] = r2c_bin(zj, zk, tw_real[L - k], scale, false);
             }
         }
     } else if constexpr (MODE == 1) {
@@ -330,13 +314,7 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
             auto stitch = [&](int k) {
                 const float2 zk = lt[pad(k & (L - 1))];
                 const float2 zj = lt[pad((L - k) & (L - 1))];
-                const float ar = 0.5f * (zk.x + zj.x), ai = 0.5f * (zk.y - zj.y);
-                const float cr = 0.5f * (zk.x - zj.x), ci = 0.5f * (zk.y + zj.y);
-                const float2 w = tw_real[k];
-                const float xr = ar + (w.x * ci + w.y * cr);
-                float xi = ai - (w.x * cr - w.y * ci);
-                if (k == 0 || k == L) xi = 0.0f;
-                xo[k] = make_float2(xr * scale, xi * scale);
+                xo[k] = r2c_bin(zk, zj, tw_real[k], scale, k == 0 || k == L);
             };
             static_for<0, E>([&](auto m) { stitch(j + m.value * T); });
             if (j == 0) stitch(L);

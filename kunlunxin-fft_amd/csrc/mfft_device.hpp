@@ -175,6 +175,27 @@ __device__ __forceinline__ void store_nt(float2* p, float2 x) {
     __builtin_nontemporal_store(v, reinterpret_cast<nt_float2*>(p));
 }
 
+// Real transforms on a half-length complex core (kernels.py:1127-1229
+// formulas).  R2C stitch: bin k from core outputs zk = Z[k], zj = Z[L-k]
+// and w = exp(-2 pi i k / n): X[k] = a - i w c with a = (zk + conj zj)/2,
+// c = (zk - conj zj)/2; `edge` (bins 0 and L) zeroes the imaginary part.
+__device__ __forceinline__ float2 r2c_bin(float2 zk, float2 zj, float2 w, float scale, bool edge) {
+    const float ar = 0.5f * (zk.x + zj.x), ai = 0.5f * (zk.y - zj.y);
+    const float cr = 0.5f * (zk.x - zj.x), ci = 0.5f * (zk.y + zj.y);
+    const float xr = ar + (w.x * ci + w.y * cr);
+    const float xi = edge ? 0.0f : ai - (w.x * cr - w.y * ci);
+    return make_float2(xr * scale, xi * scale);
+}
+// C2R pre-twiddle: core input Z[k] from bins xk = X[k], xj = X[L-k] and
+// t = exp(-2 pi i k / n): Z[k] = a + i conj(t) c (callers zero the imaginary
+// parts of bins 0 and L).
+__device__ __forceinline__ float2 c2r_pre_bin(float2 xk, float2 xj, float2 t) {
+    const float ar = 0.5f * (xk.x + xj.x), ai = 0.5f * (xk.y - xj.y);
+    const float cr = 0.5f * (xk.x - xj.x), ci = 0.5f * (xk.y + xj.y);
+    const float wr = t.x, wi = -t.y;
+    return make_float2(ar - (wr * ci + wi * cr), ai + (wr * cr - wi * ci));
+}
+
 // Multiply v[OFF + q] (q = 1..R-1) by W^(q*k) of a pass whose table rows
 // `tp[i*NS + k]` hold W^(2^i * k): loads the log2(R) power-of-two roots
 // (coalesced across lanes) and composes the rest, w_q = w_(q - hb) * w_hb,

@@ -161,14 +161,6 @@ __global__ void bitrev_kernel(const float2* __restrict__ x, float2* __restrict__
 // read once (non-temporal: it is not read again).  Pair 0 also writes bin
 // np (both from Z[0]); pair np/2 is one bin.  A block covers 256 pairs of
 // one row (bpr blocks per row), so the row is a per-block quotient.
-__device__ __forceinline__ float2 stitch_bin(float2 zk, float2 zj, float2 w, float scale, bool edge) {
-    const float ar = 0.5f * (zk.x + zj.x), ai = 0.5f * (zk.y - zj.y);
-    const float cr = 0.5f * (zk.x - zj.x), ci = 0.5f * (zk.y + zj.y);
-    const float xr = ar + (w.x * ci + w.y * cr);
-    const float xi = edge ? 0.0f : ai - (w.x * cr - w.y * ci);
-    return make_float2(xr * scale, xi * scale);
-}
-
 __global__ __launch_bounds__(256) void r2c_stitch_kernel(const float2* __restrict__ z, float2* __restrict__ x,
                                                          const float2* __restrict__ tw_real, int64_t np, int bpr,
                                                          float scale) {
@@ -181,9 +173,9 @@ __global__ __launch_bounds__(256) void r2c_stitch_kernel(const float2* __restric
     const int64_t j = (np - k) & (np - 1);
     const float2 zk = load_nt(zr + k);
     const float2 zj = load_nt(zr + j);
-    xr[k] = stitch_bin(zk, zj, tw_real[k], scale, k == 0);
-    if (k == 0) xr[np] = stitch_bin(zk, zj, tw_real[np], scale, true);
-    else if (k != half) xr[np - k] = stitch_bin(zj, zk, tw_real[np - k], scale, false);
+    xr[k] = r2c_bin(zk, zj, tw_real[k], scale, k == 0);
+    if (k == 0) xr[np] = r2c_bin(zk, zj, tw_real[np], scale, true);
+    else if (k != half) xr[np - k] = r2c_bin(zj, zk, tw_real[np - k], scale, false);
 }
 
 // C2R pre-twiddle (kernels.py:1180-1229 formula): Z[k] = a + i*w'*c with
@@ -191,13 +183,6 @@ __global__ __launch_bounds__(256) void r2c_stitch_kernel(const float2* __restric
 // w' = exp(+2*pi*i*k/n); imaginary parts of bins 0 and np are ignored.
 // Paired like the stitch: thread k in [0, np/2] reads X[k] and X[np-k] once
 // and writes Z[k] and Z[np-k] (pair 0 only Z[0]; pair np/2 one value).
-__device__ __forceinline__ float2 pre_bin(float2 xk, float2 xj, float2 t) {
-    const float ar = 0.5f * (xk.x + xj.x), ai = 0.5f * (xk.y - xj.y);
-    const float cr = 0.5f * (xk.x - xj.x), ci = 0.5f * (xk.y + xj.y);
-    const float wr = t.x, wi = -t.y;
-    return make_float2(ar - (wr * ci + wi * cr), ai + (wr * cr - wi * ci));
-}
-
 __global__ __launch_bounds__(256) void c2r_pre_kernel(const float2* __restrict__ x, float2* __restrict__ z,
                                                       const float2* __restrict__ tw_real, int64_t np, int bpr) {
     const int row = (int)(blockIdx.x / (unsigned)bpr);
@@ -212,8 +197,8 @@ __global__ __launch_bounds__(256) void c2r_pre_kernel(const float2* __restrict__
         xk.y = 0.0f;
         xj.y = 0.0f;
     }
-    zr[k] = pre_bin(xk, xj, tw_real[k]);
-    if (k != 0 && k != half) zr[np - k] = pre_bin(xj, xk, tw_real[np - k]);
+    zr[k] = c2r_pre_bin(xk, xj, tw_real[k]);
+    if (k != 0 && k != half) zr[np - k] = c2r_pre_bin(xj, xk, tw_real[np - k]);
 }
 
 inline unsigned grid_for(int64_t total, int block) { return (unsigned)((total + block - 1) / block); }
