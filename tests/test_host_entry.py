@@ -1,7 +1,6 @@
 """Host-only plan API contract (no GPU): restates the reference's
 tests/test_entry.py, test_selector.py and test_semantic_key.py contracts
 against this package's plan_fft / select / load_table."""
-import copy
 import json
 import os
 
