@@ -73,6 +73,7 @@ def main() -> int:
     ap.add_argument("--no-vendor", action="store_true", help="skip the torch.fft (rocFFT) comparison column")
     ap.add_argument("--sizes", default="", help="comma-separated subset of N (profiling runs)")
     ap.add_argument("--no-real", action="store_true", help="skip the R2C / C2R throughput leg")
+    ap.add_argument("--detail-out", default="", help="also write the JSON line, indented, to this file")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every box here has one MI355X; "
@@ -435,9 +436,8 @@ def main() -> int:
         "real_per_size": real_rows,
     }
     print(json.dumps(line), flush=True)
-    out_dir = os.path.join(ROOT, "gpurun_out")
-    if os.path.isdir(out_dir):
-        with open(os.path.join(out_dir, "bench_detail.json"), "w") as f:
+    if args.detail_out:
+        with open(args.detail_out, "w") as f:
             json.dump(line, f, indent=1)
     return 0
 

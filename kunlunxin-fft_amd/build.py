@@ -20,7 +20,9 @@ LIB = os.path.join(HERE, "libmfft.so")
 ARCH = "gfx950"
 
 # Packed-FP32 instructions are disabled on purpose: hipcc must not emit
-# v_pk_{add,mul,fma}_f32 (see DESIGN notes on the gfx950 pool).
+# v_pk_{add,mul,fma}_f32, some forms of which have given wrong results, now
+# and then and with no error, on the gfx950 machines this library is
+# measured on (hipcc's host pass warns that it does not know the feature).
 HIP_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
