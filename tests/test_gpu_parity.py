@@ -428,6 +428,31 @@ def test_config5_selector_and_m0_cells(gpu, n, b):
     check(execute_fft_plan(m0, xd).cpu().numpy(), ref, f"C5 N={n} B={b} M0")
 
 
+@pytest.mark.parametrize("n", [16, 256, 4096, 16384])
+@pytest.mark.parametrize("b", [1, 64])
+@pytest.mark.parametrize("tt,td,norm", [("c2c", "inverse", "ortho"), ("r2c", "forward", "forward"),
+                                        ("c2r", "inverse", "none")])
+def test_config5_cells_other_semantics(gpu, n, b, tt, td, norm):
+    """The C2C entries of the config-5 sweep also answer the other
+    semantics (legacy entries carry no semantic triple): the selected plan
+    runs inverse, R2C and C2R with any norm on the cell's shape."""
+    prof = DeviceProfile.load().hash()
+    plan = plan_fft("dit", n, batch=b, profile_hash=prof, transform_type=tt, transform_direction=td, norm=norm)
+    assert not plan.fallback
+    rng = np.random.default_rng(8000 + n + b)
+    if tt == "r2c":
+        h = rng.standard_normal((b, n)).astype(np.float32)
+        ref = np.fft.rfft(h.astype(np.float64), norm=norm)
+    elif tt == "c2r":
+        h = (rng.standard_normal((b, n // 2 + 1)) + 1j * rng.standard_normal((b, n // 2 + 1))).astype(np.complex64)
+        ref = np.fft.irfft(h.astype(np.complex128), n=n, norm="forward")  # "none" on the inverse: no 1/N
+    else:
+        h = seeded_c64(n, b, session=11).reshape(b, n)
+        ref = np_ref(h, td, norm)
+    y = execute_fft_plan(plan, torch.from_numpy(h if b > 1 else h[0]).to(gpu)).cpu().numpy()
+    check(y.reshape(ref.shape), ref, f"C5 {tt} {td} {norm} N={n} B={b} ({plan.executed})")
+
+
 def _real_entries():
     import json
     import os
