@@ -36,9 +36,12 @@
  * It enqueues on `stream` (a hipStream_t; NULL = the default stream) of the
  * device that was current at plan creation, which must be current at
  * execute.  `in` and `out` must not overlap; `in` is never written.
- * Executes of one plan that overlap in time (two streams or two host threads)
- * share the plan's workspace and race: serialise them, give each its own
- * workspace (mfft_execute_ws), or create one plan per stream.
+ * A plan is immutable after creation.  A plan that needs no workspace
+ * (mfft_plan_workspace_size = 0: every LDS_FUSED plan and FOUR_STEP C2C) can
+ * be executed from any number of host threads and streams at once.  Executes
+ * of a plan that needs workspace and overlap in time (two streams or two
+ * host threads) share the plan's workspace and race: serialise them, give
+ * each its own workspace (mfft_execute_ws), or create one plan per stream.
  */
 #ifndef MFFT_H_
 #define MFFT_H_
