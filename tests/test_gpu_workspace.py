@@ -132,3 +132,25 @@ def test_caller_workspace_two_streams(gpu):
     for h, y in ((h1, y1), (h2, y2)):
         ref = np.fft.fft(h.astype(np.complex128))
         assert oracle.rel_l2(y.cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("flow,params,n", [(native.FLOW_LDS_FUSED, (), 4096), (native.FLOW_FOUR_STEP, (256,), 1 << 16)])
+def test_no_workspace_plan_two_streams(gpu, flow, params, n):
+    """A plan that needs no workspace holds nothing an execute writes, so two
+    streams may run it at once."""
+    b = 32
+    p = native.NativePlan(n, b, "c2c", "forward", "backward", flow, params)
+    assert p.workspace_size() == 0 and p.info.workspace_bytes == 0
+    s1, s2 = torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)
+    h1, x1 = _inputs(n, b, "c2c", gpu, seed=21)
+    h2, x2 = _inputs(n, b, "c2c", gpu, seed=22)
+    y1, y2 = _out(n, b, "c2c", gpu), _out(n, b, "c2c", gpu)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        p.execute(x1.data_ptr(), y1.data_ptr(), s1.cuda_stream)
+        p.execute(x2.data_ptr(), y2.data_ptr(), s2.cuda_stream)
+    torch.cuda.synchronize()
+    for h, y in ((h1, y1), (h2, y2)):
+        rows = [0, b - 1]
+        ref = np.fft.fft(h[rows].astype(np.complex128))
+        assert oracle.rel_l2(y[rows].cpu().numpy(), ref) <= TOL
