@@ -25,8 +25,9 @@
 //   0  c2c: core + norm scale in the final store (inverse = conjugated roots)
 //   1  r2c: the real input viewed as n/2 complex (x[2k] + i x[2k+1]) is the
 //      core input for free; the stitch of kernels.py:1127-1177 runs from LDS
-//      (32 elements per thread: from the output row) and writes the n/2+1
-//      bins with the scale
+//      (32 elements per thread: in registers across lane pairs when the core
+//      length is a power of 32, else through the output row) and writes the
+//      n/2+1 bins with the scale
 //   2  c2r: the pre-twiddle of kernels.py:1180-1229 is applied while loading
 //      the n/2+1 bins; the inverse core writes the n real samples as n/2
 //      complex pairs with scale 2*norm_scale
@@ -53,7 +54,7 @@ struct LdsCfg {
     // half the LDS, twice the barriers.  Always with 32 elements per thread;
     // with 16 from kSplit16MinLog points, except for r2c, whose 16-element
     // stitch reads whole complex values out of LDS (the 32-element r2c
-    // kernel stitches through its output row instead).
+    // kernel stitches across lane pairs or through its output row instead).
     static constexpr bool SPLIT = LE == 5 || (LE == 4 && LOGL >= kSplit16MinLog && MODE != 1);
     // Exchange padding: one slot per 16 elements in float2 rows and in the
     // split rows of 16-element threads (pad; a half-wave's stride-16 writes
@@ -68,6 +69,17 @@ struct LdsCfg {
     // block uses at most 70 KB of LDS, so up to 16 waves of it fit a CU when
     // each wave stays within 128 VGPRs.
     static constexpr int MIN_WAVES = SPLIT ? 4 : 1;
+    // Lane pairing of the real modes with 32 elements per thread, whose
+    // registers have no room for the mirror values: when whole waves make
+    // up a transform and the pass next to HBM has the full radix (c2r: the
+    // first pass, always; r2c: the last, when L is a power of 32), thread
+    // t plays Stockham index pair_j(t), which puts the indices j and T - j
+    // in lanes l and l ^ 32 of one wave.  The mirror L - k of every bin
+    // k = j + T*q a thread holds is then its partner lane's element
+    // E - 1 - q, one lane swap away (j = 0 and j = T/2 pair with
+    // themselves).
+    static constexpr bool PAIR =
+        LE == 5 && T >= 64 && (MODE == 2 || (MODE == 1 && sched_logr(LOGL, LE, P - 1) == LE));
     static constexpr int logr(int p) { return sched_logr(LOGL, LE, p); }
     static constexpr int lns(int p) { return sched_lns(LE, p); }
 };
@@ -88,6 +100,20 @@ template <int SH, int K>
 __device__ __forceinline__ int padf_add(int pi, int i) {
     if constexpr (K % (1 << SH) == 0) return pi + K + (K >> SH);
     else return padf<SH>(i + K);
+}
+
+// Stockham index of thread t of a T-thread transform under lane pairing:
+// lanes 0-31 of wave w take 32w + l, lanes 32-63 take T - (32w + l - 32),
+// except that lane 32 of wave 0 takes T/2 (T - 0 would be index 0 again).
+template <int T>
+__device__ __forceinline__ int pair_j(int t) {
+    const int l = t & 63;
+    const int u = ((t >> 6) << 5) + (l & 31);
+    return l < 32 ? u : (u == 0 ? T / 2 : T - u);
+}
+// the value lane l ^ 32 holds
+__device__ __forceinline__ float2 swap_halves(float2 x) {
+    return make_float2(__shfl_xor(x.x, 32), __shfl_xor(x.y, 32));
 }
 
 template <int LOGL, int LOGE, int DIR, int MODE>
@@ -115,7 +141,7 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
     }
     const int tid = threadIdx.x;
     const int tl = tid / T;
-    const int j = tid & (T - 1);
+    const int j = C::PAIR ? pair_j<T>(tid & (T - 1)) : tid & (T - 1);
     const int64_t row = (int64_t)blockIdx.x * C::TPB + tl;
     const bool active = row < rows;
     float2* lt = lds + (NEED_LDS ? tl * C::PITCH : 0);
@@ -127,7 +153,51 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
     {
         constexpr int R0 = 1 << C::logr(0);
         constexpr int NB0 = E / R0;
-        if constexpr (MODE == 2 && P > 1 && C::LE < 5) {
+        if constexpr (MODE == 2 && C::PAIR) {
+            // Each bin is loaded once (non-temporal), v[q] = X[j + T*q]; the
+            // mirror of bin j + T*q is the partner lane's v[E-1-q], except for
+            // j = T/2 (its own v[E-1-q]) and j = 0 (its own v[E-q], and bin L
+            // for q = 0, loaded by that thread).  The pairs (s, E-1-s) are
+            // turned into core inputs from s = E/2 - 1 down to 0, so what
+            // j = 0 reads is still the bin: v[E-s] belongs to a later pair,
+            // and v[s+1], already turned, was kept in `prev`.
+            static_assert(R0 == E && NB0 == 1, "lane pairing needs a full radix first pass");
+            const float2* xb = (const float2*)src_v + row * (L + 1);
+            static_for<0, E>([&](auto q) {
+                v[q.value] = active ? load_nt(xb + j + q.value * T) : make_float2(0.0f, 0.0f);
+            });
+            const bool jz = j == 0, jh = j == T / 2;
+            const float2 xny = (active && jz) ? load_nt(xb + L) : make_float2(0.0f, 0.0f);
+            // exp(-2 pi i (j + T*s) / 2L) = tw_real[j] * exp(-2 pi i s / 2E):
+            // one table load and compile-time rotations
+            const float2 tj = tw_real[j];
+            float2 prev = make_float2(0.0f, 0.0f);
+            static_for<0, E / 2>([&](auto ss) {
+                constexpr int s = E / 2 - 1 - ss.value;
+                constexpr int sb = E - 1 - s;
+                const float2 a = v[s], b = v[sb];
+                const float2 pa = swap_halves(b), pb = swap_halves(a);
+                // selects, not branches: the lane's own values for j = 0
+                // (bin 0 pairs with bin L, both imaginary parts ignored; bin
+                // L/2 is its own mirror) and j = T/2, the partner's otherwise
+                float2 xa = a;
+                float2 ma, mb;
+                if constexpr (s == 0) {
+                    xa.y = jz ? 0.0f : a.y;
+                    ma = jz ? make_float2(xny.x, 0.0f) : (jh ? b : pa);
+                } else {
+                    ma = jz ? v[E - s] : (jh ? b : pa);
+                }
+                if constexpr (s == E / 2 - 1) mb = jz ? b : (jh ? a : pb);
+                else mb = jz ? prev : (jh ? a : pb);
+                v[s] = c2r_pre_bin(xa, ma, rot<2 * E, s, -1>(tj));
+                v[sb] = c2r_pre_bin(b, mb, rot<2 * E, sb, -1>(tj));
+                prev = a;
+                // keeps the scheduler from hoisting later pairs' lane swaps,
+                // whose results would not fit the registers beside v
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        } else if constexpr (MODE == 2 && P > 1 && C::LE < 5) {
             // Each bin is loaded once (non-temporal); the partner bin L - i
             // of the pre-twiddle comes from the thread that loaded it,
             // through LDS, one component at a time (the exchange rows hold L
@@ -175,9 +245,10 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
                 });
             });
         } else if constexpr (MODE == 2) {
-            // single-pass lengths, and 32 elements per thread (whose partner
-            // values would not fit the register budget): both bins straight
-            // from global memory
+            // single-pass lengths, and 32 elements per thread with one
+            // transform per 32 lanes (no lane pairing; the partner values
+            // would not fit the register budget): both bins straight from
+            // global memory
             const float2* xb = (const float2*)src_v + row * (L + 1);
             static_for<0, NB0>([&](auto m) {
                 static_for<0, R0>([&](auto q) {
@@ -275,11 +346,35 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
     });
 
     // ---- epilogue
-    if constexpr (MODE == 1 && C::SPLIT) {
-        // r2c with 32 elements per thread: the split LDS rows hold one
-        // component at a time and the registers have no room for the mirror
-        // values, so the core outputs z go to the output row itself (L of
-        // its L + 1 bins), and each thread then turns disjoint mirror pairs
+    if constexpr (MODE == 1 && C::PAIR) {
+        // r2c under lane pairing: v[q] = Z[j + T*q] and the mirror of
+        // Z[j + T*q] is the partner lane's v[E-1-q] (own v[E-1-q] for
+        // j = T/2, own v[(E-q) mod E] for j = 0), so every bin is stitched
+        // in registers and stored once; thread j = 0 also writes bin L.
+        static_assert(C::logr(P - 1) == C::LE, "lane pairing needs a full radix last pass");
+        float2* xo = (float2*)dst_v + row * (L + 1);
+        const bool jz = j == 0, jh = j == T / 2;
+        const float2 tj = tw_real[j];  // tw_real[j + T*s] = tj * exp(-2 pi i s / 2E)
+        static_for<0, E / 2>([&](auto ss) {
+            constexpr int s = ss.value;
+            constexpr int sb = E - 1 - s;
+            const float2 a = v[s], b = v[sb];
+            const float2 pa = swap_halves(b), pb = swap_halves(a);
+            const float2 ma = jz ? v[(E - s) % E] : (jh ? b : pa);
+            const float2 mb = jz ? v[s + 1] : (jh ? a : pb);
+            if (active) {
+                xo[j + s * T] = r2c_bin(a, ma, rot<2 * E, s, -1>(tj), scale, s == 0 && jz);
+                xo[j + sb * T] = r2c_bin(b, mb, rot<2 * E, sb, -1>(tj), scale, false);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        if (active && jz) xo[L] = r2c_bin(v[0], v[0], tw_real[L], scale, true);
+    } else if constexpr (MODE == 1 && C::SPLIT) {
+        // r2c with 32 elements per thread and no lane pairing (the last
+        // pass has a smaller radix, or 32 lanes hold a transform): the split
+        // LDS rows hold one component at a time and the registers have no
+        // room for the mirror values, so the core outputs z go to the output
+        // row itself (L of its L + 1 bins), and each thread then turns disjoint mirror pairs
         // (k, L - k) into bins in place: it alone reads and writes those two
         // addresses, so no thread overwrites a value another still needs.
         // The row was last written by this block's own waves (same CU and

@@ -298,7 +298,7 @@ def test_r2c_c2r_match_oracle(gpu, name, n, norm):
 @pytest.mark.parametrize("b", [1, 3, 37])
 def test_c2r_mirror_pairs(gpu, elems, n, b):
     """Fused C2R: each bin is loaded once and meets its mirror bin n/2 - k
-    through LDS (up to 16 elements per thread; 32 load both bins), bin 0
+    through LDS (up to 16 elements per thread; 32: from the partner lane), bin 0
     pairs with bin n/2, and the DC/Nyquist imaginary parts are ignored.
     Ragged batches leave rows of a multi-transform block inactive."""
     if elems < 16 and n > 8192:
@@ -316,10 +316,12 @@ def test_c2r_mirror_pairs(gpu, elems, n, b):
 @pytest.mark.parametrize("n", [1 << k for k in range(11, 17)])
 @pytest.mark.parametrize("b", [1, 5, 11])
 def test_r2c_32_elements_stitch_through_output(gpu, n, b):
-    """R2C with 32 elements per thread (the split exchange): the core outputs
-    go to the output row, then each thread turns disjoint mirror pairs into
-    bins in place.  Small cores put several transforms in one workgroup, so
-    ragged batches leave some of its rows inactive."""
+    """R2C with 32 elements per thread (the split exchange).  A 32768-point
+    core (n = 2^16) ends in a full radix-32 pass and stitches in registers,
+    each bin's mirror coming from the partner lane; the other cores send
+    their outputs to the output row, then each thread turns disjoint mirror
+    pairs into bins in place.  Small cores put several transforms in one
+    workgroup, so ragged batches leave some of its rows inactive."""
     rng = np.random.default_rng(6000 + n + b)
     h = rng.standard_normal((b, n)).astype(np.float32)
     p = native.NativePlan(n, b, "r2c", "forward", "ortho", native.FLOW_LDS_FUSED, (32,))
@@ -327,6 +329,26 @@ def test_r2c_32_elements_stitch_through_output(gpu, n, b):
     y = torch.full((b, n // 2 + 1), float("nan"), dtype=torch.complex64, device=gpu)
     p.execute(x.data_ptr(), y.data_ptr(), torch.cuda.current_stream(gpu).cuda_stream)
     check(y.cpu().numpy(), np.fft.rfft(h.astype(np.float64), norm="ortho"), f"r2c e32 N={n} B={b}")
+
+
+@pytest.mark.parametrize("n", [1 << k for k in range(11, 17)])
+@pytest.mark.parametrize("b", [1, 5, 11])
+def test_c2r_32_elements_lane_pairs(gpu, n, b):
+    """C2R with 32 elements per thread through the C ABI (the Python runner
+    maps 32 to 16 below a 32768-point core).  From a 2048-point core each
+    wave holds the indices j and T - j in lanes l and l ^ 32, so every bin is
+    loaded once and its mirror comes from the partner lane (bin 0 pairs with
+    bin n/2, loaded by the j = 0 lane; j = T/2 and j = 0 pair with
+    themselves); the 1024-point core (one transform per 32 lanes) loads both
+    bins.  The DC and Nyquist imaginary parts are nonzero and ignored."""
+    rng = np.random.default_rng(6500 + n + b)
+    m = n // 2 + 1
+    h = (rng.standard_normal((b, m)) + 1j * rng.standard_normal((b, m))).astype(np.complex64)
+    p = native.NativePlan(n, b, "c2r", "inverse", "backward", native.FLOW_LDS_FUSED, (32,))
+    x = torch.from_numpy(h).to(gpu)
+    y = torch.full((b, n), float("nan"), dtype=torch.float32, device=gpu)
+    p.execute(x.data_ptr(), y.data_ptr(), torch.cuda.current_stream(gpu).cuda_stream)
+    check(y.cpu().numpy(), np.fft.irfft(h.astype(np.complex128), n=n), f"c2r e32 N={n} B={b}")
 
 
 @pytest.mark.parametrize("name", ["fft_lds_fused", "fft_four_step", "fft_dit"])
