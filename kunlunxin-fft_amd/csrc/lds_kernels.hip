@@ -69,17 +69,18 @@ struct LdsCfg {
     // block uses at most 70 KB of LDS, so up to 16 waves of it fit a CU when
     // each wave stays within 128 VGPRs.
     static constexpr int MIN_WAVES = SPLIT ? 4 : 1;
-    // Lane pairing of the real modes with 32 elements per thread, whose
-    // registers have no room for the mirror values: when whole waves make
+    // Lane pairing of the real modes with 16 or 32 elements per thread
+    // (the 32-element registers have no room for the mirror values, and it
+    // saves the 16-element kernels an LDS round trip): when whole waves make
     // up a transform and the pass next to HBM has the full radix (c2r: the
-    // first pass, always; r2c: the last, when L is a power of 32), thread
+    // first pass, always; r2c: the last, when L is a power of E), thread
     // t plays Stockham index pair_j(t), which puts the indices j and T - j
     // in lanes l and l ^ 32 of one wave.  The mirror L - k of every bin
     // k = j + T*q a thread holds is then its partner lane's element
     // E - 1 - q, one lane swap away (j = 0 and j = T/2 pair with
     // themselves).
     static constexpr bool PAIR =
-        LE == 5 && T >= 64 && (MODE == 2 || (MODE == 1 && sched_logr(LOGL, LE, P - 1) == LE));
+        LE >= 4 && T >= 64 && (MODE == 2 || (MODE == 1 && sched_logr(LOGL, LE, P - 1) == LE));
     static constexpr int logr(int p) { return sched_logr(LOGL, LE, p); }
     static constexpr int lns(int p) { return sched_lns(LE, p); }
 };
@@ -303,9 +304,9 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
             }
             dft<R, DIR, m.value * R, 1>(v);
         });
-        if constexpr ((p < P - 1 || MODE == 1) && !C::SPLIT) {
+        if constexpr ((p < P - 1 || (MODE == 1 && !C::PAIR)) && !C::SPLIT) {
             // every thread has read this pass's inputs (pass 0 of c2r: the partner bins)
-            if constexpr (p > 0 || MODE == 2) __syncthreads();
+            if constexpr (p > 0 || (MODE == 2 && !C::PAIR)) __syncthreads();
             static_for<0, NB>([&](auto m) {
                 const int b = j + m.value * T;
                 const int base = ((b >> LNS) << (LNS + LR)) + (b & (NS - 1));
