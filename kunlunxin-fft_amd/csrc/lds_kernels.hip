@@ -25,9 +25,10 @@
 //   0  c2c: core + norm scale in the final store (inverse = conjugated roots)
 //   1  r2c: the real input viewed as n/2 complex (x[2k] + i x[2k+1]) is the
 //      core input for free; the stitch of kernels.py:1127-1177 runs from LDS
-//      (32 elements per thread: in registers across lane pairs when the core
-//      length is a power of 32, else through the output row) and writes the
-//      n/2+1 bins with the scale
+//      (16 or 32 elements per thread and whole waves per transform: in
+//      registers across lane pairs, the remainder radix running first; 32
+//      elements and 32 lanes per transform: through the output row) and
+//      writes the n/2+1 bins with the scale
 //   2  c2r: the pre-twiddle of kernels.py:1180-1229 is applied while loading
 //      the n/2+1 bins; the inverse core writes the n real samples as n/2
 //      complex pairs with scale 2*norm_scale
@@ -50,12 +51,14 @@ struct LdsCfg {
     static constexpr int WG = T >= 256 ? T : 256;          // threads per block
     static constexpr int TPB = WG / T;                     // transforms per block
     static constexpr int P = sched_passes(LOGL, LE);       // passes
+    static constexpr bool RF = lds_remainder_first(LOGL, LE, MODE == 1);  // remainder radix first
     // Real and imaginary parts exchanged separately through a float array:
     // half the LDS, twice the barriers.  Always with 32 elements per thread;
-    // with 16 from kSplit16MinLog points, except for r2c, whose 16-element
-    // stitch reads whole complex values out of LDS (the 32-element r2c
-    // kernel stitches across lane pairs or through its output row instead).
-    static constexpr bool SPLIT = LE == 5 || (LE == 4 && LOGL >= kSplit16MinLog && MODE != 1);
+    // with 16 from kSplit16MinLog points, except for an r2c kernel without
+    // lane pairing, whose 16-element stitch reads whole complex values out
+    // of LDS (at 32 elements it stitches through its output row instead).
+    static constexpr bool SPLIT =
+        LE == 5 || (LE == 4 && LOGL >= kSplit16MinLog && (MODE != 1 || sched_logr(LOGL, LE, P - 1, RF) == LE));
     // Exchange padding: one slot per 16 elements in float2 rows and in the
     // split rows of 16-element threads (pad; a half-wave's stride-16 writes
     // then tile the 64 banks), one per 32 in the split rows of 32-element
@@ -73,16 +76,16 @@ struct LdsCfg {
     // (the 32-element registers have no room for the mirror values, and it
     // saves the 16-element kernels an LDS round trip): when whole waves make
     // up a transform and the pass next to HBM has the full radix (c2r: the
-    // first pass, always; r2c: the last, when L is a power of E), thread
+    // first pass, always; r2c: the last, as its remainder runs first), thread
     // t plays Stockham index pair_j(t), which puts the indices j and T - j
     // in lanes l and l ^ 32 of one wave.  The mirror L - k of every bin
     // k = j + T*q a thread holds is then its partner lane's element
     // E - 1 - q, one lane swap away (j = 0 and j = T/2 pair with
     // themselves).
     static constexpr bool PAIR =
-        LE >= 4 && T >= 64 && (MODE == 2 || (MODE == 1 && sched_logr(LOGL, LE, P - 1) == LE));
-    static constexpr int logr(int p) { return sched_logr(LOGL, LE, p); }
-    static constexpr int lns(int p) { return sched_lns(LE, p); }
+        LE >= 4 && T >= 64 && (MODE == 2 || (MODE == 1 && sched_logr(LOGL, LE, P - 1, RF) == LE));
+    static constexpr int logr(int p) { return sched_logr(LOGL, LE, p, RF); }
+    static constexpr int lns(int p) { return sched_lns_rf(LOGL, LE, p, RF); }
 };
 
 __device__ __forceinline__ int pad(int i) { return i + (i >> 4); }
@@ -124,7 +127,8 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
     using C = LdsCfg<LOGL, LOGE, MODE>;
     constexpr int L = C::L, E = C::E, T = C::T, P = C::P;
     constexpr bool NEED_LDS = (P > 1) || (MODE == 1);
-    static_assert(!(C::SPLIT && MODE == 1 && C::LE != 5), "16-element r2c kernels exchange whole complex values");
+    static_assert(!(C::SPLIT && MODE == 1 && C::LE != 5 && !C::PAIR),
+                  "16-element r2c kernels without lane pairing stitch whole complex values out of LDS");
     __shared__ float2 lds_raw[NEED_LDS ? (C::LDS_FLOATS + 1) / 2 : 1];
     float2* const lds = lds_raw;
     float* const ldsf = reinterpret_cast<float*>(lds_raw);
@@ -299,7 +303,7 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
         static_for<0, NB>([&](auto m) {
             if constexpr (NS > 1) {
                 const int b = j + m.value * T;
-                constexpr int TW_OFF = sched_tw_off(LOGL, C::LE, p);
+                constexpr int TW_OFF = sched_tw_off(LOGL, C::LE, p, C::RF);
                 pass_twiddle<R, DIR, m.value * R>(v, tw + TW_OFF, NS, b & (NS - 1));
             }
             dft<R, DIR, m.value * R, 1>(v);

@@ -78,16 +78,17 @@ std::vector<float2> roots(int64_t len, int64_t count, int64_t step) {
 
 // Stockham pass table of a length-2^logl transform at 2^le elements per
 // thread: pass p >= 1 (span NS, radix R) holds rows i < log2 R of
-// W_{NS*R}^(2^i * k), k < NS, at offset sched_tw_off (mfft_device.hpp).
-std::vector<float2> pass_table(int logl, int le) {
+// W_{NS*R}^(2^i * k), k < NS, at offset sched_tw_off (mfft_device.hpp);
+// rf: the remainder radix runs first.
+std::vector<float2> pass_table(int logl, int le, bool rf = false) {
     const int passes = mfft::sched_passes(logl, le);
-    const int size = mfft::sched_tw_size(logl, le);
+    const int size = mfft::sched_tw_size(logl, le, rf);
     std::vector<float2> t((size_t)(size > 0 ? size : 1), make_float2(0.0f, 0.0f));
     for (int p = 1; p < passes; ++p) {
-        const int lr = mfft::sched_logr(logl, le, p);
-        const int64_t ns = (int64_t)1 << mfft::sched_lns(le, p);
+        const int lr = mfft::sched_logr(logl, le, p, rf);
+        const int64_t ns = (int64_t)1 << mfft::sched_lns_rf(logl, le, p, rf);
         const int64_t span = ns << lr;
-        const int off = mfft::sched_tw_off(logl, le, p);
+        const int off = mfft::sched_tw_off(logl, le, p, rf);
         for (int i = 0; i < lr; ++i)
             for (int64_t k = 0; k < ns; ++k) t[(size_t)(off + i * ns + k)] = root(span, k << i);
     }
@@ -400,7 +401,8 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
         if (rc == MFFT_OK)
             rc = upload(&p->tw_hi, roots(core_n, core_n >> p->tw_h, (int64_t)1 << p->tw_h), &p->table_bytes);
     } else if (flow == MFFT_FLOW_LDS_FUSED) {
-        rc = upload(&p->tw, pass_table(logc, mfft::sched_le(logc, mfft::ilog2(elems))), &p->table_bytes);
+        const int le = mfft::sched_le(logc, mfft::ilog2(elems));
+        rc = upload(&p->tw, pass_table(logc, le, mfft::lds_remainder_first(logc, le, p->r2c_fused)), &p->table_bytes);
     } else {
         rc = upload(&p->tw, roots(core_n, core_n, 1), &p->table_bytes);
     }

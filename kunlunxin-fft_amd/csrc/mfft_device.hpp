@@ -141,22 +141,32 @@ __device__ __forceinline__ void dft(float2 (&v)[E]) {
 
 // ---- Stockham schedule shared by the host (table builder) and the kernels --
 // A transform of length 2^logl with up to 2^loge elements per thread runs P
-// passes; pass p has radix 2^logr(p) and accumulated span NS = 2^(le*p).
-// Every pass but the last has radix 2^le (the remainder goes last).
+// passes; pass p has radix 2^logr(p) and accumulated span NS = 2^lns(p), the
+// product of the radices before it.  Every pass but one has radix 2^le; the
+// remainder goes last, or first when `rf` is set (the LDS kernel's r2c mode,
+// whose stitch wants a full-radix last pass).
 constexpr int sched_le(int logl, int loge) { return loge < logl ? loge : logl; }
 constexpr int sched_passes(int logl, int le) { return logl == 0 ? 1 : (logl + le - 1) / le; }
-constexpr int sched_logr(int logl, int le, int p) {
-    return p < sched_passes(logl, le) - 1 ? le : logl - le * (sched_passes(logl, le) - 1);
+constexpr int sched_logr(int logl, int le, int p, bool rf = false) {
+    return (rf ? p > 0 : p < sched_passes(logl, le) - 1) ? le : logl - le * (sched_passes(logl, le) - 1);
 }
 constexpr int sched_lns(int le, int p) { return le * p; }
+constexpr int sched_lns_rf(int logl, int le, int p, bool rf) {
+    return rf && p > 0 ? sched_logr(logl, le, 0, true) + le * (p - 1) : le * p;
+}
 // Pass twiddle table: pass p >= 1 owns logr(p) rows of NS entries, row i
 // holding W_{NS*R}^(2^i * k) for k < NS (forward roots).  Offset of pass p:
-constexpr int sched_tw_off(int logl, int le, int p) {
+constexpr int sched_tw_off(int logl, int le, int p, bool rf = false) {
     int off = 0;
-    for (int q = 1; q < p; ++q) off += sched_logr(logl, le, q) << sched_lns(le, q);
+    for (int q = 1; q < p; ++q) off += sched_logr(logl, le, q, rf) << sched_lns_rf(logl, le, q, rf);
     return off;
 }
-constexpr int sched_tw_size(int logl, int le) { return sched_tw_off(logl, le, sched_passes(logl, le)); }
+// The LDS kernel runs the remainder first in r2c mode when whole waves make
+// up a transform (then its last pass can pair lanes for the stitch).
+constexpr bool lds_remainder_first(int logl, int le, bool r2c) { return r2c && le >= 4 && logl - le >= 6; }
+constexpr int sched_tw_size(int logl, int le, bool rf = false) {
+    return sched_tw_off(logl, le, sched_passes(logl, le), rf);
+}
 
 // highest power of two <= q (q >= 1)
 constexpr int high_bit(int q) { return q <= 1 ? 1 : 2 * high_bit(q >> 1); }

@@ -316,12 +316,13 @@ def test_c2r_mirror_pairs(gpu, elems, n, b):
 @pytest.mark.parametrize("n", [1 << k for k in range(11, 17)])
 @pytest.mark.parametrize("b", [1, 5, 11])
 def test_r2c_32_elements_stitch_through_output(gpu, n, b):
-    """R2C with 32 elements per thread (the split exchange).  A 32768-point
-    core (n = 2^16) ends in a full radix-32 pass and stitches in registers,
-    each bin's mirror coming from the partner lane; the other cores send
-    their outputs to the output row, then each thread turns disjoint mirror
-    pairs into bins in place.  Small cores put several transforms in one
-    workgroup, so ragged batches leave some of its rows inactive."""
+    """R2C with 32 elements per thread (the split exchange).  From a
+    2048-point core the remainder radix runs first, so the last pass has the
+    full radix 32 and the stitch runs in registers, each bin's mirror coming
+    from the partner lane; the 1024-point core (32 lanes per transform, two
+    transforms per wave) sends its outputs to the output row, then each
+    thread turns disjoint mirror pairs into bins in place.  Ragged batches
+    leave rows of a multi-transform block inactive."""
     rng = np.random.default_rng(6000 + n + b)
     h = rng.standard_normal((b, n)).astype(np.float32)
     p = native.NativePlan(n, b, "r2c", "forward", "ortho", native.FLOW_LDS_FUSED, (32,))
