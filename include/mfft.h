@@ -95,7 +95,9 @@ enum {
  *                                    computing and storing in lockstep
  *   FOUR_STEP:           params[0] = n1 (column FFT length; n2 = core_n/n1),
  *                        params[1] = batch rows per chunk (both passes run
- *                                    chunk by chunk; 0 = whole batch),
+ *                                    chunk by chunk, and a real transform's
+ *                                    stitch or pre-twiddle runs between the
+ *                                    chunks; 0 = whole batch),
  *                        params[2] = schedule: 0 = one column group per
  *                                    workgroup; 1 = persistent workgroups (one
  *                                    resident wave of them) that load their

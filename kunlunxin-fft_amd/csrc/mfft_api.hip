@@ -162,6 +162,12 @@ int run_core(const mfft_plan* p, const float2* src, float2* dst, int dir, float 
     return MFFT_OK;
 }
 
+// A real transform over a four-step core whose batch is split into chunks:
+// its stitch or pre-twiddle runs chunk by chunk between the core's chunks.
+bool real_chunked(const mfft_plan* p) {
+    return p->flow == MFFT_FLOW_FOUR_STEP && p->schedule != 2 && p->chunk_rows > 0 && p->chunk_rows < p->batch;
+}
+
 // One execute with the scratch `w`; ws/ws_bytes: the caller's workspace
 // (checked against in and out), or NULL for the plan's own.
 int execute_impl(const mfft_plan* p, const void* in, void* out, const Work& w, void* stream_v,
@@ -205,6 +211,21 @@ int execute_impl(const mfft_plan* p, const void* in, void* out, const Work& w, v
                                   p->num_cus, p->stagger);
             return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
         }
+        if (real_chunked(p)) {
+            // chunk by chunk: the stitch reads the core output of its chunk
+            // while that is still in the MALL
+            const int64_t cn = p->core_n;
+            for (int64_t r0 = 0; r0 < p->batch; r0 += p->chunk_rows) {
+                const int64_t rc = p->batch - r0 < p->chunk_rows ? p->batch - r0 : p->chunk_rows;
+                he = mfft::launch_fourstep(-1, (const float2*)in + r0 * cn, w.a + r0 * cn, p, rc, 1.0f, stream,
+                                           nullptr);
+                if (he == hipSuccess)
+                    he = mfft::launch_r2c_stitch(w.a + r0 * cn, (float2*)out + r0 * (cn + 1), p->tw_real, p->n, rc,
+                                                 p->scale, stream);
+                if (he != hipSuccess) return hip_fail(he, "kernel launch");
+            }
+            return MFFT_OK;
+        }
         int rc = run_core(p, (const float2*)in, w.a, -1, 1.0f, w, stream);
         if (rc != MFFT_OK) return rc;
         he = mfft::launch_r2c_stitch(w.a, (float2*)out, p->tw_real, p->n, p->batch, p->scale, stream);
@@ -215,6 +236,19 @@ int execute_impl(const mfft_plan* p, const void* in, void* out, const Work& w, v
         he = mfft::launch_lds(2, 1, logc, p->elems, in, out, p->tw, p->tw_real, p->batch, p->scale, stream,
                               p->num_cus, p->stagger);
         return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
+    }
+    if (real_chunked(p)) {
+        // chunk by chunk: pass 1 reads the pre-twiddled chunk while that is
+        // still in the MALL
+        const int64_t cn = p->core_n;
+        for (int64_t r0 = 0; r0 < p->batch; r0 += p->chunk_rows) {
+            const int64_t rc = p->batch - r0 < p->chunk_rows ? p->batch - r0 : p->chunk_rows;
+            he = mfft::launch_c2r_pre((const float2*)in + r0 * (cn + 1), w.a + r0 * cn, p->tw_real, p->n, rc, stream);
+            if (he == hipSuccess)
+                he = mfft::launch_fourstep(1, w.a + r0 * cn, (float2*)out + r0 * cn, p, rc, p->scale, stream, nullptr);
+            if (he != hipSuccess) return hip_fail(he, "kernel launch");
+        }
+        return MFFT_OK;
     }
     he = mfft::launch_c2r_pre((const float2*)in, w.a, p->tw_real, p->n, p->batch, stream);
     if (he != hipSuccess) return hip_fail(he, "kernel launch");
@@ -456,7 +490,10 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
             break;
         }
     }
-    p->launches = core_launches + (need_a ? 1 : 0);
+    // the stitch / pre-twiddle of a non-fused real flow: once, or once per
+    // chunk of a chunked four-step core
+    const int64_t real_launches = !need_a ? 0 : real_chunked(p) ? (batch + chunk - 1) / chunk : 1;
+    p->launches = core_launches + (int)real_launches;
 
     if (rc == MFFT_OK) {
         he = hipDeviceSynchronize();  // table uploads complete before the first execute
