@@ -70,8 +70,13 @@ struct LdsCfg {
     static constexpr int LDS_FLOATS = TPB * PITCH * (SPLIT ? 1 : 2);
     // Waves per SIMD the register allocation must allow.  A split-exchange
     // block uses at most 70 KB of LDS, so up to 16 waves of it fit a CU when
-    // each wave stays within 128 VGPRs.
-    static constexpr int MIN_WAVES = SPLIT ? 4 : 1;
+    // each wave stays within 128 VGPRs.  Two 16-wave blocks of the
+    // 16-element 16384-point kernel (70 KB each) fit a CU when each wave
+    // stays within 64 VGPRs: the lane-paired r2c stitch took 71 and lost
+    // the second block (measured 13% slower).  The 8192-point kernel keeps
+    // the looser bound: 64 VGPRs would make its r2c mode spill 40 bytes for
+    // a fourth block, which measured 6% slower than three.
+    static constexpr int MIN_WAVES = SPLIT ? (LE == 4 && T == 1024 ? 8 : 4) : 1;
     // Lane pairing of the real modes with 16 or 32 elements per thread
     // (the 32-element registers have no room for the mirror values, and it
     // saves the 16-element kernels an LDS round trip): when whole waves make
