@@ -6,13 +6,15 @@ per block, elements per thread, start stagger, n1, chunk rows, schedule, pass-2
 row order) from their published ranges (N <= 2^20), then checks the GPU result
 to the north-star gate (rel-L2 and peak-normalised worst element <= 1e-5).
 Sizes stay small enough (N * B <= 2^21) that the whole set runs in seconds.
+A second set drives the real LDS modes through the C ABI with an explicit
+16 or 32 elements per thread.
 """
 import numpy as np
 import pytest
 import torch
 
 import oracle
-from kunlunxin_fft_amd import ExecutionPlan, execute_fft_plan
+from kunlunxin_fft_amd import ExecutionPlan, execute_fft_plan, native
 
 pytestmark = pytest.mark.gpu
 
@@ -88,4 +90,43 @@ def test_random_configuration(gpu, case, name, tt, td, norm, n, b, block, params
     ref = _reference(h, tt, td, norm, n)
     l2 = oracle.rel_l2(y, ref)
     mx = oracle.max_rel_error(y, ref)
+    assert l2 <= TOL and mx <= TOL, f"rel_l2={l2:.3e} max_rel={mx:.3e}"
+
+
+def _real_lds_cases(count=200, seed=4242):
+    """Real LDS modes through the C ABI with an explicit 16 or 32 elements per
+    thread (the plan API maps 32 to 16 below a 32768-point core), a start
+    stagger, a norm and a ragged batch."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        tt = ("r2c", "c2r")[int(rng.integers(2))]
+        e = (16, 32)[int(rng.integers(2))]
+        logc = int(rng.integers(10, 16)) if e == 32 else int(rng.integers(6, 15))
+        n = 1 << (logc + 1)
+        b = int(rng.integers(1, min(40, max(1, (1 << 21) >> (logc + 1))) + 1))
+        norm = NORMS[int(rng.integers(4))]
+        stg = (0, 0, 1, 3)[int(rng.integers(4))]
+        out.append(pytest.param(i, tt, e, n, b, norm, stg, id=f"{i}-{tt}-e{e}-N{n}-B{b}-{norm}-s{stg}"))
+    return out
+
+
+@pytest.mark.parametrize("case,tt,elems,n,b,norm,stagger", _real_lds_cases())
+def test_random_real_lds_through_abi(gpu, case, tt, elems, n, b, norm, stagger):
+    rng = np.random.default_rng(9000 + case)
+    td = "forward" if tt == "r2c" else "inverse"
+    p = native.NativePlan(n, b, tt, td, norm, native.FLOW_LDS_FUSED, (elems, stagger))
+    if tt == "r2c":
+        h = rng.standard_normal((b, n)).astype(np.float32)
+        y = torch.full((b, n // 2 + 1), float("nan"), dtype=torch.complex64, device=gpu)
+    else:
+        m = n // 2 + 1
+        h = (rng.standard_normal((b, m)) + 1j * rng.standard_normal((b, m))).astype(np.complex64)
+        y = torch.full((b, n), float("nan"), dtype=torch.float32, device=gpu)
+    x = torch.from_numpy(h).to(gpu)
+    p.execute(x.data_ptr(), y.data_ptr(), torch.cuda.current_stream(gpu).cuda_stream)
+    ref = _reference(h, tt, td, norm, n)
+    got = y.cpu().numpy()
+    l2 = oracle.rel_l2(got, ref)
+    mx = oracle.max_rel_error(got, ref)
     assert l2 <= TOL and mx <= TOL, f"rel_l2={l2:.3e} max_rel={mx:.3e}"
