@@ -70,13 +70,11 @@ struct LdsCfg {
     static constexpr int LDS_FLOATS = TPB * PITCH * (SPLIT ? 1 : 2);
     // Waves per SIMD the register allocation must allow.  A split-exchange
     // block uses at most 70 KB of LDS, so up to 16 waves of it fit a CU when
-    // each wave stays within 128 VGPRs.  Two 16-wave blocks of the
-    // 16-element 16384-point kernel (70 KB each) fit a CU when each wave
-    // stays within 64 VGPRs: the lane-paired r2c stitch took 71 and lost
-    // the second block (measured 13% slower).  The 8192-point kernel keeps
-    // the looser bound: 64 VGPRs would make its r2c mode spill 40 bytes for
-    // a fourth block, which measured 6% slower than three.
-    static constexpr int MIN_WAVES = SPLIT ? (LE == 4 && T == 1024 ? 8 : 4) : 1;
+    // each wave stays within 128 VGPRs.  The 16-element split blocks (two
+    // 16-wave blocks of 16384 points, four 8-wave blocks of 8192) fill a CU
+    // when each wave stays within 64 VGPRs: the lane-paired r2c stitch took
+    // 71-73 and lost a block per CU (N = 2^15 measured 13% slower).
+    static constexpr int MIN_WAVES = SPLIT ? (LE == 4 ? 8 : 4) : 1;
     // Lane pairing of the real modes with 16 or 32 elements per thread
     // (the 32-element registers have no room for the mirror values, and it
     // saves the 16-element kernels an LDS round trip): when whole waves make
@@ -364,21 +362,23 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
         static_assert(C::logr(P - 1) == C::LE, "lane pairing needs a full radix last pass");
         float2* xo = (float2*)dst_v + row * (L + 1);
         const bool jz = j == 0, jh = j == T / 2;
-        const float2 tj = tw_real[j];  // tw_real[j + T*s] = tj * exp(-2 pi i s / 2E)
-        static_for<0, E / 2>([&](auto ss) {
-            constexpr int s = ss.value;
-            constexpr int sb = E - 1 - s;
-            const float2 a = v[s], b = v[sb];
-            const float2 pa = swap_halves(b), pb = swap_halves(a);
-            const float2 ma = jz ? v[(E - s) % E] : (jh ? b : pa);
-            const float2 mb = jz ? v[s + 1] : (jh ? a : pb);
-            if (active) {
+        // A transform spans whole waves, so `active` is wave-uniform and the
+        // lane swaps run with every lane of the wave or none.
+        if (active) {
+            const float2 tj = tw_real[j];  // tw_real[j + T*s] = tj * exp(-2 pi i s / 2E)
+            static_for<0, E / 2>([&](auto ss) {
+                constexpr int s = ss.value;
+                constexpr int sb = E - 1 - s;
+                const float2 a = v[s], b = v[sb];
+                const float2 pa = swap_halves(b), pb = swap_halves(a);
+                const float2 ma = jz ? v[(E - s) % E] : (jh ? b : pa);
+                const float2 mb = jz ? v[s + 1] : (jh ? a : pb);
                 xo[j + s * T] = r2c_bin(a, ma, rot<2 * E, s, -1>(tj), scale, s == 0 && jz);
                 xo[j + sb * T] = r2c_bin(b, mb, rot<2 * E, sb, -1>(tj), scale, false);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        });
-        if (active && jz) xo[L] = r2c_bin(v[0], v[0], tw_real[L], scale, true);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+            if (jz) xo[L] = r2c_bin(v[0], v[0], tw_real[L], scale, true);
+        }
     } else if constexpr (MODE == 1 && C::SPLIT) {
         // r2c with 32 elements per thread and no lane pairing (the last
         // pass has a smaller radix, or 32 lanes hold a transform): the split
