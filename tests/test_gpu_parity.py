@@ -331,7 +331,8 @@ def test_r2c_c2r_match_oracle(gpu, name, n, norm):
 @pytest.mark.parametrize("b", [1, 3, 37])
 def test_c2r_mirror_pairs(gpu, elems, n, b):
     """Fused C2R: each bin is loaded once and meets its mirror bin n/2 - k
-    through LDS (up to 16 elements per thread; 32: from the partner lane), bin 0
+    from the partner lane (16 or 32 elements per thread and whole waves per
+    transform) or through LDS (the other forms), bin 0
     pairs with bin n/2, and the DC/Nyquist imaginary parts are ignored.
     Ragged batches leave rows of a multi-transform block inactive."""
     if elems < 16 and n > 8192:
