@@ -11,10 +11,13 @@ HBM before the timed region.  ``value`` = algorithmic bytes of all K steps
 (16*N*B per transform) / timed wall time, in GB/s.
 
 Also reported (on the same JSON line):
-* ``roofline``: the dominant kernel (largest share of a step), its algorithmic
-  bytes per launch over its mean launch duration (HIP events on the stream the
-  kernel runs on), against 8 TB/s; ``traffic`` from the committed rocprofv3
-  PMC summary (profiles/pmc_traffic.json) when present, else null;
+* ``roofline``: the dominant flow (the size whose launches take the largest
+  share of a step): the transforms' algorithmic bytes (16 N per row) over the
+  sum of the durations of all launches of one execute (both four-step passes
+  of every chunk together; HIP events on the stream the kernels run on),
+  against 8 TB/s; ``traffic`` = the HBM bytes of the same launches from the
+  committed rocprofv3 PMC summary (profiles/pmc_traffic.json) when present,
+  else null, and its ratio to the algorithmic bytes;
 * ``per_size``: GB/s, fraction of peak and GFLOP/s (5 N log2 N per transform)
   per N, from HIP events;
 * ``latency_n2048_b1``: the reference protocol (warmup 5, 5 x 32 trials,
@@ -30,6 +33,9 @@ Also reported (on the same JSON line):
   counting 4N + 8(N/2+1) bytes per row;
 * ``per_size[].vendor_*``: torch.fft.fft (rocFFT) on the same inputs, a
   comparison column only;
+* ``config5``: the selector sweep (N = 16 .. 2^14, B in {1, 16, 64, 256}):
+  per cell the selected plan's and the M0 incumbent's time per execute and
+  whether the selected plan clears the 2% promotion guard in this run;
 * ``cpu_baseline``: the reference's own CPU FFT (butterfly::fft_dit built
   into oracle/_ref; the C restatement when that build is absent) on one core,
   on a bounded sample -- 16 transforms of each N = 2^10..2^20 -- median of 5,
@@ -73,6 +79,7 @@ def main() -> int:
     ap.add_argument("--no-vendor", action="store_true", help="skip the torch.fft (rocFFT) comparison column")
     ap.add_argument("--sizes", default="", help="comma-separated subset of N (profiling runs)")
     ap.add_argument("--no-real", action="store_true", help="skip the R2C / C2R throughput leg")
+    ap.add_argument("--no-config5", action="store_true", help="skip the config-5 selector-vs-M0 sweep")
     ap.add_argument("--detail-out", default="", help="also write the JSON line, indented, to this file")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -88,7 +95,7 @@ def main() -> int:
     import __graft_entry__
 
     pkg = __graft_entry__.load_package()
-    from kunlunxin_fft_amd import native
+    from kunlunxin_fft_amd import runner
     from kunlunxin_fft_amd.entry import _resolve
 
     if not torch.cuda.is_available():
@@ -163,20 +170,24 @@ def main() -> int:
     # reads 8.3 TB/s, above the HBM peak).  In the cycle, every size starts
     # after the others' traffic, as in the timed steps.
     per_size = []
-    kernels = {}  # (kernel, flow, n, rows per launch) -> [launch ms, ...] within one execute
     stream = torch.cuda.current_stream(dev)
     natives = []
     for n, b, x, plan in work:
         nplan, (shape, dt) = _resolve(plan, 0)
-        natives.append((nplan, torch.empty(shape, dtype=dt, device=dev)))
+        natives.append((nplan, torch.empty(shape, dtype=dt, device=dev), runner.workspace_for(nplan, dev)))
+
+    def run_native(nplan, x, out, ws):
+        nplan.execute_ws(x.data_ptr(), out.data_ptr(), ws.data_ptr() if ws is not None else 0,
+                         nplan.ws_bytes, stream.cuda_stream)
+
     evs = [[] for _ in work]
     for _ in range(10):
         for i, (n, b, x, plan) in enumerate(work):
-            nplan, out = natives[i]
+            nplan, out, ws = natives[i]
             s = torch.cuda.Event(enable_timing=True)
             e = torch.cuda.Event(enable_timing=True)
             s.record(stream)
-            nplan.execute(x.data_ptr(), out.data_ptr(), stream.cuda_stream)
+            run_native(nplan, x, out, ws)
             e.record(stream)
             evs[i].append((s, e))
     torch.cuda.synchronize()
@@ -186,25 +197,29 @@ def main() -> int:
     launch_runs = [[] for _ in work]
     for _ in range(5):
         for i, (n, b, x, plan) in enumerate(work):
-            pn, pout = natives[i - 1]
-            px = work[i - 1][2]
-            pn.execute(px.data_ptr(), pout.data_ptr(), stream.cuda_stream)
-            nplan, out = natives[i]
-            launch_runs[i].append(nplan.execute_timed(x.data_ptr(), out.data_ptr(), stream.cuda_stream))
+            pn, pout, pws = natives[i - 1]
+            run_native(pn, work[i - 1][2], pout, pws)
+            nplan, out, ws = natives[i]
+            launch_runs[i].append(nplan.execute_timed(x.data_ptr(), out.data_ptr(), stream.cuda_stream,
+                                                      ws_ptr=ws.data_ptr() if ws is not None else 0,
+                                                      ws_bytes=nplan.ws_bytes))
+    flows = []  # per size: (launch names, per-launch ms) of one execute
     for i, (n, b, x, plan) in enumerate(work):
-        nplan, out = natives[i]
+        nplan, out, _ = natives[i]
         ms = statistics.median(s.elapsed_time(e) for s, e in evs[i])
         per_launch = [statistics.median(col) for col in zip(*launch_runs[i])]
         flow = nplan.flow_name
         rows = int(nplan.info.chunk_rows) or b
+        names = []
         for j, t in enumerate(per_launch):
             if flow == "four-step":
-                kname = f"fourstep_pass_kernel pass {j % 2 + 1} (n{'12'[j % 2]}={nplan.info.n1 if j % 2 == 0 else nplan.info.n2})"
+                names.append(f"fourstep_pass_kernel pass {j % 2 + 1} "
+                             f"(n{'12'[j % 2]}={nplan.info.n1 if j % 2 == 0 else nplan.info.n2})")
             elif flow == "lds-fused":
-                kname = "lds_fft_kernel"
+                names.append("lds_fft_kernel")
             else:
-                kname = f"{flow} stage {j + 1}"
-            kernels.setdefault((kname, flow, n, b, rows), []).append(t)
+                names.append(f"{flow} stage {j + 1}")
+        flows.append((names, per_launch, rows))
         gbps = 16 * n * b / (ms * 1e-3) / 1e9
         per_size.append({
             "n": n, "batch": b, "executed": plan.executed, "flow": flow,
@@ -217,25 +232,34 @@ def main() -> int:
         log(f"N={n:>8} B={b:>6} {flow:>10} {ms:8.4f} ms {gbps:8.1f} GB/s "
             f"({gbps / PEAK_GBPS:.1%}) launches={['%.4f' % t for t in per_launch]}")
 
-    # ---- dominant kernel: the (kernel, size) with the largest total time per step
-    (kname, dflow, dn, db, drows), dts = max(kernels.items(), key=lambda kv: sum(kv[1]))
-    dms = sum(dts) / len(dts)
-    d_bytes = 16 * dn * drows  # each launch reads and writes every element of its rows once
-    d_ach = d_bytes / (dms * 1e-3) / 1e9
+    # ---- dominant kernel: the size whose launches take the most time per step.
+    # A flow of several launches (the four-step's two passes, per chunk) is
+    # one unit: the transforms' algorithmic bytes (16 N per row, read once and
+    # written once) over the sum of all launch durations of one execute.
+    di = max(range(len(work)), key=lambda i: sum(flows[i][1]))
+    dn, db = work[di][0], work[di][1]
+    dnames, dts, drows = flows[di]
+    dflow = natives[di][0].flow_name
+    d_bytes = 16 * dn * db
+    d_ms = sum(dts)
+    d_ach = d_bytes / (d_ms * 1e-3) / 1e9
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "pmc_traffic.json")
-    key = f"{kname}|N={dn}|rows={drows}"
     if os.path.exists(tpath):
         try:
-            traffic = json.load(open(tpath)).get(key)
-        except (OSError, ValueError):
+            tmap = json.load(open(tpath))
+            parts = [tmap.get(f"{nm}|N={dn}|rows={drows}") for nm in dnames]
+            traffic = sum(parts) if all(v is not None for v in parts) else None
+        except (OSError, ValueError, TypeError):
             traffic = None
+    kinds = sorted(set(dnames), key=dnames.index)
     roofline = {"bound": "hbm", "achieved": round(d_ach, 1), "peak": PEAK_GBPS, "unit": "GB/s",
                 "frac": round(d_ach / PEAK_GBPS, 4), "traffic": traffic,
-                "kernel": f"{kname} [{dflow}, N={dn}, B={db}, {drows} rows per launch, "
-                          f"{len(dts)} launches per execute]",
-                "algorithmic_bytes_per_launch": d_bytes, "mean_launch_ms": round(dms, 5),
-                "share_of_step": round(sum(dts) / ms_per_step, 3)}
+                "traffic_over_algorithmic": round(traffic / d_bytes, 3) if traffic else None,
+                "kernel": f"{' + '.join(kinds)} [{dflow}, N={dn}, B={db}, {drows} rows per launch, "
+                          f"{len(dts)} launches per execute, counted together]",
+                "algorithmic_bytes_per_execute": d_bytes, "launch_ms": [round(t, 5) for t in dts],
+                "sum_launch_ms": round(d_ms, 5), "share_of_step": round(d_ms / ms_per_step, 3)}
     log(f"dominant kernel: {roofline}")
 
     # ---- latency at N=2048 B=1 (reference protocol) and config 2
@@ -263,12 +287,13 @@ def main() -> int:
                 wall.append((time.perf_counter() - a) * 1e3)
         nplan, (shape, dt) = _resolve(plan, 0)
         out = torch.empty(shape, dtype=dt, device=dev)
+        ws = runner.workspace_for(nplan, dev)
         evs = []
         for _ in range(100):
             s = torch.cuda.Event(enable_timing=True)
             e = torch.cuda.Event(enable_timing=True)
             s.record(stream)
-            nplan.execute(x.data_ptr(), out.data_ptr(), stream.cuda_stream)
+            run_native(nplan, x, out, ws)
             e.record(stream)
             evs.append((s, e))
         torch.cuda.synchronize()
@@ -340,20 +365,21 @@ def main() -> int:
             for tt, td, x in (("r2c", "forward", xr), ("c2r", "inverse", xc)):
                 plan = pkg.plan_fft("dit", n, batch=b, profile_hash=prof, transform_type=tt, transform_direction=td)
                 nplan, (shape, dt) = _resolve(plan, 0)
-                rwork.append((n, b, tt, x, plan, nplan, torch.empty(shape, dtype=dt, device=dev)))
-        for _, _, _, x, _, nplan, out in rwork:
-            nplan.execute(x.data_ptr(), out.data_ptr(), stream.cuda_stream)
+                rwork.append((n, b, tt, x, plan, nplan, torch.empty(shape, dtype=dt, device=dev),
+                              runner.workspace_for(nplan, dev)))
+        for _, _, _, x, _, nplan, out, ws in rwork:
+            run_native(nplan, x, out, ws)
         revs = [[] for _ in rwork]
         for _ in range(5):
-            for i, (_, _, _, x, _, nplan, out) in enumerate(rwork):
+            for i, (_, _, _, x, _, nplan, out, ws) in enumerate(rwork):
                 s = torch.cuda.Event(enable_timing=True)
                 e = torch.cuda.Event(enable_timing=True)
                 s.record(stream)
-                nplan.execute(x.data_ptr(), out.data_ptr(), stream.cuda_stream)
+                run_native(nplan, x, out, ws)
                 e.record(stream)
                 revs[i].append((s, e))
         torch.cuda.synchronize()
-        for i, (n, b, tt, _, plan, nplan, _) in enumerate(rwork):
+        for i, (n, b, tt, _, plan, nplan, _, _) in enumerate(rwork):
             ms = statistics.median(s.elapsed_time(e) for s, e in revs[i])
             gbps = b * (4 * n + 8 * (n // 2 + 1)) / (ms * 1e-3) / 1e9
             real_rows.append({"n": n, "batch": b, "transform": tt, "executed": plan.executed,
@@ -385,6 +411,52 @@ def main() -> int:
             log(f"N={n:>8} B={b:>6} torch.fft (rocFFT) {vms:8.4f} ms {row['vendor_gbps']:8.1f} GB/s "
                 f"(this library {row['ms']:.4f} ms)")
 
+    # ---- config 5: the selector sweep, N = 16 .. 2^14 x B in {1, 16, 64, 256},
+    # forward C2C.  Per cell: the selected plan and the M0 incumbent (fft_dit /
+    # fft_dit_batch), each timed as the table builder times a cell (back-to-back
+    # executes between HIP events, median of rounds), and whether the selected
+    # plan still clears the reference's 2% promotion guard
+    # (src/xpu/selector.py:59-63) in this run.
+    cfg5 = []
+    if not args.no_config5:
+        from kunlunxin_fft_amd.selector import GUARD_PCT as guard
+
+        def cell_ms(plan, x, reps=20, rounds=5):
+            nplan, (shape, dt) = _resolve(plan, 0)
+            out = torch.empty(shape, dtype=dt, device=dev)
+            ws = runner.workspace_for(nplan, dev)
+            for _ in range(3):
+                run_native(nplan, x, out, ws)
+            res = []
+            for _ in range(rounds):
+                s = torch.cuda.Event(enable_timing=True)
+                e = torch.cuda.Event(enable_timing=True)
+                s.record(stream)
+                for _ in range(reps):
+                    run_native(nplan, x, out, ws)
+                e.record(stream)
+                e.synchronize()
+                res.append(s.elapsed_time(e) / reps)
+            return statistics.median(res), nplan.flow_name
+
+        for n in [1 << k for k in range(4, 15)]:
+            for b in (1, 16, 64, 256):
+                x = torch.randn((n,) if b == 1 else (b, n), dtype=torch.complex64, device=dev, generator=gen)
+                sel = pkg.plan_fft("dit", n, batch=b, profile_hash=prof)
+                m0 = pkg.plan_fft("dit", n, batch=b)  # no profile: the M0 closure
+                sel_ms, sel_flow = cell_ms(sel, x)
+                m0_ms, _ = cell_ms(m0, x)
+                row = {"n": n, "batch": b, "selected": sel.executed, "selected_flow": sel_flow,
+                       "selection_source": sel.selection_source, "selected_us": round(sel_ms * 1e3, 2),
+                       "m0": m0.executed, "m0_us": round(m0_ms * 1e3, 2),
+                       "speedup_vs_m0": round(m0_ms / sel_ms, 2),
+                       "guard_pct": guard, "clears_guard": bool(sel_ms <= m0_ms * (1 - guard / 100.0))}
+                cfg5.append(row)
+                log(f"config5 N={n:>6} B={b:>4} {sel.executed:>22} {row['selected_us']:8.2f} us "
+                    f"M0 {row['m0_us']:8.2f} us  x{row['speedup_vs_m0']:.2f} guard={'ok' if row['clears_guard'] else 'NO'}")
+                del x
+        torch.cuda.synchronize()
+
     # ---- CPU baseline (reference CPU path, 1 core, bounded sample)
     cpu = None
     if not args.no_cpu:
@@ -404,7 +476,20 @@ def main() -> int:
             kinds.add(kind_mt)
             tot_mt += s_mt
             tot_bytes += 16 * n * rows
+        model = "unknown"
+        try:
+            for ln in open("/proc/cpuinfo"):
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+        try:
+            usable = len(os.sched_getaffinity(0))
+        except (AttributeError, OSError):
+            usable = os.cpu_count() or 1
         cpu = {"value": round(tot_bytes / tot_s / 1e9, 4), "unit": "GB/s", "cores": 1,
+               "cpu_model": model, "host_cpus": os.cpu_count(), "usable_cpus": usable,
                "kind": "reference" if kinds == {"reference"} else "port",
                "sample": f"{rows} transforms of each N = 2^10..2^20 (complex<double>, butterfly::fft_dit "
                          f"with its per-stage twiddle rebuild), median of 5 passes, {tot_s:.1f} s per pass",
@@ -432,6 +517,7 @@ def main() -> int:
         "config2": cfg2,
         "config3": cfg3,
         "config4": cfg4,
+        "config5": cfg5,
         "per_size": per_size,
         "real_per_size": real_rows,
     }

@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define MFFT_ABI_VERSION 1
+#define MFFT_ABI_VERSION 2
 
 /* return codes (0 = success); the Python layer maps them to exceptions */
 enum {
@@ -190,16 +190,22 @@ int mfft_plan_workspace_size(const mfft_plan* plan, int64_t* bytes);
 int mfft_execute_ws(const mfft_plan* plan, const void* in, void* out, void* workspace,
                     int64_t workspace_bytes, void* stream);
 
-/* mfft_execute with a HIP event recorded on `stream` before the first and
- * after every kernel launch (the profiling counterpart of the reference's
- * phase ledger, src/xpu/ledger.py:262-296).  Waits for the stream, then
- * writes the duration of each launch in milliseconds to launch_ms[0..k) with
+/* mfft_execute (workspace NULL) or mfft_execute_ws (workspace given) with a
+ * HIP event recorded on `stream` before the first and after every kernel
+ * launch (the profiling counterpart of the reference's phase ledger,
+ * src/xpu/ledger.py:262-296).  Waits for the stream, then writes the
+ * duration of each launch in milliseconds to launch_ms[0..k) with
  * k = min(launches, cap) and stores k in *n_launches.  Same work and results
- * as mfft_execute; creates and destroys its events (no device memory). */
-int mfft_execute_timed(const mfft_plan* plan, const void* in, void* out, void* stream,
-                       float* launch_ms, int cap, int* n_launches);
+ * as the untimed call; creates and destroys its events (no device memory). */
+int mfft_execute_timed(const mfft_plan* plan, const void* in, void* out, void* workspace,
+                       int64_t workspace_bytes, void* stream, float* launch_ms, int cap, int* n_launches);
 
-/* Release the plan's device memory (synchronises its device first). NULL is a no-op. */
+/* Release the plan's device memory.  NULL is a no-op.  It does not
+ * synchronise the device: the caller makes sure that no execute of the plan
+ * is still pending on any stream (synchronise the streams it ran on, or the
+ * device), as for freeing any memory a pending kernel reads.  Plan creation
+ * likewise waits only for its own uploads (a private stream of the device),
+ * never for other streams' work. */
 int mfft_plan_destroy(mfft_plan* plan);
 
 /* Describe a plan (resolved flow, launch count, memory held). */

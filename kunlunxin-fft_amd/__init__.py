@@ -20,7 +20,6 @@ from .config import (  # noqa: F401
     ConfigError,
     DesignSpace,
     DeviceProfile,
-    SizeMatrix,
     NORMALIZATIONS,
     TRANSFORM_DIRECTIONS,
     TRANSFORM_TYPES,
@@ -71,7 +70,7 @@ _TORCH_ATTRS = {
 }
 
 __all__ = [
-    "ConfigError", "DesignSpace", "DeviceProfile", "SizeMatrix", "ExecutionPlan",
+    "ConfigError", "DesignSpace", "DeviceProfile", "ExecutionPlan",
     "ExecutionReport", "Selection", "SUPPORTED_NORMS", "SUPPORTED_TRANSFORMS",
     "SUPPORTED_TRANSFORM_DIRECTIONS", "composition_select", "execute_fft_plan",
     "load_composition_table", "load_table", "norm_scale", "plan_fft", "run_fft", "select",

@@ -160,19 +160,3 @@ class DesignSpace:
             batch_candidates=tuple(b["candidates"]), batch_variants=tuple(variants),
             layout_in=lay["in"][0], layout_out=lay["out"][0],
         )
-
-
-@dataclass(frozen=True)
-class SizeMatrix:
-    """Length lists of the correctness and benchmark matrices (config/sizes.json)."""
-
-    correctness_sizes: tuple
-    bench_sizes: tuple
-    batches: tuple
-
-    @staticmethod
-    def load() -> "SizeMatrix":
-        d = _read_json("sizes.json")
-        for key in ("correctness_sizes", "bench_sizes", "batches"):
-            _require(_pow2_list(d.get(key)), f"sizes.json: {key} must be a non-empty list of powers of two")
-        return SizeMatrix(tuple(d["correctness_sizes"]), tuple(d["bench_sizes"]), tuple(d["batches"]))

@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -95,13 +96,38 @@ std::vector<float2> pass_table(int logl, int le, bool rf = false) {
     return t;
 }
 
-int upload(float2** dptr, const std::vector<float2>& h, int64_t* bytes) {
+// Plan uploads go through one private non-blocking stream per device, and
+// plan creation waits for that stream alone: a plan created while other
+// streams run kernels neither waits for them nor stalls them (a plain
+// hipMemcpy would run on the legacy default stream and wait for every
+// blocking stream's work).
+constexpr int kMaxDevices = 64;
+std::mutex g_upload_mu;
+hipStream_t g_upload[kMaxDevices] = {};
+
+int upload_stream(int dev, hipStream_t* out) {
+    if (dev < 0 || dev >= kMaxDevices) return fail(MFFT_ERR_RUNTIME, "device %d beyond %d devices", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lk(g_upload_mu);
+    if (!g_upload[dev]) {
+        hipError_t e = hipStreamCreateWithFlags(&g_upload[dev], hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            g_upload[dev] = nullptr;
+            return hip_fail(e, "hipStreamCreateWithFlags(upload stream)");
+        }
+    }
+    *out = g_upload[dev];
+    return MFFT_OK;
+}
+
+// Allocates a device copy of `h` and enqueues the copy on `us`; the caller
+// waits for `us` before the plan is handed out (`h` must live until then).
+int upload(float2** dptr, const std::vector<float2>& h, int64_t* bytes, hipStream_t us) {
     const size_t nb = h.size() * sizeof(float2);
     hipError_t e = hipMalloc((void**)dptr, nb > 0 ? nb : sizeof(float2));
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(twiddle table)");
     if (nb) {
-        e = hipMemcpy(*dptr, h.data(), nb, hipMemcpyHostToDevice);
-        if (e != hipSuccess) return hip_fail(e, "hipMemcpy(twiddle table)");
+        e = hipMemcpyAsync(*dptr, h.data(), nb, hipMemcpyHostToDevice, us);
+        if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(twiddle table)");
     }
     *bytes += (int64_t)nb;
     return MFFT_OK;
@@ -423,26 +449,32 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
     const double sc = norm_scale(n, transform_direction, norm) * (transform_type == MFFT_C2R ? 2.0 : 1.0);
     p->scale = (float)sc;
 
-    int rc = MFFT_OK;
-    // ---- twiddle tables
-    if (flow == MFFT_FLOW_FOUR_STEP) {
+    hipStream_t us = nullptr;
+    int rc = upload_stream(dev, &us);
+    // ---- twiddle tables (host copies live until the upload stream is drained)
+    std::vector<std::vector<float2>> host;
+    auto put = [&](float2** d, std::vector<float2>&& h) {
+        host.push_back(std::move(h));
+        return upload(d, host.back(), &p->table_bytes, us);
+    };
+    host.reserve(5);
+    if (rc == MFFT_OK && flow == MFFT_FLOW_FOUR_STEP) {
         const int lc = logc;
         const int l1 = mfft::ilog2((int)n1), l2 = mfft::ilog2((int)n2);
         p->tw_h = (lc + 1) / 2;
-        if (rc == MFFT_OK) rc = upload(&p->tw_n1, pass_table(l1, mfft::fourstep_col_loge(l1)), &p->table_bytes);
-        if (rc == MFFT_OK) rc = upload(&p->tw_n2, pass_table(l2, mfft::fourstep_col_loge(l2)), &p->table_bytes);
-        if (rc == MFFT_OK) rc = upload(&p->tw_lo, roots(core_n, (int64_t)1 << p->tw_h, 1), &p->table_bytes);
-        if (rc == MFFT_OK)
-            rc = upload(&p->tw_hi, roots(core_n, core_n >> p->tw_h, (int64_t)1 << p->tw_h), &p->table_bytes);
-    } else if (flow == MFFT_FLOW_LDS_FUSED) {
+        if (rc == MFFT_OK) rc = put(&p->tw_n1, pass_table(l1, mfft::fourstep_col_loge(l1)));
+        if (rc == MFFT_OK) rc = put(&p->tw_n2, pass_table(l2, mfft::fourstep_col_loge(l2)));
+        if (rc == MFFT_OK) rc = put(&p->tw_lo, roots(core_n, (int64_t)1 << p->tw_h, 1));
+        if (rc == MFFT_OK) rc = put(&p->tw_hi, roots(core_n, core_n >> p->tw_h, (int64_t)1 << p->tw_h));
+    } else if (rc == MFFT_OK && flow == MFFT_FLOW_LDS_FUSED) {
         const int le = mfft::sched_le(logc, mfft::ilog2(elems));
-        rc = upload(&p->tw, pass_table(logc, le, mfft::lds_remainder_first(logc, le, p->r2c_fused)), &p->table_bytes);
-    } else {
-        rc = upload(&p->tw, roots(core_n, core_n, 1), &p->table_bytes);
+        rc = put(&p->tw, pass_table(logc, le, mfft::lds_remainder_first(logc, le, p->r2c_fused)));
+    } else if (rc == MFFT_OK) {
+        rc = put(&p->tw, roots(core_n, core_n, 1));
     }
     if (rc == MFFT_OK && real) {
         // exp(-2*pi*i*k/n), k in [0, n/2]  (runner.py:1650-1658 range)
-        rc = upload(&p->tw_real, roots(n, n / 2 + 1, 1), &p->table_bytes);
+        rc = put(&p->tw_real, roots(n, n / 2 + 1, 1));
     }
 
     // ---- workspace
@@ -470,7 +502,7 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
         const int64_t rows = chunk > 0 && chunk < batch ? chunk : batch;
         const size_t sb = (size_t)(9 + rows) * sizeof(int);
         he = hipMalloc((void**)&p->sync, sb);
-        if (he == hipSuccess) he = hipMemset(p->sync, 0, sb);
+        if (he == hipSuccess) he = hipMemsetAsync(p->sync, 0, sb, us);
         if (he != hipSuccess) rc = hip_fail(he, "hipMalloc(four-step counters)");
         else p->ws_bytes += (int64_t)sb;
     }
@@ -495,9 +527,11 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
     const int64_t real_launches = !need_a ? 0 : real_chunked(p) ? (batch + chunk - 1) / chunk : 1;
     p->launches = core_launches + (int)real_launches;
 
-    if (rc == MFFT_OK) {
-        he = hipDeviceSynchronize();  // table uploads complete before the first execute
-        if (he != hipSuccess) rc = hip_fail(he, "hipDeviceSynchronize");
+    // the uploads are complete before the plan is handed out (and before the
+    // host copies go); an error return still drains the stream first
+    if (us) {
+        he = hipStreamSynchronize(us);
+        if (he != hipSuccess && rc == MFFT_OK) rc = hip_fail(he, "hipStreamSynchronize(upload stream)");
     }
     if (rc != MFFT_OK) {
         release(p);
@@ -545,8 +579,8 @@ int mfft_execute_ws(const mfft_plan* p, const void* in, void* out, void* workspa
                         stream_v, workspace, p->work_bytes);
 }
 
-int mfft_execute_timed(const mfft_plan* p, const void* in, void* out, void* stream_v,
-                       float* launch_ms, int cap, int* n_launches) {
+int mfft_execute_timed(const mfft_plan* p, const void* in, void* out, void* workspace, int64_t workspace_bytes,
+                       void* stream_v, float* launch_ms, int cap, int* n_launches) {
     g_err.clear();
     if (!launch_ms || !n_launches || cap < 1 || cap > 4096)
         return fail(MFFT_ERR_VALUE, "launch_ms/n_launches must be valid and 1 <= cap <= 4096");
@@ -569,7 +603,8 @@ int mfft_execute_timed(const mfft_plan* p, const void* in, void* out, void* stre
     }
     if (rc == MFFT_OK) {
         mfft::g_timer = &timer;
-        rc = mfft_execute(p, in, out, stream_v);
+        rc = workspace ? mfft_execute_ws(p, in, out, workspace, workspace_bytes, stream_v)
+                       : mfft_execute(p, in, out, stream_v);
         mfft::g_timer = nullptr;
     }
     if (rc == MFFT_OK && timer.count > 0) {
@@ -591,14 +626,15 @@ int mfft_execute_timed(const mfft_plan* p, const void* in, void* out, void* stre
 int mfft_plan_destroy(mfft_plan* p) {
     g_err.clear();
     if (!p) return MFFT_OK;
+    // no synchronisation here: the caller has made sure no execute of the
+    // plan is still pending on any stream (include/mfft.h)
     int cur = -1;
     (void)hipGetDevice(&cur);
     if (cur != p->device) (void)hipSetDevice(p->device);
-    hipError_t e = hipDeviceSynchronize();
     release(p);
     if (cur >= 0 && cur != p->device) (void)hipSetDevice(cur);
     delete p;
-    return e == hipSuccess ? MFFT_OK : hip_fail(e, "hipDeviceSynchronize");
+    return MFFT_OK;
 }
 
 int mfft_plan_query(const mfft_plan* p, mfft_plan_info* info) {

@@ -103,7 +103,7 @@ def load() -> ctypes.CDLL:
         lib.mfft_plan_workspace_size.restype = i32
         lib.mfft_execute_ws.argtypes = [vp, vp, vp, vp, i64, vp]
         lib.mfft_execute_ws.restype = i32
-        lib.mfft_execute_timed.argtypes = [vp, vp, vp, vp, ctypes.POINTER(ctypes.c_float), i32,
+        lib.mfft_execute_timed.argtypes = [vp, vp, vp, vp, i64, vp, ctypes.POINTER(ctypes.c_float), i32,
                                            ctypes.POINTER(i32)]
         lib.mfft_execute_timed.restype = i32
         lib.mfft_plan_destroy.argtypes = [vp]
@@ -139,7 +139,7 @@ def check(rc: int) -> None:
 class NativePlan:
     """Owner of one ``mfft_plan*``; destroyed with the object."""
 
-    __slots__ = ("_h", "info", "__weakref__")
+    __slots__ = ("_h", "info", "ws_bytes", "__weakref__")
 
     def __init__(self, n: int, batch: int, transform_type: str = "c2c",
                  transform_direction: str = "forward", norm: str = "backward",
@@ -164,6 +164,7 @@ class NativePlan:
         info = PlanInfo()
         check(lib.mfft_plan_query(self._h, ctypes.byref(info)))
         self.info = info
+        self.ws_bytes = self.workspace_size()
 
     def execute(self, in_ptr: int, out_ptr: int, stream_ptr: int) -> None:
         # plain ints convert through the c_void_p argtypes
@@ -182,12 +183,15 @@ class NativePlan:
         of at least workspace_size() bytes) instead of the plan's own."""
         check(_lib.mfft_execute_ws(self._h, in_ptr, out_ptr, ws_ptr, int(ws_bytes), stream_ptr))
 
-    def execute_timed(self, in_ptr: int, out_ptr: int, stream_ptr: int, cap: int = 64) -> list:
-        """Execute once and return each kernel launch's duration in ms (HIP
-        events on the same stream; waits for the stream)."""
+    def execute_timed(self, in_ptr: int, out_ptr: int, stream_ptr: int, cap: int = 64,
+                      ws_ptr: int = 0, ws_bytes: int = 0) -> list:
+        """Execute once (with the caller's workspace when ws_ptr is given) and
+        return each kernel launch's duration in ms (HIP events on the same
+        stream; waits for the stream)."""
         ms = (ctypes.c_float * cap)()
         k = ctypes.c_int(0)
         check(_lib.mfft_execute_timed(self._h, ctypes.c_void_p(in_ptr), ctypes.c_void_p(out_ptr),
+                                      ctypes.c_void_p(ws_ptr or None), int(ws_bytes),
                                       ctypes.c_void_p(stream_ptr), ms, cap, ctypes.byref(k)))
         return [float(ms[i]) for i in range(k.value)]
 
@@ -203,15 +207,44 @@ class NativePlan:
         return FLOW_NAMES.get(self.info.flow, str(self.info.flow))
 
     def close(self) -> None:
+        """Destroy the native plan now.  The caller makes sure no execute of
+        it is still pending (mfft_plan_destroy does not synchronise)."""
         h, self._h = self._h, None
         if h is not None and _lib is not None:
             _lib.mfft_plan_destroy(h)
 
     def __del__(self):
-        try:
-            self.close()
-        except Exception:  # noqa: BLE001 -- interpreter shutdown
-            pass
+        # Never destroy from here: a collection can run while kernels that
+        # read the plan's tables are still queued, or inside a graph capture.
+        # The handle waits in a list that release_retired() empties at a
+        # point the owner chooses (after synchronising the device).
+        h, self._h = getattr(self, "_h", None), None
+        if h is not None:
+            _RETIRED.append((h, int(self.info.device) if hasattr(self, "info") else 0))
+
+
+# Native plans dropped by their owners, not yet destroyed: (handle, device).
+_RETIRED: list = []
+
+
+def retired_count() -> int:
+    return len(_RETIRED)
+
+
+def release_retired(sync=None) -> int:
+    """Destroy every retired plan; ``sync(device)`` is called once per
+    device first, to make sure none of their executes is pending.  Returns
+    how many plans were destroyed."""
+    if not _RETIRED or _lib is None:
+        return 0
+    items = _RETIRED[:]
+    del _RETIRED[:len(items)]
+    if sync is not None:
+        for dev in sorted({d for _, d in items}):
+            sync(dev)
+    for h, _ in items:
+        _lib.mfft_plan_destroy(h)
+    return len(items)
 
 
 def bit_reverse_permute(in_ptr: int, out_ptr: int, n: int, batch: int, stream_ptr: int) -> None:

@@ -41,7 +41,7 @@ import torch
 
 from . import native
 from .context import device_name, device_ready  # noqa: F401  (re-exported)
-from .validate import log2_exact, validate_batch_input, validate_input, validate_tensor
+from .validate import log2_exact, validate_batch_input, validate_input, validate_tensor, validate_twiddle
 
 DEFAULT_STAGE_BLOCK = 256
 
@@ -136,9 +136,30 @@ def flow_params(executed: str, n: int, transform_type: str, block, params: dict)
     return flow, ()
 
 
+# Native plans, cached by (flow, params, shape, semantics, device).  They are
+# created with a caller-owned workspace: a plan holds only its twiddle tables
+# (a few KB to a few hundred KB), and every execute that needs scratch takes
+# it from torch's stream-ordered allocator on the stream it runs on, so one
+# cached plan can run on several streams at once.
 _NATIVE: "OrderedDict[tuple, native.NativePlan]" = OrderedDict()
 _NATIVE_LOCK = threading.Lock()
-NATIVE_CACHE_SIZE = 32
+NATIVE_CACHE_SIZE = 256
+# Dropped native plans are destroyed in a batch once this many wait (never
+# inside a graph capture), after one synchronisation of their devices.
+RETIRED_FLUSH = 64
+
+
+def _sync_device(dev: int) -> None:
+    torch.cuda.synchronize(dev)
+
+
+def release_retired_plans() -> int:
+    """Destroy the native plans dropped so far (evicted from the cache, or
+    whose owners went away), after synchronising their devices.  A no-op
+    inside a graph capture.  Returns how many were destroyed."""
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        return 0
+    return native.release_retired(_sync_device)
 
 
 def get_native_plan(executed: str, n: int, batch: int, transform_type: str,
@@ -152,18 +173,23 @@ def get_native_plan(executed: str, n: int, batch: int, transform_type: str,
         if p is not None:
             _NATIVE.move_to_end(key)
             return p
+    if native.retired_count() >= RETIRED_FLUSH:
+        release_retired_plans()
     with torch.cuda.device(device_index):
-        p = native.NativePlan(n, batch, transform_type, transform_direction, norm, flow, prm)
+        p = native.NativePlan(n, batch, transform_type, transform_direction, norm, flow, prm,
+                              caller_workspace=True)
     with _NATIVE_LOCK:
         _NATIVE[key] = p
         while len(_NATIVE) > NATIVE_CACHE_SIZE:
-            _NATIVE.popitem(last=False)
+            _NATIVE.popitem(last=False)  # retired when its last user lets go
     return p
 
 
 def clear_native_cache() -> None:
+    """Drop every cached native plan and destroy those no caller holds."""
     with _NATIVE_LOCK:
         _NATIVE.clear()
+    release_retired_plans()
 
 
 def output_spec(transform_type: str, n: int, batch: int):
@@ -194,10 +220,29 @@ def current_device() -> int:
     return _raw_device() if _raw_device is not None else torch.cuda.current_device()
 
 
+def workspace_for(nplan: native.NativePlan, device) -> "torch.Tensor | None":
+    """Scratch for one execute of ``nplan`` from torch's caching allocator
+    (512-byte aligned, ordered on the current stream), or None."""
+    if not nplan.ws_bytes:
+        return None
+    return torch.empty(nplan.ws_bytes, dtype=torch.uint8, device=device)
+
+
 def launch(nplan: native.NativePlan, x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
-    """Enqueue one execute on x's device and current stream."""
+    """Enqueue one execute on x's device and current stream.  A plan that
+    needs scratch gets it per call on that stream: the block returns to the
+    allocator when this call returns, and the allocator hands it out again
+    only to work ordered after this execute on the same stream."""
     dev = x.get_device()
     stream = stream_handle(dev)
+    if nplan.ws_bytes:
+        ws = torch.empty(nplan.ws_bytes, dtype=torch.uint8, device=x.device)
+        if current_device() == dev:
+            nplan.execute_ws(x.data_ptr(), out.data_ptr(), ws.data_ptr(), nplan.ws_bytes, stream)
+        else:
+            with torch.cuda.device(dev):
+                nplan.execute_ws(x.data_ptr(), out.data_ptr(), ws.data_ptr(), nplan.ws_bytes, stream)
+        return out
     if current_device() == dev:
         nplan.execute(x.data_ptr(), out.data_ptr(), stream)
     else:
@@ -220,8 +265,45 @@ def run(executed: str, x: torch.Tensor, batch: int, n: int, transform_type: str 
 
 # ---------------- reference runner entry points (forward C2C) ----------------
 
-def _single(name, x, block, params=None):
+# Largest deviation of a caller's table from exp(-2*pi*i*idx/N) that still
+# counts as those roots: the reference builds them from a float32 angle
+# (runner.py:93-97), which is off by up to ~2e-7 at N = 2^20.
+TWIDDLE_TOL = 1e-6
+_TWIDDLE_OK: dict = {}  # (ptrs, versions, n, device) of tables already checked
+
+
+def check_twiddle(twiddle, x) -> None:
+    """The reference's twiddle= contract for the stage runners: validate the
+    table (validate.py:71-84), then require that it holds the forward roots
+    exp(-2*pi*i*idx/N), idx < N/2.  Every native plan computes with its own
+    table of those roots (built once per plan); any other table would ask
+    for a different transform, which the library does not run, so it raises
+    ValueError instead of silently using its own.  The value check costs one
+    device round trip per distinct table and is then remembered."""
+    if twiddle is None:
+        return
+    n = x.numel() if x.dim() == 1 else int(x.shape[-1])
+    validate_twiddle(twiddle, n, x.device)
+    wr, wi = twiddle
+    key = (wr.data_ptr(), wi.data_ptr(), wr._version, wi._version, n, str(x.device))
+    if key in _TWIDDLE_OK:
+        return
+    idx = torch.arange(n >> 1, dtype=torch.float64, device=x.device)
+    ang = -2.0 * math.pi * idx / n
+    dev = max(float((wr.double() - torch.cos(ang)).abs().max().item()) if n > 1 else 0.0,
+              float((wi.double() - torch.sin(ang)).abs().max().item()) if n > 1 else 0.0)
+    if not dev <= TWIDDLE_TOL:
+        raise ValueError(f"twiddle table differs from exp(-2*pi*i*idx/{n}) by up to {dev:.3e} "
+                         f"(> {TWIDDLE_TOL:g}): only the forward roots are supported (every plan "
+                         "builds and keeps its own table of them)")
+    if len(_TWIDDLE_OK) > 64:
+        _TWIDDLE_OK.clear()
+    _TWIDDLE_OK[key] = True
+
+
+def _single(name, x, block, params=None, twiddle=None):
     validate_input(x, "x", block=block)
+    check_twiddle(twiddle, x)
     return run(name, x, 1, x.numel(), block=block, params=params, norm="backward")
 
 
@@ -234,12 +316,12 @@ def _batched(name, x, block, params=None):
 
 def fft_dit(x, block: int = DEFAULT_STAGE_BLOCK, twiddle=None):
     """M0 radix-2 DIT: log2(N) stage launches, bit reversal folded into stage 0."""
-    return _single("fft_dit", x, block)
+    return _single("fft_dit", x, block, twiddle=twiddle)
 
 
 def fft_dif(x, block: int = DEFAULT_STAGE_BLOCK, twiddle=None):
     """M0 radix-2 DIF: log2(N) stage launches, bit reversal folded into the last."""
-    return _single("fft_dif", x, block)
+    return _single("fft_dif", x, block, twiddle=twiddle)
 
 
 def fft_dit_batch(x, block: int = DEFAULT_STAGE_BLOCK, variant: str = "folded"):
@@ -257,13 +339,13 @@ def fft_dit_radix4(x, block: int = DEFAULT_STAGE_BLOCK, twiddle=None):
     """M5 radix-4 DIT (radix-2 tail for odd log2 N), digit reversal folded in."""
     if x.numel() < 4:
         raise ValueError(f"radix-4 requires N >= 4, got N={x.numel()}")
-    return _single("fft_dit_radix4", x, block)
+    return _single("fft_dit_radix4", x, block, twiddle=twiddle)
 
 
 def fft_dif_radix4(x, block: int = DEFAULT_STAGE_BLOCK, twiddle=None):
     if x.numel() < 4:
         raise ValueError(f"radix-4 requires N >= 4, got N={x.numel()}")
-    return _single("fft_dif_radix4", x, block)
+    return _single("fft_dif_radix4", x, block, twiddle=twiddle)
 
 
 def fft_dit_radix4_batch(x, block: int = DEFAULT_STAGE_BLOCK, variant: str = "folded"):

@@ -270,22 +270,6 @@ def load_table(path: str = TABLE_PATH) -> dict:
     return table
 
 
-def assert_current_environment(table: dict) -> str:
-    """Freshness gate for measurement scripts: raise unless the live
-    environment matches the table's ``env_hash`` (reference selector.py:482-510)."""
-    bound = table.get("env_hash") or ""
-    if not bound:
-        raise RuntimeError("selector table carries no env_hash; refusing to measure against it")
-    from .envcheck import current_env_hash
-
-    cur = current_env_hash()
-    if cur is None:
-        raise RuntimeError("live environment fingerprint unknown; cannot verify the table")
-    if cur != bound:
-        raise RuntimeError(f"environment hash {cur} != table {bound}; re-measure first")
-    return cur
-
-
 def _abstain(n, direction, batch, precision, reason, tt, td, norm) -> Selection:
     return Selection(n=n, direction=direction, batch=batch, precision=precision, source="abstain",
                      reason=reason, transform_type=tt, transform_direction=td,

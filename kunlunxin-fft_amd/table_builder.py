@@ -190,7 +190,7 @@ def main() -> int:
     from kunlunxin_fft_amd import envcheck
     from kunlunxin_fft_amd.config import DesignSpace, DeviceProfile
     from kunlunxin_fft_amd.entry import ExecutionPlan
-    from kunlunxin_fft_amd.runner import get_native_plan, output_spec
+    from kunlunxin_fft_amd.runner import get_native_plan, output_spec, workspace_for
     from kunlunxin_fft_amd.selector import GUARD_PCT
 
     space = DesignSpace.load()
@@ -216,8 +216,14 @@ def main() -> int:
         np_ = get_native_plan(name, n, b, tt, td, "backward", block, params, 0)
         shape, dt = output_spec(tt, n, b)
         out = torch.empty(shape, dtype=dt, device=dev)
+        ws = workspace_for(np_, dev)
+        wp = ws.data_ptr() if ws is not None else 0
+
+        def execute():
+            np_.execute_ws(x.data_ptr(), out.data_ptr(), wp, np_.ws_bytes, stream.cuda_stream)
+
         for _ in range(3):
-            np_.execute(x.data_ptr(), out.data_ptr(), stream.cuda_stream)
+            execute()
         res = []
         if n * b * (8 if tt == "c2c" else 4) >= (64 << 20):
             for _ in range(args.rounds):
@@ -226,7 +232,7 @@ def main() -> int:
                     s = torch.cuda.Event(enable_timing=True)
                     e = torch.cuda.Event(enable_timing=True)
                     s.record(stream)
-                    np_.execute(x.data_ptr(), out.data_ptr(), stream.cuda_stream)
+                    execute()
                     e.record(stream)
                     e.synchronize()
                     res.append(s.elapsed_time(e))
@@ -236,7 +242,7 @@ def main() -> int:
             e = torch.cuda.Event(enable_timing=True)
             s.record(stream)
             for _ in range(args.reps):
-                np_.execute(x.data_ptr(), out.data_ptr(), stream.cuda_stream)
+                execute()
             e.record(stream)
             e.synchronize()
             res.append(s.elapsed_time(e) / args.reps)

@@ -55,3 +55,22 @@ def validate_batch_input(x, name: str = "x", *, block: int | None = None) -> Non
     log2_exact(int(x.shape[-1]))
     if x.shape[0] < 1:
         raise ValueError(f"{name} batch must be >= 1")
+
+
+def validate_twiddle(tw, n: int, device) -> None:
+    """A caller's twiddle table (reference validate.py:71-84): a ``(cos,
+    sin)`` tuple of float32 tensors of length N/2 on the input's device.
+    Both tables are checked (the reference's loop returns after the first)."""
+    import torch
+
+    if not isinstance(tw, tuple) or len(tw) != 2:
+        raise TypeError("twiddle must be a (cos, sin) tuple from twiddle_tables()")
+    for t, nm in zip(tw, ("cos", "sin")):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"twiddle {nm} must be a torch.Tensor")
+        if t.dtype != torch.float32:
+            raise TypeError(f"twiddle {nm} must be float32, got {t.dtype}")
+        if t.device != device:
+            raise ValueError(f"twiddle {nm} device {t.device} != input device {device}")
+        if t.numel() != n >> 1:
+            raise ValueError(f"twiddle {nm} length {t.numel()} != N/2 ({n >> 1})")

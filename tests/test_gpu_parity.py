@@ -472,9 +472,12 @@ def test_config4_n2p16_b256(gpu):
     assert np.abs(ey / ex - 1).max() < 1e-5
 
 
-@pytest.mark.parametrize("n", [16, 64, 256, 1024, 4096, 16384])
+@pytest.mark.parametrize("n", [1 << k for k in range(4, 15)])
 @pytest.mark.parametrize("b", [1, 16, 64, 256])
 def test_config5_selector_and_m0_cells(gpu, n, b):
+    """All 44 cells of the selector sweep: the selected plan and the M0
+    incumbent (fft_dit / fft_dit_batch) against the C oracle (numpy for the
+    cells above 2^20 points)."""
     prof = DeviceProfile.load().hash()
     x = seeded_c64(n, b)
     xd = torch.from_numpy(x).to(gpu)

@@ -154,3 +154,45 @@ def test_no_workspace_plan_two_streams(gpu, flow, params, n):
         rows = [0, b - 1]
         ref = np.fft.fft(h[rows].astype(np.complex128))
         assert oracle.rel_l2(y[rows].cpu().numpy(), ref) <= TOL
+
+
+def test_plan_api_two_streams_share_cached_plans(gpu):
+    """execute_fft_plan on two streams at once, for plans that need scratch
+    (an M0 stage flow and a 2^18-point R2C over the four-step core): the
+    cached native plans take their scratch per call from torch's allocator
+    on the calling stream, so overlapping executes do not share it.  Every
+    result equals the same plan's eager result on the default stream."""
+    from kunlunxin_fft_amd import ExecutionPlan, execute_fft_plan
+
+    def mk(executed, n, b, tt="c2c", params=None):
+        return ExecutionPlan(n=n, batch=b, direction="dit", precision="fp32", selection_source="table",
+                             reason="test", fallback=False, executed=executed, block=256, flow_id="test",
+                             flow_realization="test", processing_unit="test", params=params or {},
+                             transform_type=tt)
+
+    m0 = mk("fft_dit_batch", 4096, 64)
+    r2c = mk("fft_four_step_batch", 1 << 18, 4, tt="r2c", params={"n1": 256})
+    xs = {}
+    for plan, seed in ((m0, 41), (r2c, 42)):
+        rng = np.random.default_rng(seed)
+        for k in range(2):
+            if plan.transform_type == "r2c":
+                h = rng.standard_normal((plan.batch, plan.n)).astype(np.float32)
+            else:
+                h = (rng.standard_normal((plan.batch, plan.n))
+                     + 1j * rng.standard_normal((plan.batch, plan.n))).astype(np.complex64)
+            xs[(id(plan), k)] = torch.from_numpy(h).to(gpu)
+    eager = {key: execute_fft_plan(m0 if key[0] == id(m0) else r2c, x).cpu() for key, x in xs.items()}
+    s1, s2 = torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)
+    torch.cuda.synchronize()
+    outs = {}
+    for _ in range(3):
+        for k, st in ((0, s1), (1, s2)):
+            with torch.cuda.stream(st):
+                for plan in (m0, r2c):
+                    x = xs[(id(plan), k)]
+                    x.record_stream(st)
+                    outs[(id(plan), k)] = execute_fft_plan(plan, x)
+    torch.cuda.synchronize()
+    for key, y in outs.items():
+        assert torch.equal(y.cpu(), eager[key]), key

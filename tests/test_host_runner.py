@@ -122,3 +122,51 @@ def test_real_candidates_respect_the_real_modes():
                 e = _entry(params, real=real, unit=unit, n=n, b=b, executed=name)
                 e.update(transform_type=tt, transform_direction=td, normalization="backward")
                 assert not entry_contract_violations(e), (tt, n, label, entry_contract_violations(e))
+
+
+def test_twiddle_contract_on_host_tensors():
+    """runner.check_twiddle (reference validate.py:71-84 plus a value check),
+    run on CPU tensors: forward-root tables pass, others raise."""
+    import math
+
+    import torch
+
+    from kunlunxin_fft_amd.runner import TWIDDLE_TOL, check_twiddle, twiddle_tables
+
+    for n in (2, 8, 1 << 12):
+        x = torch.zeros(n, dtype=torch.complex64)
+        check_twiddle(None, x)
+        check_twiddle(twiddle_tables(n, "cpu"), x)
+        # the reference's own tables: float32 angle, then cos/sin (runner.py:93-97)
+        ang = (-2.0 * math.pi * torch.arange(n >> 1, dtype=torch.float32) / n).to(torch.float32)
+        check_twiddle((torch.cos(ang), torch.sin(ang)), x)
+        wr, wi = twiddle_tables(n, "cpu")
+        wi = wi.clone()
+        wi[0] += 10 * TWIDDLE_TOL
+        with pytest.raises(ValueError, match="differs"):
+            check_twiddle((wr, wi), x)
+        # the inverse roots are a different table
+        if n > 2:
+            with pytest.raises(ValueError, match="differs"):
+                check_twiddle((wr, -twiddle_tables(n, "cpu")[1]), x)
+    x = torch.zeros(16, dtype=torch.complex64)
+    wr, wi = twiddle_tables(16, "cpu")
+    with pytest.raises(ValueError, match="length"):
+        check_twiddle((wr[:4], wi[:4]), x)
+    with pytest.raises(TypeError, match="float32"):
+        check_twiddle((wr.double(), wi), x)
+    with pytest.raises(TypeError, match="tuple"):
+        check_twiddle([wr, wi], x)
+    with pytest.raises(TypeError, match="torch.Tensor"):
+        check_twiddle((wr, wi.numpy()), x)
+
+
+def test_semantic_families():
+    from kunlunxin_fft_amd.semantic import family_allows
+
+    assert family_allows("r2c", "dedicated-r2c-pack-v1")
+    assert not family_allows("c2r", "dedicated-r2c-pack-v1")
+    assert not family_allows("c2c", "dedicated-c2r-hermitian-v1")
+    assert all(family_allows(t, "four-step-two-pass") for t in ("c2c", "r2c", "c2r"))
+    with pytest.raises(KeyError):
+        family_allows("dct", "four-step-two-pass")

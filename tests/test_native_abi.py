@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     lib = native.load()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.mfft_abi_version() == 1
+    assert lib.mfft_abi_version() == 2
 
 
 def test_struct_layouts():
