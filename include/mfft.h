@@ -80,7 +80,10 @@ enum {
     MFFT_FLOW_RADIX4_DIT = 3,  /* M5 fft_dit_radix4: digit reversal folded into stage 0 (runner.py:1399-1470) */
     MFFT_FLOW_RADIX4_DIF = 4,  /* M5 fft_dif_radix4 (runner.py:1473-1540) */
     MFFT_FLOW_LDS_FUSED = 5,   /* one pass: whole transform resident in LDS/registers (core n <= 32768) */
-    MFFT_FLOW_FOUR_STEP = 6    /* two passes: column FFTs + twiddle, then row FFTs (core n >= 256) */
+    MFFT_FLOW_FOUR_STEP = 6,   /* two passes: column FFTs + twiddle, then row FFTs (core n >= 256) */
+    MFFT_FLOW_DENSE_MFMA = 7   /* M2 fft_{dit,dif}_matrix (runner.py:379-442, kernels.py:487-532): one pass,
+                                  every butterfly a dense DFT-8 matrix product on the fp32 matrix cores;
+                                  the first two passes form the 8 x 8 factored DFT-64 (core n 2..16384) */
 };
 
 /* Flow parameters (params[i], all optional, 0 = library default):
@@ -93,6 +96,7 @@ enum {
  *                                    every XCD's CUs start params[1] x 8128
  *                                    clocks late, so that CUs stop loading,
  *                                    computing and storing in lockstep
+ *   DENSE_MFMA:          no parameters
  *   FOUR_STEP:           params[0] = n1 (column FFT length; n2 = core_n/n1),
  *                        params[1] = batch rows per chunk (both passes run
  *                                    chunk by chunk, and a real transform's

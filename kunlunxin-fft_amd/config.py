@@ -106,6 +106,7 @@ class DesignSpace:
     lds_elems: tuple
     lds_max_n: int
     lds_stagger: tuple
+    dense_max_n: int
     fourstep_n1: tuple
     fourstep_chunk_rows: tuple
     fourstep_min_n: int
@@ -126,6 +127,9 @@ class DesignSpace:
         st = p.get("global_stage", {})
         _require(_pow2_list(st.get("blocks")), "butterfly_space.json: P.global_stage.blocks must be powers of two")
         lds = p.get("lds_fused", {})
+        dense = p.get("dense_mfma", {})
+        _require(isinstance(dense.get("max_n"), int) and 2 <= dense["max_n"] <= 16384,
+                 "butterfly_space.json: P.dense_mfma.max_n must be in [2, 16384]")
         _require(_pow2_list(lds.get("elems")), "butterfly_space.json: P.lds_fused.elems must be powers of two")
         _require(isinstance(lds.get("max_n"), int) and lds["max_n"] > 0, "butterfly_space.json: P.lds_fused.max_n required")
         stag = lds.get("stagger", [0])
@@ -154,7 +158,7 @@ class DesignSpace:
         return DesignSpace(
             space_id=d["space_id"], target=d["target"], radix=tuple(p["radix"]),
             stage_blocks=tuple(st["blocks"]), lds_elems=tuple(lds["elems"]), lds_max_n=lds["max_n"],
-            lds_stagger=tuple(stag),
+            lds_stagger=tuple(stag), dense_max_n=dense["max_n"],
             fourstep_n1=tuple(fs["n1"]), fourstep_chunk_rows=tuple(ch), fourstep_min_n=fs["min_n"],
             fourstep_schedule=tuple(sched), fourstep_pass2_order=tuple(order),
             batch_candidates=tuple(b["candidates"]), batch_variants=tuple(variants),

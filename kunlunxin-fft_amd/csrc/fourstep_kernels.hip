@@ -428,53 +428,58 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG), 4) void fourstep_pe
 // Fused schedule: both passes in one launch, each transform's pass 2 reading
 // pass 1's output Z while it is still in the L2 of the XCD that wrote it.
 // Every block reads the XCD it runs on (hardware register XCC_ID) and takes
-// work only for the transforms t == xcd (mod 8) of the launch, from that
-// XCD's queue: pass-1 groups of transform k, then pass-2 groups of transform
-// k-1, and so on.  A pass-2 group first waits until all pass-1 groups of its
-// transform have stored Z.  Every pass-1 group is handed out before any
-// pass-2 group of the same transform and never waits, so the wait always
-// ends; it is nevertheless bounded by `wait_ticks` of the constant-rate wall
-// clock, and counted in sync[8] when exceeded.  Producer and consumer share
-// one L2 and the consumer's L1 has never held these lines (each group's rows
-// are whole 128-byte lines of its own), so completed stores plus a counter
-// in L2 are the whole handshake: no cache write-back or invalidation.  Both
-// sides touch the counter with read-modify-write atomics, which execute
-// where the producer's increments live; an atomic load would be issued
-// system-coherent and read memory behind the L2, never seeing them.
-// sync (int32, zeroed before the launch): [0, 8) next item per XCD, [8]
-// overruns, [9, 9 + rows) pass-1 groups done per transform.
+// work only from the queue of that XCD's slot, XCC_ID mod nslot (nslot = the
+// device's XCD count, so a partitioned device with fewer XCDs still drains
+// every queue): transform t belongs to slot t mod nslot, and its queue hands
+// out pass-1 groups of the slot's transform k, then pass-2 groups of k-1, and
+// so on.  A pass-2 group first waits until all pass-1 groups of its transform
+// have stored Z.  Every pass-1 group is handed out, to a block that is
+// running, before any pass-2 group of the same transform, and pass-1 groups
+// never wait, so the wait always ends whatever the residency; it is
+// nevertheless bounded by `wait_ticks` of the constant-rate wall clock and by
+// a trip count.  A wait that gives up is counted in sync[kFusedOverrun] and
+// its group writes NaN instead of a transform of incomplete data.  Producer
+// and consumer share one L2 and the consumer's L1 has never held these lines
+// (each group's rows are whole 128-byte lines of its own), so completed
+// stores plus a counter in L2 are the whole handshake: no cache write-back or
+// invalidation.  Both sides touch the counter with read-modify-write atomics,
+// which execute where the producer's increments live; an atomic load would be
+// issued system-coherent and read memory behind the L2, never seeing them.
+// Every branch of the work loop is on a wave-uniform value: wave 0 does the
+// queue and counter atomics with all of its lanes (lane 0 adds 1, the others
+// 0), and only scalar-register values steer the loop.  (A per-thread
+// `if (tid == 0)` beside the barriers let the compiler split the loop into an
+// inner loop around the barriers that only thread 0 could leave.)  The loop
+// also stops after `total + 1` trips: a block dequeues at most `total` items.
+// sync (int32, zeroed before the launch): [0, kFusedSlots) next item per
+// slot, [kFusedOverrun] overruns, [kFusedHead, kFusedHead + rows) pass-1
+// groups done per transform.
 template <int LL1, int LE1, int LC1, int LL2, int LE2, int LC2, int DIR>
 __global__ __launch_bounds__((ColCfg<LL1, LE1, LC1>::WG)) void fourstep_fused_kernel(
     const float2* src, float2* dst, const float2* __restrict__ tw1, const float2* __restrict__ tw2,
     const float2* __restrict__ tw_lo, const float2* __restrict__ tw_hi, int tw_h, float scale, int rows,
-    int* sync, long long wait_ticks) {
+    int nslot, int* sync, long long wait_ticks) {
     using A = ColCfg<LL1, LE1, LC1>;
     using B = ColCfg<LL2, LE2, LC2>;
     static_assert(A::WG == B::WG, "both passes run with the same block size");
     constexpr int LDS_N = A::LDS_FLOAT2 > B::LDS_FLOAT2 ? A::LDS_FLOAT2 : B::LDS_FLOAT2;
     __shared__ float2 lds[LDS_N];
-    __shared__ int item_s;
+    __shared__ int item_s, fail_s;
     constexpr int LOGN = LL1 + LL2;
     constexpr int G1 = (1 << LL2) >> LC1;  // pass-1 column groups per transform (columns n2)
     constexpr int G2 = (1 << LL1) >> LC2;  // pass-2 column groups per transform (columns k1)
+    constexpr int kMaxPolls = 1 << 22;     // a second bound on one wait, besides the clock
     const int tid = threadIdx.x;
     // HW_REG_XCC_ID (hwreg 20), bits [3:0]
-    const int xcd = (int)__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 7;
-    const int nt = rows > xcd ? (rows - xcd + 7) / 8 : 0;  // this XCD's transforms: t = xcd + 8k
+    const int xcc = (int)__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15;
+    const int slot = __builtin_amdgcn_readfirstlane(xcc % nslot);
+    const int nt = rows > slot ? (rows - slot + nslot - 1) / nslot : 0;  // this slot's transforms
     const int total = nt * (G1 + G2);
-    int* done = sync + 9;
-    // Every branch in this loop is wave-uniform (a scalar branch).  A
-    // per-thread `if (tid == 0)` next to the barriers lets the compiler
-    // thread the paths of thread 0 and of the others apart: the loop is then
-    // compiled as an inner loop around the barriers whose exit is taken by
-    // thread 0 alone, the other lanes of its wave run the barriers again
-    // without it, and the block re-reads a stale item forever.  So wave 0
-    // runs the queue and counter atomics with all of its lanes (lane 0 adds
-    // 1, the others 0) and only scalar-register values steer control flow.
+    int* done = sync + kFusedHead;
     const bool lead = __builtin_amdgcn_readfirstlane(tid) < 64;  // wave 0
     const int one = tid == 0 ? 1 : 0;
-    for (;;) {
-        if (lead) item_s = __builtin_amdgcn_readfirstlane(atomicAdd(sync + xcd, one));
+    for (int trip = 0; trip <= total; ++trip) {
+        if (lead) item_s = __builtin_amdgcn_readfirstlane(atomicAdd(sync + slot, one));
         __syncthreads();
         const int it = __builtin_amdgcn_readfirstlane(item_s);
         __syncthreads();  // every thread has read item_s before it is written again
@@ -489,7 +494,7 @@ __global__ __launch_bounds__((ColCfg<LL1, LE1, LC1>::WG)) void fourstep_fused_ke
             if (blk < nt - 1 && r < G1) k = blk + 1, g = r, second = false;
             else k = blk, g = blk < nt - 1 ? r - G1 : r, second = true;
         }
-        const int t = xcd + 8 * k;
+        const int t = slot + nslot * k;
         const int64_t base = (int64_t)t << LOGN;
         // the lane index, hidden from the optimizer per item, so lane
         // addresses are recomputed per item instead of held across the loop
@@ -513,29 +518,34 @@ __global__ __launch_bounds__((ColCfg<LL1, LE1, LC1>::WG)) void fourstep_fused_ke
                 // an (L2-bypassing) atomic load by the compiler
                 const int zero = opaque(0);
                 const long long t_start = wall_clock64();
-                while (__builtin_amdgcn_readfirstlane(atomicAdd(done + t, zero)) < G1) {
-                    if (wall_clock64() - t_start > wait_ticks) {
-                        atomicAdd(sync + 8, one);
+                int ok = 1;
+                for (int poll = 0; __builtin_amdgcn_readfirstlane(atomicAdd(done + t, zero)) < G1; ++poll) {
+                    if (poll >= kMaxPolls || wall_clock64() - t_start > wait_ticks) {
+                        atomicAdd(sync + kFusedOverrun, one);
+                        ok = 0;
                         break;
                     }
                     __builtin_amdgcn_s_sleep(2);
                 }
+                fail_s = 1 - ok;
             }
             __syncthreads();
+            const int failed = __builtin_amdgcn_readfirstlane(fail_s);
             const int c = tl & (B::C - 1), j = tl >> LC2, c0 = g << LC2;
             float2 v[B::E];
             col_load<B>(v, dst + base + c0, c, j, LL1);
             col_passes<B, DIR, 1, true>(v, lds, tw2, c, j, [&] { return BigTw<B>{}; });
-            col_store<B, 1>(v, dst + base + c0, lds, tl, c, j, LL1, scale);
+            // a group whose wait gave up writes NaN, not a transform of partial data
+            col_store<B, 1>(v, dst + base + c0, lds, tl, c, j, LL1, failed ? __builtin_nanf("") : scale);
         }
     }
 }
 
-// clears a fused launch's counters: sync[0, 8) and sync[9, n); sync[8]
-// (wait overruns) accumulates over the plan's launches
+// clears a fused launch's counters: the queues and the per-transform counts;
+// sync[kFusedOverrun] (wait overruns) accumulates over the plan's launches
 __global__ void zero_sync(int* sync, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n && i != 8) sync[i] = 0;
+    if (i < n && i != kFusedOverrun) sync[i] = 0;
 }
 
 // Blocks of the persistent kernel one CU holds at once (occupancy query,
@@ -617,7 +627,7 @@ hipError_t launch_fused_one(const float2* src, float2* dst, const mfft_plan* p, 
                             hipStream_t stream) {
     constexpr int E1 = col_loge(L1), C1 = col_logc(L1), E2 = col_loge(L2), C2 = col_logc(L2);
     using A = ColCfg<L1, E1, C1>;
-    const int nsync = 9 + (int)rows;
+    const int nsync = kFusedHead + (int)rows;
     zero_sync<<<(nsync + 255) / 256, 256, 0, stream>>>(p->sync, nsync);
     mark(stream);
     static const int per_cu = [] {
@@ -629,10 +639,12 @@ hipError_t launch_fused_one(const float2* src, float2* dst, const mfft_plan* p, 
         }
         return b > 0 ? b : 1;
     }();
-    // one resident wave of blocks, a multiple of the 8 XCDs
-    const int grid = ((per_cu * p->num_cus) / 8) * 8 > 0 ? ((per_cu * p->num_cus) / 8) * 8 : 8;
+    // one resident wave of blocks, a multiple of the XCD count (blocks go to
+    // the XCDs round-robin, so every XCD, and every queue, gets blocks)
+    const int nx = p->num_xcc;
+    const int grid = ((per_cu * p->num_cus) / nx) * nx > 0 ? ((per_cu * p->num_cus) / nx) * nx : nx;
     fourstep_fused_kernel<L1, E1, C1, L2, E2, C2, DIR><<<grid, A::WG, 0, stream>>>(
-        src, dst, p->tw_n1, p->tw_n2, p->tw_lo, p->tw_hi, p->tw_h, scale, (int)rows, p->sync,
+        src, dst, p->tw_n1, p->tw_n2, p->tw_lo, p->tw_hi, p->tw_h, scale, (int)rows, nx, p->sync,
         (long long)kFusedWaitMs * p->clock_khz);
     mark(stream);
     return hipGetLastError();

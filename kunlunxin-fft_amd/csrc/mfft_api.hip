@@ -181,6 +181,9 @@ int run_core(const mfft_plan* p, const float2* src, float2* dst, int dir, float 
         case MFFT_FLOW_FOUR_STEP:
             e = mfft::launch_fourstep(dir, src, dst, p, p->batch, scale, stream, &launches);
             break;
+        case MFFT_FLOW_DENSE_MFMA:
+            e = mfft::launch_mfma(dir, mfft::ilog2((int)p->core_n), src, dst, p->tw, p->batch, scale, stream);
+            break;
         default:
             return fail(MFFT_ERR_VALUE, "internal: unknown flow %d", p->flow);
     }
@@ -399,16 +402,21 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
                             "the fused FOUR_STEP schedule needs n1, n2 in [128, 512] within a factor 2 "
                             "(got 2^%d x 2^%d)",
                             l1, l2);
-            // The fused schedule did not finish on the MI355X (its first launch, N=2^14 B=1, ran
-            // past a 60 s limit twice).  Its work loop had been compiled into an inner loop around
-            // the barriers that only thread 0 could leave, so the other lanes redid a stale item
-            // forever; the loop now branches on wave-uniform values only, which has not yet run on
-            // the GPU, so the schedule stays switched off.
+            // The fused schedule did not finish on the MI355X in two runs (N=2^14, B=1): its work
+            // loop had been compiled into an inner loop around the barriers that only thread 0
+            // could leave.  The loop now branches on wave-uniform values only and is bounded by
+            // its item count; until that has run on the GPU the schedule stays switched off.
             if (schedule == 2 && !mfft::kFusedScheduleEnabled)
                 return fail(MFFT_ERR_UNSUPPORTED,
                             "the fused FOUR_STEP schedule (params[2] = 2) is disabled in this build");
             break;
         }
+        case MFFT_FLOW_DENSE_MFMA:
+            if (!mfft::mfma_supported(logc))
+                return fail(MFFT_ERR_UNSUPPORTED, "DENSE_MFMA runs core lengths 2..2^%d (got core length %lld)",
+                            mfft::kMaxMfmaLog2, (long long)core_n);
+            block = core_n > 4096 ? (int)(core_n / 16) : 256;  // threads per block of the kernel
+            break;
         default:
             return fail(MFFT_ERR_VALUE, "unknown flow id %d", flow);
     }
@@ -422,6 +430,12 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
     int clock_khz = 0;
     he = hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, dev);
     if (he != hipSuccess) return hip_fail(he, "hipDeviceGetAttribute(WallClockRate)");
+    int num_xcc = 0;
+    he = hipDeviceGetAttribute(&num_xcc, hipDeviceAttributeNumberOfXccs, dev);
+    if (he != hipSuccess) return hip_fail(he, "hipDeviceGetAttribute(NumberOfXccs)");
+    if (schedule == 2 && (num_xcc < 1 || num_xcc > mfft::kFusedSlots))
+        return fail(MFFT_ERR_UNSUPPORTED, "the fused FOUR_STEP schedule needs 1..%d XCDs (device reports %d)",
+                    mfft::kFusedSlots, num_xcc);
 
     mfft_plan* p = new (std::nothrow) mfft_plan();
     if (!p) return fail(MFFT_ERR_RUNTIME, "out of host memory");
@@ -443,6 +457,7 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
     p->pass2_rev = pass2_rev;
     p->num_cus = num_cus > 0 ? num_cus : 1;
     p->clock_khz = clock_khz > 0 ? clock_khz : 100000;
+    p->num_xcc = num_xcc > 0 ? num_xcc : 1;
     p->r2c_fused = transform_type == MFFT_R2C && flow == MFFT_FLOW_LDS_FUSED;
     p->c2r_fused = transform_type == MFFT_C2R && flow == MFFT_FLOW_LDS_FUSED;
     // c2r: the half-length inverse core carries a factor 2 (entry.py:583-587)
@@ -498,9 +513,10 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
         else p->ws_bytes += (int64_t)core_bytes;
     }
     if (rc == MFFT_OK && schedule == 2) {
-        // fused four-step counters: 9 + rows of one launch (a chunk, or the batch)
+        // fused four-step counters: the queues, the overrun count, and one
+        // per transform of a launch (a chunk, or the batch)
         const int64_t rows = chunk > 0 && chunk < batch ? chunk : batch;
-        const size_t sb = (size_t)(9 + rows) * sizeof(int);
+        const size_t sb = (size_t)(mfft::kFusedHead + rows) * sizeof(int);
         he = hipMalloc((void**)&p->sync, sb);
         if (he == hipSuccess) he = hipMemsetAsync(p->sync, 0, sb, us);
         if (he != hipSuccess) rc = hip_fail(he, "hipMalloc(four-step counters)");
@@ -514,7 +530,8 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
         case MFFT_FLOW_RADIX2_DIF: core_launches = logc; break;
         case MFFT_FLOW_RADIX4_DIT:
         case MFFT_FLOW_RADIX4_DIF: core_launches = logc / 2 + (logc & 1); break;
-        case MFFT_FLOW_LDS_FUSED: core_launches = 1; break;
+        case MFFT_FLOW_LDS_FUSED:
+        case MFFT_FLOW_DENSE_MFMA: core_launches = 1; break;
         case MFFT_FLOW_FOUR_STEP: {
             const int64_t ch = chunk > 0 ? chunk : batch;
             const int64_t nc = (batch + ch - 1) / ch;
@@ -667,7 +684,7 @@ int mfft_plan_sync_overruns(const mfft_plan* p, int64_t* count) {
     *count = 0;
     if (!p->sync) return MFFT_OK;
     int v = 0;
-    hipError_t he = hipMemcpy(&v, p->sync + 8, sizeof(int), hipMemcpyDeviceToHost);
+    hipError_t he = hipMemcpy(&v, p->sync + mfft::kFusedOverrun, sizeof(int), hipMemcpyDeviceToHost);
     if (he != hipSuccess) return hip_fail(he, "hipMemcpy(four-step counters)");
     *count = v;
     return MFFT_OK;

@@ -24,6 +24,7 @@ struct mfft_plan {
     int pass2_rev = 0;   // FOUR_STEP: pass 2 walks the batch rows in reverse order
     int num_cus = 0;     // compute units of `device` (persistent / fused grid size)
     int clock_khz = 0;   // constant wall-clock rate of `device` (fused schedule wait bound)
+    int num_xcc = 8;     // XCDs of `device` (fused schedule work queues)
     bool r2c_fused = false, c2r_fused = false;
 
     // device memory owned by the plan
@@ -36,7 +37,7 @@ struct mfft_plan {
     float2* tw_real = nullptr;  // exp(-2*pi*i*k/n), k in [0, n/2]  (r2c stitch / c2r pre)
     float2* ws_a = nullptr;     // core-sized scratch (real flows: core output / input)
     float2* ws_b = nullptr;     // core-sized scratch (stage-flow ping-pong)
-    int* sync = nullptr;        // fused four-step: [0,8) work counters, [8] wait overruns, then one per row
+    int* sync = nullptr;        // fused four-step counters (kFusedSlots, kFusedOverrun, kFusedHead)
     int64_t ws_bytes = 0, table_bytes = 0;  // device memory held by the plan
     // Scratch an execute needs: ws_a and/or ws_b, each core_bytes; caller
     // workspaces hold ws_a at offset 0 and ws_b at work_b_off.
@@ -94,12 +95,24 @@ hipError_t launch_lds(int mode, int dir, int log2l, int elems, const void* src, 
                       const float2* tw, const float2* tw_real, int64_t rows, float scale,
                       hipStream_t stream, int num_cus = 0, int stagger = 0);
 
+// ---- mfma_kernels.hip: dense-dot core on the fp32 matrix cores -----------
+constexpr int kMaxMfmaLog2 = 14;  // core length 2 .. 16384
+bool mfma_supported(int log2l);
+// c2c core over `rows` rows of length 2^log2l; tw = W_L^m for m < L
+hipError_t launch_mfma(int dir, int log2l, const float2* src, float2* dst, const float2* tw, int64_t rows,
+                       float scale, hipStream_t stream);
+
 // ---- fourstep_kernels.hip: two-pass column/row FFT -----------------------
 bool fourstep_supported(int log2n1, int log2n2);
 bool fourstep_fused_supported(int log2n1, int log2n2);  // schedule 2: n1, n2 in [128, 512], within 2x
 constexpr int kMaxStagger = 16;  // LDS_FUSED start stagger limit (16 x 8128 clocks)
 constexpr int kFusedWaitMs = 20;  // longest pass-2 wait of the fused schedule before it gives up
-constexpr bool kFusedScheduleEnabled = false;  // fused schedule switched off until its fixed loop has run on the GPU
+constexpr bool kFusedScheduleEnabled = false;  // switched off until its bounded loop has run on the GPU
+// fused-schedule counters: [0, kFusedSlots) work queues (one per XCD),
+// [kFusedOverrun] wait overruns, then one per transform of a launch
+constexpr int kFusedSlots = 16;
+constexpr int kFusedOverrun = kFusedSlots;
+constexpr int kFusedHead = kFusedSlots + 1;
 int fourstep_col_loge(int logl);  // log2 elements per thread of a pass of length 2^logl
 void fourstep_default_split(int log2n, int* log2n1, int* log2n2);
 hipError_t launch_fourstep(int dir, const float2* src, float2* dst, const mfft_plan* p,

@@ -24,12 +24,13 @@ NORM_IDS = {"none": 0, "forward": 1, "backward": 2, "ortho": 3}
 TYPE_IDS = {"c2c": C2C, "r2c": R2C, "c2r": C2R}
 DIR_IDS = {"forward": FORWARD, "inverse": INVERSE}
 FLOW_AUTO, FLOW_RADIX2_DIT, FLOW_RADIX2_DIF, FLOW_RADIX4_DIT, FLOW_RADIX4_DIF, \
-    FLOW_LDS_FUSED, FLOW_FOUR_STEP = range(7)
+    FLOW_LDS_FUSED, FLOW_FOUR_STEP, FLOW_DENSE_MFMA = range(8)
 FLOW_NAMES = {
     FLOW_AUTO: "auto", FLOW_RADIX2_DIT: "radix2-dit", FLOW_RADIX2_DIF: "radix2-dif",
     FLOW_RADIX4_DIT: "radix4-dit", FLOW_RADIX4_DIF: "radix4-dif",
-    FLOW_LDS_FUSED: "lds-fused", FLOW_FOUR_STEP: "four-step",
+    FLOW_LDS_FUSED: "lds-fused", FLOW_FOUR_STEP: "four-step", FLOW_DENSE_MFMA: "dense-mfma",
 }
+MAX_MFMA_CORE = 1 << 14
 ERR_VALUE, ERR_TYPE, ERR_RUNTIME, ERR_UNSUPPORTED = 1, 2, 3, 4
 MAX_PARAMS = 4
 

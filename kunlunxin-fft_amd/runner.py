@@ -14,15 +14,17 @@ fft_dif_radix4(_batch) (runner.py:1473,1193) RADIX4_DIF (M5)                 blo
 fft_lds_fused(_batch)                        LDS_FUSED (single pass)         elems
 fft_four_step(_batch)                        FOUR_STEP (two passes)          n1, chunk_rows, schedule
 fft_dit_fused (runner.py:209)                LDS_FUSED / FOUR_STEP (auto)    --
-fft_{dit,dif}_matrix(_batch) (runner.py:379) LDS_FUSED / FOUR_STEP (auto)    --
+fft_{dit,dif}_matrix(_batch) (runner.py:379) DENSE_MFMA (core 2..16384)      --
 fft_{dit,dif}_grouped (runner.py:505)        LDS_FUSED / FOUR_STEP (auto)    --
 run_hybrid (adapter_hybrid.py:224)           FOUR_STEP (n1 = N/tile)         tile
 ===========================================  ==============================  =========
 
-The M1/M2/M3 names exist so a plan naming them still runs: on MI355X the
-stages they fuse (in global memory, as a dense matmul, or as XOR-gather
-maps) all run inside one LDS-resident kernel, or the four-step for core
-lengths above 32768.
+The M2 names (the reference's dense-dot matrix flow) run the dense-dot core
+on the fp32 matrix cores, every butterfly a DFT-8 matrix product (cores of
+2..16384 points; longer ones go to the library's choice).  The M1/M3 names
+exist so a plan naming them still runs: on MI355X the stages they fuse (in
+global memory, or as XOR-gather maps) all run inside one LDS-resident
+kernel, or the four-step for core lengths above 32768.
 
 Every transform semantic -- C2C forward/inverse with its norm, R2C and C2R
 -- is one native plan: the conjugation, the norm scale and the real-FFT
@@ -60,10 +62,10 @@ RUNNER_FLOWS = {
     "fft_four_step": (native.FLOW_FOUR_STEP, "fourstep"),
     "fft_four_step_batch": (native.FLOW_FOUR_STEP, "fourstep"),
     "fft_dit_fused": (native.FLOW_AUTO, "none"),
-    "fft_dit_matrix": (native.FLOW_AUTO, "none"),
-    "fft_dif_matrix": (native.FLOW_AUTO, "none"),
-    "fft_dit_matrix_batch": (native.FLOW_AUTO, "none"),
-    "fft_dif_matrix_batch": (native.FLOW_AUTO, "none"),
+    "fft_dit_matrix": (native.FLOW_DENSE_MFMA, "dense"),
+    "fft_dif_matrix": (native.FLOW_DENSE_MFMA, "dense"),
+    "fft_dit_matrix_batch": (native.FLOW_DENSE_MFMA, "dense"),
+    "fft_dif_matrix_batch": (native.FLOW_DENSE_MFMA, "dense"),
     "fft_dit_grouped": (native.FLOW_AUTO, "none"),
     "fft_dif_grouped": (native.FLOW_AUTO, "none"),
     "run_hybrid": (native.FLOW_FOUR_STEP, "hybrid"),
@@ -129,6 +131,12 @@ def flow_params(executed: str, n: int, transform_type: str, block, params: dict)
         if b < 64 or b > 1024:
             raise ValueError(f"block must be a power of two in [64, 1024], got {b}")
         return flow, (b,)
+    if kind == "dense":
+        # the dense-dot matrix-core flow runs cores of 2 .. 16384 points;
+        # other lengths leave the flow to the library
+        if not 2 <= core <= native.MAX_MFMA_CORE:
+            return native.FLOW_AUTO, ()
+        return flow, ()
     if kind == "hybrid":
         tile = int(params.get("tile", 0))
         n1 = core // tile if tile and core % tile == 0 else 0
@@ -383,7 +391,8 @@ def fft_dit_fused(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64):
 
 
 def fft_dit_matrix(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64, rows: int = 8):
-    """Reference M2 name: runs the LDS / four-step kernels on MI355X."""
+    """Reference M2 name: the dense-dot core on the fp32 matrix cores
+    (cores of 2..16384 points; the library's choice above)."""
     return _single("fft_dit_matrix", x, None)
 
 

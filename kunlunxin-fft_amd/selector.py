@@ -110,6 +110,11 @@ def entry_contract_violations(entry: dict) -> list[str]:
             bad.append(f"stagger {stg!r} not in {sp.lds_stagger}")
         if isinstance(n, int) and n > 2 * sp.lds_max_n:
             bad.append(f"N={n} exceeds the LDS kernel's range ({sp.lds_max_n} complex core)")
+    if real == "matrix-resident":
+        if params.get("elems") or params.get("n1") or params.get("stagger"):
+            bad.append("the dense-dot matrix-core flow takes no elems / stagger / n1 parameters")
+        if isinstance(n, int) and n > 2 * sp.dense_max_n:
+            bad.append(f"N={n} exceeds the dense-dot core's range ({sp.dense_max_n} complex core)")
     if real == "four-step":
         n1 = params.get("n1", 0)
         if n1 not in (0,) + sp.fourstep_n1:

@@ -5,7 +5,8 @@ MI355X counterpart of the reference's table builder
 For every cell (N, batch, direction) it times the M0 incumbent (fft_dit /
 fft_dif and their batch forms) and every legal challenger of the published
 design space (config/butterfly_space.json): the radix-4 global-stage flow,
-the single-pass LDS kernel at each elements-per-thread setting (and start
+the dense-dot matrix-core flow (the reference's M2 FFT64 on fp32 MFMA), the
+single-pass LDS kernel at each elements-per-thread setting (and start
 stagger, where it can act), and the four-step at each split, chunking,
 schedule (one column group per workgroup, persistent workgroups, or both
 passes fused per XCD) and pass-2 row order.  The fastest challenger is promoted
@@ -142,6 +143,10 @@ def candidates(n: int, b: int, direction: str, space):
                 params = {"elems": e} if stg == 0 else {"elems": e, "stagger": stg}
                 out.append((f"lds_e{e}" + (f"_s{stg}" if stg else ""), "fft_lds_fused" + sfx, 256, params,
                             ("lds-resident", "stockham-radix16", "lds-stockham-single-pass")))
+    if 2 <= n <= space.dense_max_n:
+        # the dense-dot matrix-core flow (the reference's M2 dense-dot FFT64)
+        name = ("fft_dit_matrix" if direction == "dit" else "fft_dif_matrix") + sfx
+        out.append(("dense_mfma", name, 256, {}, ("matrix-resident", "dense-dot-fft64", "local-fused-tile")))
     if space.fourstep_min_n <= n <= (1 << 20):
         for n1 in space.fourstep_n1:
             n2 = n // n1
