@@ -80,6 +80,8 @@ def main() -> int:
     ap.add_argument("--sizes", default="", help="comma-separated subset of N (profiling runs)")
     ap.add_argument("--no-real", action="store_true", help="skip the R2C / C2R throughput leg")
     ap.add_argument("--no-config5", action="store_true", help="skip the config-5 selector-vs-M0 sweep")
+    ap.add_argument("--runner", default="", help="run every size through this runner name (e.g. "
+                    "fft_dit_matrix_batch) instead of the selected plan: profiling runs of one flow")
     ap.add_argument("--detail-out", default="", help="also write the JSON line, indented, to this file")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -133,7 +135,12 @@ def main() -> int:
     for n in sizes:
         b = batch_for(n)
         x = torch.randn((b, n), dtype=torch.complex64, device=dev, generator=gen) * math.sqrt(2.0)
-        plan = pkg.plan_fft("dit", n, batch=b, profile_hash=prof)
+        if args.runner:
+            plan = pkg.ExecutionPlan(n=n, batch=b, direction="dit", precision="fp32", selection_source="table",
+                                     reason="bench.py --runner", fallback=False, executed=args.runner, block=256,
+                                     flow_id="bench", flow_realization="bench", processing_unit="bench", params={})
+        else:
+            plan = pkg.plan_fft("dit", n, batch=b, profile_hash=prof)
         work.append((n, b, x, plan))
         log(f"size N={n} B={b} executed={plan.executed} fallback={plan.fallback}")
     torch.cuda.synchronize()
@@ -217,6 +224,8 @@ def main() -> int:
                              f"(n{'12'[j % 2]}={nplan.info.n1 if j % 2 == 0 else nplan.info.n2})")
             elif flow == "lds-fused":
                 names.append("lds_fft_kernel")
+            elif flow == "dense-mfma":
+                names.append("mfma_fft_kernel")
             else:
                 names.append(f"{flow} stage {j + 1}")
         flows.append((names, per_launch, rows))
@@ -509,6 +518,7 @@ def main() -> int:
                                "N=2^10..2^20, B=max(64, 2^25/N) per N (256 MiB in + 256 MiB out "
                                "per N, 512 MiB each way at 2^20); one step = all 11 sizes",
                    "frac_hbm_of_value": round(value / PEAK_GBPS, 4),
+                   "runner_forced": args.runner or None,
                    "d2d_copy_gbps": round(copy_gbps, 1),
                    "frac_of_d2d_copy": round(value / copy_gbps, 4)},
         "roofline": roofline,

@@ -19,6 +19,9 @@ Writes
 ``stats``: kernel durations per launch shape (kernel, grid) from the
 kernel_trace.csv of ``rocprofv3 --kernel-trace``, as Markdown.
 
+``counters``: matrix-core use per launch shape (MFMA busy fraction and fp32
+MFMA TFLOP/s) from ``rocprofv3 --pmc`` runs of the MFMA counters.
+
 Usage:
     python kunlunxin-fft_amd/pmc_summary.py traffic --fetch DIR --write DIR --detail bench_detail.json \
         --json profiles/pmc_traffic.json --md profiles/<name>.md [--sq DIR] [--trace DIR] [--command TEXT]
@@ -82,8 +85,12 @@ def bench_keys(name: str, grid: int, sizes) -> list:
     points.  Persistent kernels are not matched: their grid is the resident
     wave, not the work."""
     t = _template_args(name)
-    if t is None or not name.startswith(("fourstep_pass_kernel", "lds_fft_kernel")):
+    if t is None or not name.startswith(("fourstep_pass_kernel", "lds_fft_kernel", "mfma_fft_kernel")):
         return []
+    if name.startswith("mfma_fft_kernel"):
+        # 16 points per thread at every length (4096 or L points per block)
+        return [f"mfma_fft_kernel|N={s['n']}|rows={s['batch']}" for s in sizes
+                if s["flow"] == "dense-mfma" and s["n"] == (1 << t[0]) and grid * 16 == s["n"] * s["batch"]]
     logl, loge = t[0], t[1]
     points = grid << loge
     keys = []
@@ -124,12 +131,43 @@ def real_keys(name: str, grid: int, real_sizes) -> list:
             if (rows * core == (grid << loge) and (n1 if kind == 0 else n2) == (1 << logl)
                     and t[3] == (-1 if tt == "r2c" else 1)):
                 keys.append(f"{tt} pass {kind + 1}|N={n}|rows={rows}")
-        elif name.startswith(("r2c_stitch_kernel", "c2r_pre_kernel")) and s["flow"] == "four-step":
+        elif name.startswith(("r2c_stitch_kernel", "c2r_pre_kernel")) and s["flow"] != "lds-fused":
+            # around a non-fused core: once per execute, or once per chunk of
+            # a chunked four-step core
             want = "r2c" if name.startswith("r2c") else "c2r"
             bpr = ((core >> 1) + 1 + 255) // 256
-            if tt == want and grid == bpr * b * 256:
-                keys.append(f"{tt} {name}|N={n}|rows={b}")
+            rows = s["split"][2] if s.get("split") else b
+            for r in sorted({b, rows}):
+                if tt == want and grid == bpr * r * 256:
+                    keys.append(f"{tt} {name}|N={n}|rows={r}")
     return keys
+
+
+def real_alg_bytes(n: int) -> int:
+    """Algorithmic bytes of one real-transform row: n float32 one way, n/2+1
+    complex64 the other."""
+    return 4 * n + 8 * (n // 2 + 1)
+
+
+def execute_rows(traffic: dict, sizes, real_sizes) -> list:
+    """Per size: HBM bytes of all launches of one execute (every launch key
+    that size owns, times the launches of that key per execute = batch / rows
+    per launch), against the transform's algorithmic bytes."""
+    out = []
+    for rows_list, alg_row, key_of in (
+            (sizes, lambda n: 16 * n, lambda k, s: not k.startswith(("r2c ", "c2r "))),
+            (real_sizes, real_alg_bytes, lambda k, s: k.startswith(s["transform"] + " "))):
+        for s in rows_list:
+            n, b = s["n"], s["batch"]
+            mine = [k for k in traffic if f"|N={n}|rows=" in k and key_of(k, s)]
+            if not mine:
+                continue
+            total = sum(traffic[k] * (b // int(k.rsplit("=", 1)[1])) for k in mine)
+            alg = alg_row(n) * b
+            out.append({"transform": s.get("transform", "c2c"), "n": n, "batch": b, "flow": s["flow"],
+                        "launch_keys": sorted(k.split("|", 1)[0] for k in mine),
+                        "hbm_bytes": total, "algorithmic_bytes": alg, "ratio": round(total / alg, 3)})
+    return out
 
 
 SQ_COUNTERS = ("SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_INSTS_LDS", "SQ_INSTS_VALU")
@@ -204,6 +242,61 @@ def stats(args) -> int:
     return 0
 
 
+def agent_facts(d: str) -> dict:
+    """SIMD and XCD counts of the GPU agent, from run_agent_info.csv."""
+    files = glob.glob(os.path.join(d, "**", "*agent_info.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no *agent_info.csv under {d}")
+    with open(files[0], newline="") as f:
+        for r in csv.DictReader(f):
+            if r.get("Agent_Type") == "GPU":
+                return {"simd": int(r["Simd_Count"]), "xcc": int(r["Num_Xcc"]), "cu": int(r["Cu_Count"])}
+    raise SystemExit(f"no GPU agent in {files[0]}")
+
+
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_F32", "SQ_INSTS_MFMA", "SQ_BUSY_CU_CYCLES",
+                 "GRBM_GUI_ACTIVE")
+
+
+def counters(args) -> int:
+    """Matrix-core use per launch shape: MfmaUtil = SQ_VALU_MFMA_BUSY_CYCLES /
+    (GRBM_GUI_ACTIVE of one XCD x SIMDs) (the rocprofv3 derived metric; the
+    CSV sums GRBM_GUI_ACTIVE over the XCDs), and fp32 MFMA TFLOP/s = 512 x
+    SQ_INSTS_VALU_MFMA_MOPS_F32 over the launch shape's average duration in a
+    kernel-trace run of the same command."""
+    with open(args.md, "w") as f:
+        f.write("# Matrix-core use per launch (rocprofv3 --pmc " + " ".join(MFMA_COUNTERS) + ")\n\n")
+        _commands(f, args.command)
+        f.write("MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x SIMDs), rocprofv3's MfmaUtil.  "
+                "fp32 MFMA TFLOP/s = 512 x SQ_INSTS_VALU_MFMA_MOPS_F32 / the average duration of the same launch "
+                "shape in the kernel-trace run, against 157.3 TFLOP/s (dense fp32 MFMA peak).\n\n")
+        for label, d, trace, detail in zip(args.label, args.dir, args.trace, args.detail):
+            fac = agent_facts(d)
+            vals = {c: per_kernel(d, c) for c in MFMA_COUNTERS}
+            durs = trace_durations(trace) if trace else {}
+            sizes = json.load(open(detail))["per_size"] if detail else []
+            f.write(f"## {label}\n\n| bench key | kernel | grid | MFMA busy | MFMA instructions | "
+                    "fp32 MFMA flop | avg us | fp32 MFMA TFLOP/s | % of 157.3 |\n|---|---|---:|---:|---:|---:|---:|---:|---:|\n")
+            for (name, grid) in sorted(vals["GRBM_GUI_ACTIVE"]):
+                keys = bench_keys(name, grid, sizes)
+                if not keys:
+                    continue
+                busy = vals["SQ_VALU_MFMA_BUSY_CYCLES"].get((name, grid), 0.0)
+                gui = vals["GRBM_GUI_ACTIVE"][(name, grid)] / fac["xcc"]
+                util = busy / (gui * fac["simd"]) if gui else 0.0
+                flop = 512.0 * vals["SQ_INSTS_VALU_MFMA_MOPS_F32"].get((name, grid), 0.0)
+                v = durs.get((name, grid))
+                us = sum(v) / len(v) / 1e3 if v else float("nan")
+                tf = flop / (us * 1e-6) / 1e12 if v else float("nan")
+                for key in keys:
+                    f.write(f"| {key.replace('|', chr(92) + '|')} | {name} | {grid} | {util:.1%} | "
+                            f"{vals['SQ_INSTS_MFMA'].get((name, grid), 0.0):.0f} | {flop:.3g} | {us:.2f} | "
+                            f"{tf:.1f} | {tf / 157.3:.1%} |\n")
+            f.write("\n")
+    print(f"wrote {args.md}")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -222,9 +315,18 @@ def main() -> int:
     st.add_argument("--detail", default="", help="bench_detail.json of the same command (labels the rows)")
     st.add_argument("--top", type=int, default=40, help="launch shapes listed")
     st.add_argument("--command", default="")
+    c = sub.add_parser("counters")
+    c.add_argument("--dir", action="append", required=True, help="output dir of a --pmc run of MFMA_COUNTERS")
+    c.add_argument("--trace", action="append", required=True, help="kernel-trace dir of the same command")
+    c.add_argument("--detail", action="append", required=True, help="bench_detail.json of the same command")
+    c.add_argument("--label", action="append", required=True, help="section title per --dir")
+    c.add_argument("--md", required=True)
+    c.add_argument("--command", default="")
     args = ap.parse_args()
     if args.cmd == "stats":
         return stats(args)
+    if args.cmd == "counters":
+        return counters(args)
 
     fetch = per_kernel(args.fetch, "FETCH_SIZE")
     write = per_kernel(args.write, "WRITE_SIZE")
@@ -233,21 +335,27 @@ def main() -> int:
     durs = trace_durations(args.trace) if args.trace else {}
     sizes = json.load(open(args.detail))["per_size"]
 
+    detail = json.load(open(args.detail))
+    real_sizes = detail.get("real_per_size", [])
     rows_out, traffic = [], {}
     for (name, grid) in sorted(set(fetch) | set(write)):
-        keys = bench_keys(name, grid, sizes)
-        if not keys:
-            continue
-        points = grid << _template_args(name)[1]
         fb = fetch.get((name, grid), float("nan")) * 1024 / f_cal
         wb = write.get((name, grid), float("nan")) * 1024 / w_cal
-        alg = 16 * points
-        for key in keys:
+        for key in bench_keys(name, grid, sizes):
             traffic[key] = round(fb + wb)
-            rows_out.append((key, name, grid, alg, fb, wb))
+            ept = 16 if name.startswith("mfma_fft_kernel") else 1 << _template_args(name)[1]
+            rows_out.append((key, name, grid, 16 * grid * ept, fb, wb))
+        for key in real_keys(name, grid, real_sizes):
+            # a real-transform launch: bytes it moves per its rows' algorithmic bytes
+            rows = int(key.rsplit("=", 1)[1])
+            n = int(key.split("|N=")[1].split("|")[0])
+            traffic[key] = round(fb + wb)
+            rows_out.append((key, name, grid, real_alg_bytes(n) * rows, fb, wb))
+    executes = execute_rows(traffic, sizes, real_sizes)
 
     with open(args.json, "w") as f:
-        json.dump(traffic, f, indent=1, sort_keys=True)
+        json.dump(dict(traffic, **{f"execute {e['transform']}|N={e['n']}|B={e['batch']}": e["hbm_bytes"]
+                                   for e in executes}), f, indent=1, sort_keys=True)
     with open(args.md, "w") as f:
         f.write("# HBM traffic per launch (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE)\n\n")
         _commands(f, args.command)
@@ -283,6 +391,16 @@ def main() -> int:
                     extra += " - | - | - |"
             f.write(f"| {key.replace('|', chr(92) + '|')} | {name} | {grid} | {alg / 2**20:.1f} | {fb / 2**20:.1f} | {wb / 2**20:.1f} | "
                     f"{(fb + wb) / alg:.3f} |{extra}\n")
+        if executes:
+            f.write("\n## Per execute: every launch of one transform call\n\n"
+                    "HBM bytes of all launches of one execute (each launch key times its launches per execute) "
+                    "over the transform's algorithmic bytes (C2C: 16 N per row; R2C / C2R: 4 N + 8 (N/2 + 1) "
+                    "per row).  A ratio of 2 means the data makes two HBM round trips.\n\n")
+            f.write("| transform | N | B | flow | launches (kinds) | algorithmic MiB | HBM MiB | HBM / algorithmic |\n")
+            f.write("|---|---:|---:|---|---|---:|---:|---:|\n")
+            for e in executes:
+                f.write(f"| {e['transform']} | {e['n']} | {e['batch']} | {e['flow']} | {', '.join(e['launch_keys'])} | "
+                        f"{e['algorithmic_bytes'] / 2**20:.1f} | {e['hbm_bytes'] / 2**20:.1f} | {e['ratio']:.3f} |\n")
     print(f"wrote {args.json} ({len(traffic)} kernels) and {args.md}")
     return 0
 

@@ -105,3 +105,28 @@ def test_stats_labels_real_transform_launches(tmp_path):
     assert "| r2c N=1024\\|rows=32768 |" in text
     assert "| r2c N=65536\\|rows=512 |" in text
     assert text.count("r2c N=65536") == 2  # pass 1 and the stitch
+
+
+def test_execute_rows_sum_every_launch_of_one_execute():
+    """Per-execute traffic: each launch key counts batch / rows-per-launch
+    times, against 16 N (C2C) or 4 N + 8 (N/2+1) (real) bytes per row."""
+    from kunlunxin_fft_amd.pmc_summary import execute_rows, real_alg_bytes
+
+    n, b = 1 << 20, 64
+    one = 16 * n * 32  # one 32-row chunk launch moving its rows once
+    traffic = {
+        f"fourstep_pass_kernel pass 1 (n1=1024)|N={n}|rows=32": one,
+        f"fourstep_pass_kernel pass 2 (n2=1024)|N={n}|rows=32": one,
+        f"lds_fft_kernel|N=1024|rows=32768": 16 * 1024 * 32768,
+        f"r2c pass 1|N={n}|rows=32": 8 * (n // 2) * 2 * 32,
+        f"r2c pass 2|N={n}|rows=32": 8 * (n // 2) * 2 * 32,
+        f"r2c r2c_stitch_kernel|N={n}|rows=32": real_alg_bytes(n) * 32 // 2 * 3,
+    }
+    sizes = [{"n": n, "batch": b, "flow": "four-step"}, {"n": 1024, "batch": 32768, "flow": "lds-fused"}]
+    real = [{"n": n, "batch": b, "flow": "four-step", "transform": "r2c"}]
+    rows = {(e["transform"], e["n"]): e for e in execute_rows(traffic, sizes, real)}
+    assert rows[("c2c", n)]["ratio"] == 2.0 and rows[("c2c", n)]["hbm_bytes"] == 4 * one
+    assert rows[("c2c", 1024)]["ratio"] == 1.0
+    r = rows[("r2c", n)]
+    assert r["launch_keys"] == ["r2c pass 1", "r2c pass 2", "r2c r2c_stitch_kernel"]
+    assert r["hbm_bytes"] == 2 * (2 * 8 * (n // 2) * 2 * 32 + real_alg_bytes(n) * 32 // 2 * 3)
