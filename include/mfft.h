@@ -204,6 +204,25 @@ int mfft_execute_ws(const mfft_plan* plan, const void* in, void* out, void* work
 int mfft_execute_timed(const mfft_plan* plan, const void* in, void* out, void* workspace,
                        int64_t workspace_bytes, void* stream, float* launch_ms, int cap, int* n_launches);
 
+/* Allocation-free execute.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory at execute time (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same work and results as mfft_execute / mfft_execute_ws, but the scratch
+ * of a plan that needs one (mfft_plan_workspace_size > 0: the stage flows
+ * and the real flows around a non-fused core) comes from a static device
+ * buffer of MFFT_NOALLOC_SCRATCH_BYTES that the library holds on every
+ * device it runs on until the process ends; the call itself allocates
+ * nothing (no hipMalloc, no allocating library routine).  A plan needing
+ * more scratch than that is refused with MFFT_ERR_VALUE before any launch.
+ * Every call on one device shares that device's buffer: calls that overlap
+ * in time on one device (two streams, two host threads) race, so serialise
+ * them.  The buffer keeps whatever the last call left in it; no kernel
+ * reads scratch it has not written in the same call, so nothing needs
+ * clearing.  The first call on a device looks the buffer's address up once
+ * (with that device current, as every execute requires). */
+#define MFFT_NOALLOC_SCRATCH_BYTES ((int64_t)32 << 20)
+int mfft_execute_noalloc(const mfft_plan* plan, const void* in, void* out, void* stream);
+
 /* Release the plan's device memory.  NULL is a no-op.  It does not
  * synchronise the device: the caller makes sure that no execute of the plan
  * is still pending on any stream (synchronise the streams it ran on, or the

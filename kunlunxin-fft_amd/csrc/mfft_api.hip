@@ -23,6 +23,12 @@ namespace mfft {
 thread_local LaunchTimer* g_timer = nullptr;
 }
 
+// Scratch of mfft_execute_noalloc: one copy per device, held until the
+// process ends.  Host code never uses this name as an address (on the host
+// it is a stand-in, not device memory); it uses the per-device address that
+// hipGetSymbolAddress returns (noalloc_scratch below).
+static __device__ __align__(256) unsigned char scratch[MFFT_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local std::string g_err;
@@ -141,6 +147,25 @@ void release(mfft_plan* p) {
     }
     if (p->sync) (void)hipFree(p->sync);
     p->sync = nullptr;
+}
+
+// Device address of `scratch` on device `dev` (current), looked up on the
+// first call for that device and kept.
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+int noalloc_scratch(int dev, void** out) {
+    if (dev < 0 || dev >= kMaxDevices) return fail(MFFT_ERR_RUNTIME, "device %d beyond %d devices", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(static scratch)");
+        if (!ptr) return fail(MFFT_ERR_RUNTIME, "hipGetSymbolAddress(static scratch) returned NULL");
+        g_scratch[dev] = ptr;
+    }
+    *out = g_scratch[dev];
+    return MFFT_OK;
 }
 
 bool is_stage_flow(int f) {
@@ -594,6 +619,29 @@ int mfft_execute_ws(const mfft_plan* p, const void* in, void* out, void* workspa
     return execute_impl(p, in, out,
                         Work{p->need_a ? (float2*)w : nullptr, p->need_b ? (float2*)(w + p->work_b_off) : nullptr},
                         stream_v, workspace, p->work_bytes);
+}
+
+int mfft_execute_noalloc(const mfft_plan* p, const void* in, void* out, void* stream_v) {
+    g_err.clear();
+    if (!p) return fail(MFFT_ERR_VALUE, "plan must not be NULL");
+    if (p->work_bytes > MFFT_NOALLOC_SCRATCH_BYTES)
+        return fail(MFFT_ERR_VALUE,
+                    "this plan needs %lld bytes of scratch, more than the %lld-byte static buffer of "
+                    "mfft_execute_noalloc: use mfft_execute or mfft_execute_ws",
+                    (long long)p->work_bytes, (long long)MFFT_NOALLOC_SCRATCH_BYTES);
+    if (p->work_bytes == 0) return execute_impl(p, in, out, Work{nullptr, nullptr}, stream_v);
+    int dev = -1;
+    const hipError_t he = hipGetDevice(&dev);
+    if (he != hipSuccess) return hip_fail(he, "hipGetDevice");
+    if (dev != p->device)
+        return fail(MFFT_ERR_RUNTIME, "plan was created on device %d but device %d is current", p->device, dev);
+    void* ws = nullptr;
+    const int rc = noalloc_scratch(dev, &ws);
+    if (rc != MFFT_OK) return rc;
+    char* w = (char*)ws;
+    return execute_impl(p, in, out,
+                        Work{p->need_a ? (float2*)w : nullptr, p->need_b ? (float2*)(w + p->work_b_off) : nullptr},
+                        stream_v, ws, p->work_bytes);
 }
 
 int mfft_execute_timed(const mfft_plan* p, const void* in, void* out, void* workspace, int64_t workspace_bytes,

@@ -39,7 +39,7 @@ EXPORTS = (
     "mfft_plan_create", "mfft_execute", "mfft_execute_timed", "mfft_plan_destroy", "mfft_plan_query",
     "mfft_bit_reverse_permute", "mfft_device_props_get", "mfft_last_error",
     "mfft_abi_version", "mfft_plan_sync_overruns", "mfft_plan_create_ex", "mfft_plan_workspace_size",
-    "mfft_execute_ws",
+    "mfft_execute_ws", "mfft_execute_noalloc",
 )
 PLAN_CALLER_WORKSPACE = 1
 
@@ -104,6 +104,8 @@ def load() -> ctypes.CDLL:
         lib.mfft_plan_workspace_size.restype = i32
         lib.mfft_execute_ws.argtypes = [vp, vp, vp, vp, i64, vp]
         lib.mfft_execute_ws.restype = i32
+        lib.mfft_execute_noalloc.argtypes = [vp, vp, vp, vp]
+        lib.mfft_execute_noalloc.restype = i32
         lib.mfft_execute_timed.argtypes = [vp, vp, vp, vp, i64, vp, ctypes.POINTER(ctypes.c_float), i32,
                                            ctypes.POINTER(i32)]
         lib.mfft_execute_timed.restype = i32
@@ -172,6 +174,11 @@ class NativePlan:
         rc = _lib.mfft_execute(self._h, in_ptr, out_ptr, stream_ptr)
         if rc:
             check(rc)
+
+    def execute_noalloc(self, in_ptr: int, out_ptr: int, stream_ptr: int) -> None:
+        """Execute with the library's static scratch (mfft_execute_noalloc):
+        no allocation; calls that overlap on one device race."""
+        check(_lib.mfft_execute_noalloc(self._h, in_ptr, out_ptr, stream_ptr))
 
     def workspace_size(self) -> int:
         """Bytes of workspace an execute of this plan needs (0: none)."""
