@@ -111,13 +111,17 @@ enum {
  *                                    the XCD whose L2 holds its pass-1 output
  *                                    (n1, n2 in [128, 512] within 2x; one
  *                                    execute of such a plan at a time: its
- *                                    counters live in the plan; switched off
- *                                    in this build: plan creation returns
- *                                    MFFT_ERR_UNSUPPORTED),
- *                        params[3] = pass-2 row order: 0 = forward; 1 =
- *                                    reverse, so the batch rows pass 1 wrote
- *                                    last (the most likely still in the
- *                                    MALL) are read first (schedules 0, 1) */
+ *                                    counters live in the plan),
+ *                        params[3] = schedules 0, 1: pass-2 row order: 0 =
+ *                                    forward; 1 = reverse, so the batch rows
+ *                                    pass 1 wrote last (the most likely still
+ *                                    in the MALL) are read first; schedule 2:
+ *                                    bits 0-7 = queue lag, 1..64 transforms
+ *                                    that pass 1 runs ahead of pass 2 on an
+ *                                    XCD (0 = one more than the XCD's resident
+ *                                    blocks hold in flight), bits 8-15 = queue
+ *                                    items a workgroup takes per dequeue,
+ *                                    1..64 (0 = 2) */
 #define MFFT_MAX_PARAMS 4
 
 typedef struct mfft_plan mfft_plan;

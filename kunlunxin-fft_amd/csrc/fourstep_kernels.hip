@@ -453,12 +453,13 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG), 4) void fourstep_pe
 // also stops after `total + 1` trips: a block dequeues at most `total` items.
 // sync (int32, zeroed before the launch): [0, kFusedSlots) next item per
 // slot, [kFusedOverrun] overruns, [kFusedHead, kFusedHead + rows) pass-1
-// groups done per transform.
+// groups done per transform.  `lag` (>= 1) sets how many transforms pass 1
+// runs ahead of pass 2 in a queue.
 template <int LL1, int LE1, int LC1, int LL2, int LE2, int LC2, int DIR>
 __global__ __launch_bounds__((ColCfg<LL1, LE1, LC1>::WG)) void fourstep_fused_kernel(
     const float2* src, float2* dst, const float2* __restrict__ tw1, const float2* __restrict__ tw2,
     const float2* __restrict__ tw_lo, const float2* __restrict__ tw_hi, int tw_h, float scale, int rows,
-    int nslot, int* sync, long long wait_ticks) {
+    int nslot, int lag, int per_take, int* sync, long long wait_ticks) {
     using A = ColCfg<LL1, LE1, LC1>;
     using B = ColCfg<LL2, LE2, LC2>;
     static_assert(A::WG == B::WG, "both passes run with the same block size");
@@ -475,24 +476,40 @@ __global__ __launch_bounds__((ColCfg<LL1, LE1, LC1>::WG)) void fourstep_fused_ke
     const int slot = __builtin_amdgcn_readfirstlane(xcc % nslot);
     const int nt = rows > slot ? (rows - slot + nslot - 1) / nslot : 0;  // this slot's transforms
     const int total = nt * (G1 + G2);
+    const int D = lag < nt ? lag : nt;  // pass 1 runs D transforms ahead of pass 2
     int* done = sync + kFusedHead;
     const bool lead = __builtin_amdgcn_readfirstlane(tid) < 64;  // wave 0
     const int one = tid == 0 ? 1 : 0;
     for (int trip = 0; trip <= total; ++trip) {
-        if (lead) item_s = __builtin_amdgcn_readfirstlane(atomicAdd(sync + slot, one));
+        // take `per_take` consecutive items with one atomic (every block
+        // hitting one counter per item serialises on that L2 address)
+        if (lead) item_s = __builtin_amdgcn_readfirstlane(atomicAdd(sync + slot, one * per_take));
         __syncthreads();
-        const int it = __builtin_amdgcn_readfirstlane(item_s);
+        const int it0 = __builtin_amdgcn_readfirstlane(item_s);
         __syncthreads();  // every thread has read item_s before it is written again
-        if (it >= total) break;
-        // queue order: P1(0) | P1(1) P2(0) | P1(2) P2(1) | ... | P2(nt-1)
+        if (it0 >= total) break;
+        const int it_end = it0 + per_take < total ? it0 + per_take : total;
+        // items of a take run in queue order: an item only waits for items
+        // earlier in the queue, so the earliest unfinished item never waits
+        for (int it = it0; it < it_end; ++it) {
+        // queue order, D = lag: P1(0) .. P1(D-1) | P1(D) P2(0) | P1(D+1) P2(1) |
+        // ... | P2(nt-D) .. P2(nt-1): pass 2 of transform k is handed out
+        // after pass 1 of k + D - 1, so the blocks resident on the XCD are
+        // rarely still writing the Z that a pass-2 group waits for
         int k, g;
         bool second;
-        if (it < G1) {
-            k = 0, g = it, second = false;
+        if (it < D * G1) {
+            k = it / G1, g = it - k * G1, second = false;
         } else {
-            const int u = it - G1, blk = u / (G1 + G2), r = u - blk * (G1 + G2);
-            if (blk < nt - 1 && r < G1) k = blk + 1, g = r, second = false;
-            else k = blk, g = blk < nt - 1 ? r - G1 : r, second = true;
+            const int u = it - D * G1, mid = (nt - D) * (G1 + G2);
+            if (u < mid) {
+                const int blk = u / (G1 + G2), r = u - blk * (G1 + G2);
+                if (r < G1) k = D + blk, g = r, second = false;
+                else k = blk, g = r - G1, second = true;
+            } else {
+                const int w = u - mid;
+                k = nt - D + w / G2, g = w - (w / G2) * G2, second = true;
+            }
         }
         const int t = slot + nslot * k;
         const int64_t base = (int64_t)t << LOGN;
@@ -537,6 +554,7 @@ __global__ __launch_bounds__((ColCfg<LL1, LE1, LC1>::WG)) void fourstep_fused_ke
             col_passes<B, DIR, 1, true>(v, lds, tw2, c, j, [&] { return BigTw<B>{}; });
             // a group whose wait gave up writes NaN, not a transform of partial data
             col_store<B, 1>(v, dst + base + c0, lds, tl, c, j, LL1, failed ? __builtin_nanf("") : scale);
+        }
         }
     }
 }
@@ -643,8 +661,16 @@ hipError_t launch_fused_one(const float2* src, float2* dst, const mfft_plan* p, 
     // the XCDs round-robin, so every XCD, and every queue, gets blocks)
     const int nx = p->num_xcc;
     const int grid = ((per_cu * p->num_cus) / nx) * nx > 0 ? ((per_cu * p->num_cus) / nx) * nx : nx;
+    // default lag: one transform more than the blocks of one XCD can hold
+    // in flight at once (each transform is G1 + G2 queue items)
+    constexpr int ITEMS = ((1 << L2) >> C1) + ((1 << L1) >> C2);
+    const int lag = p->fused_lag > 0 ? p->fused_lag : (grid / nx + ITEMS - 1) / ITEMS + 1;
+    // two items per dequeue: measured fastest at 2^14..2^18 (one per dequeue
+    // serialises every block on the queue counter; four or more unbalance
+    // the blocks' shares)
+    const int per_take = p->fused_take > 0 ? p->fused_take : 2;
     fourstep_fused_kernel<L1, E1, C1, L2, E2, C2, DIR><<<grid, A::WG, 0, stream>>>(
-        src, dst, p->tw_n1, p->tw_n2, p->tw_lo, p->tw_hi, p->tw_h, scale, (int)rows, nx, p->sync,
+        src, dst, p->tw_n1, p->tw_n2, p->tw_lo, p->tw_hi, p->tw_h, scale, (int)rows, nx, lag, per_take, p->sync,
         (long long)kFusedWaitMs * p->clock_khz);
     mark(stream);
     return hipGetLastError();

@@ -368,7 +368,7 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
         flow = mfft::lds_supported(logc, 0, lds_mode) ? MFFT_FLOW_LDS_FUSED : MFFT_FLOW_FOUR_STEP;
     int block = 256, elems = 0, stagger = 0;
     int64_t n1 = 0, n2 = 0, chunk = 0;
-    int schedule = 0, pass2_rev = 0;
+    int schedule = 0, pass2_rev = 0, fused_lag = 0, fused_take = 0;
     switch (flow) {
         case MFFT_FLOW_RADIX2_DIT:
         case MFFT_FLOW_RADIX2_DIF:
@@ -419,9 +419,18 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
             if (prm[2] < 0 || prm[2] > 2)
                 return fail(MFFT_ERR_VALUE, "FOUR_STEP schedule must be 0, 1 or 2, got %d", prm[2]);
             schedule = prm[2];
-            if (prm[3] < 0 || prm[3] > 1)
+            if (schedule != 2 && (prm[3] < 0 || prm[3] > 1))
                 return fail(MFFT_ERR_VALUE, "FOUR_STEP pass-2 row order must be 0 or 1, got %d", prm[3]);
-            pass2_rev = prm[3];
+            if (schedule == 2 && (prm[3] & 0xff) > 64)
+                return fail(MFFT_ERR_VALUE, "FOUR_STEP fused queue lag (params[3] bits 0-7) must be in [0, 64], got %d",
+                            prm[3] & 0xff);
+            if (schedule == 2 && (prm[3] >> 8) > 64)
+                return fail(MFFT_ERR_VALUE,
+                            "FOUR_STEP fused items per dequeue (params[3] bits 8-15) must be in [0, 64], got %d",
+                            prm[3] >> 8);
+            pass2_rev = schedule == 2 ? 0 : prm[3];
+            fused_lag = schedule == 2 ? (prm[3] & 0xff) : 0;
+            fused_take = schedule == 2 ? (prm[3] >> 8) : 0;
             if (schedule == 2 && !mfft::fourstep_fused_supported(l1, l2))
                 return fail(MFFT_ERR_UNSUPPORTED,
                             "the fused FOUR_STEP schedule needs n1, n2 in [128, 512] within a factor 2 "
@@ -480,6 +489,8 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
     p->chunk_rows = chunk;
     p->schedule = schedule;
     p->pass2_rev = pass2_rev;
+    p->fused_lag = fused_lag;
+    p->fused_take = fused_take;
     p->num_cus = num_cus > 0 ? num_cus : 1;
     p->clock_khz = clock_khz > 0 ? clock_khz : 100000;
     p->num_xcc = num_xcc > 0 ? num_xcc : 1;

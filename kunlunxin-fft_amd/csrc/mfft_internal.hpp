@@ -21,7 +21,9 @@ struct mfft_plan {
     int launches = 0;
     int64_t n1 = 0, n2 = 0, chunk_rows = 0;
     int schedule = 0;    // FOUR_STEP: 0 one column group per block, 1 persistent, 2 fused (one launch)
-    int pass2_rev = 0;   // FOUR_STEP: pass 2 walks the batch rows in reverse order
+    int pass2_rev = 0;   // FOUR_STEP: pass 2 walks the batch rows in reverse order (schedules 0, 1)
+    int fused_lag = 0;   // FOUR_STEP schedule 2: transforms pass 1 runs ahead of pass 2 (0 = from occupancy)
+    int fused_take = 0;  // FOUR_STEP schedule 2: queue items a block takes per dequeue (0 = default)
     int num_cus = 0;     // compute units of `device` (persistent / fused grid size)
     int clock_khz = 0;   // constant wall-clock rate of `device` (fused schedule wait bound)
     int num_xcc = 8;     // XCDs of `device` (fused schedule work queues)
@@ -107,7 +109,7 @@ bool fourstep_supported(int log2n1, int log2n2);
 bool fourstep_fused_supported(int log2n1, int log2n2);  // schedule 2: n1, n2 in [128, 512], within 2x
 constexpr int kMaxStagger = 16;  // LDS_FUSED start stagger limit (16 x 8128 clocks)
 constexpr int kFusedWaitMs = 20;  // longest pass-2 wait of the fused schedule before it gives up
-constexpr bool kFusedScheduleEnabled = false;  // switched off until its bounded loop has run on the GPU
+constexpr bool kFusedScheduleEnabled = true;
 // fused-schedule counters: [0, kFusedSlots) work queues (one per XCD),
 // [kFusedOverrun] wait overruns, then one per transform of a launch
 constexpr int kFusedSlots = 16;

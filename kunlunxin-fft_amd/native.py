@@ -227,7 +227,7 @@ class NativePlan:
         # The handle waits in a list that release_retired() empties at a
         # point the owner chooses (after synchronising the device).
         h, self._h = getattr(self, "_h", None), None
-        if h is not None:
+        if h is not None and _RETIRED is not None:  # None at interpreter shutdown
             _RETIRED.append((h, int(self.info.device) if hasattr(self, "info") else 0))
 
 

@@ -241,12 +241,6 @@ FUSED_SPLITS = [(1 << 14, 128), (1 << 15, 128), (1 << 15, 256), (1 << 16, 256), 
                 (1 << 17, 512), (1 << 18, 512)]
 
 
-FUSED_OFF = ("the fused four-step schedule is switched off: its first GPU launch (N=2^14, B=1) did not "
-             "finish twice (its loop compiled into an inner barrier loop only thread 0 could leave); the "
-             "fixed loop has not run on the GPU yet, and plan creation rejects schedule 2")
-
-
-@pytest.mark.skip(reason=FUSED_OFF)
 @pytest.mark.parametrize("n,n1", FUSED_SPLITS)
 @pytest.mark.parametrize("b,chunk", [(1, 0), (5, 0), (13, 0), (19, 4), (64, 0)])
 def test_four_step_fused(gpu, n, n1, b, chunk):
@@ -270,19 +264,34 @@ def test_four_step_fused(gpu, n, n1, b, chunk):
     assert nplan.sync_overruns() == 0
 
 
+@pytest.mark.parametrize("lag,take", [(1, 1), (1, 8), (3, 2), (12, 4), (64, 64)])
+def test_four_step_fused_queue_settings(gpu, lag, take):
+    """The fused schedule's queue lag (params[3] bits 0-7) and items per
+    dequeue (bits 8-15) only reorder work: results are bitwise the same as
+    the default settings, including lags beyond the transforms of a slot."""
+    n, b = 1 << 16, 21
+    x = torch.from_numpy(seeded_c64(n, b, session=7)).to(gpu)
+    ref = execute_fft_plan(mkplan("fft_four_step_batch", n, b, params={"n1": 256, "schedule": 2}), x)
+    p = native.NativePlan(n, b, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 2, lag | (take << 8)))
+    y = torch.empty_like(x)
+    p.execute(x.data_ptr(), y.data_ptr(), torch.cuda.current_stream(gpu).cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref) and p.sync_overruns() == 0
+
+
 def test_four_step_schedules_agree(gpu):
     """All three schedules run the same butterflies and twiddles (only the
     compiler's instruction choices may differ): outputs agree to 1e-6."""
     n, b = 1 << 18, 40
     x = torch.from_numpy(seeded_c64(n, b, session=5)).to(gpu)
     y0 = execute_fft_plan(mkplan("fft_four_step_batch", n, b, params={"n1": 512}), x)
-    for sched in (1,):  # schedule 2 is switched off (FUSED_OFF)
+    for sched in (1, 2):
         y1 = execute_fft_plan(mkplan("fft_four_step_batch", n, b, params={"n1": 512, "schedule": sched}), x)
         d = (torch.linalg.vector_norm(y1 - y0) / torch.linalg.vector_norm(y0)).item()
         assert d <= 1e-6, f"schedule {sched} differs: rel L2 {d:.3e}"
 
 
-@pytest.mark.parametrize("sched", [1, pytest.param(2, marks=pytest.mark.skip(reason=FUSED_OFF))])
+@pytest.mark.parametrize("sched", [1, 2])
 def test_four_step_schedule_real(gpu, sched):
     n, b = 1 << 17, 6
     xr = seeded_f32(n, b)
@@ -294,16 +303,20 @@ def test_four_step_schedule_real(gpu, sched):
 
 
 def test_four_step_fused_range(gpu):
-    """The fused schedule takes n1, n2 in [128, 512] within a factor 2, and
-    is switched off in this build: plan creation rejects it (no launch)."""
+    """The fused schedule takes n1, n2 in [128, 512] within a factor 2; plan
+    creation rejects other splits (no launch)."""
     with pytest.raises(ValueError, match="fused"):
         native.NativePlan(1 << 20, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (1024, 0, 2))
     with pytest.raises(ValueError, match="fused"):
         native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (128, 0, 2))
-    with pytest.raises(ValueError, match="disabled"):
-        native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 2))
+    p = native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 2))
+    assert p.info.n1 == 256 and p.info.launches == 2 and p.sync_overruns() == 0
     with pytest.raises(ValueError, match="schedule"):
         native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 3))
+    with pytest.raises(ValueError, match="lag"):
+        native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 2, 65))
+    with pytest.raises(ValueError, match="dequeue"):
+        native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 2, 65 << 8))
 
 
 # ---------------------------------------------------------------- real flows
