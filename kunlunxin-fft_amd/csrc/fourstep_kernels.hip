@@ -292,9 +292,34 @@ __device__ __forceinline__ void col_passes(float2 (&v)[C::E], float2* lds, const
 // Stockham registers writes 512/C-byte runs and measured slower).  SPLIT
 // stages half the columns at a time.  d = Z + c0*N1.
 // KIND 1: X[k1 + N1*k2] from registers, in place; d = X + c0 (k1 = c0 + c).
-template <class C, int KIND>
+// Real transforms over the four-step core pair every index k of the core
+// with its mirror L - k.  On the (k1, k2) grid of pass 2 (k = k1 + N1 k2) the
+// mirror of (k1, k2) is (N1 - k1, N2 - 1 - k2), and of (0, k2) it is
+// (0, N2 - k2); on the (n1, n2) grid of pass 1 (n = n1 N2 + n2) the mirror of
+// (n1, n2) is (N1 - 1 - n1, N2 - n2), and of (n1, 0) it is (N1 - n1, 0).  The
+// columns pair up as (p, N - p) for p = 1 .. N/2 - 1, plus (0, N/2), both of
+// which are their own mirror columns.  A workgroup of 16 lane columns takes 8
+// pairs: lane column c < 8 holds member 0 of pair 8g + c, and c ^ 8 its
+// partner, so every mirror value is in the same workgroup.
+// Column (member c >> 3 of pair 8g + (c & 7)) of an N-column grid:
+__device__ __forceinline__ int pair_col(int g, int c, int n) {
+    const int p = 8 * g + (c & 7);
+    return c < 8 ? p : (p ? n - p : n >> 1);
+}
+// lane column that holds the mirror values of lane column c
+__device__ __forceinline__ int mirror_lane_col(int g, int c) { return (g == 0 && (c & 7) == 0) ? c : (c ^ 8); }
+// R2C: pass 1 stores Z with its k1 positions permuted so that position
+// 16g + c holds k1 = pair_col(g, c, N1): pass 2 then reads 8 mirror pairs
+// as one aligned 16-column run.  k1 stored at position `pos`:
+template <int N1>
+__device__ __forceinline__ int pair_k1(int pos) { return pair_col(pos >> 4, pos & 15, N1); }
+
+// MAP 0: column c of the group is column c0 + c (d = Z + c0 N1).  MAP 1 (R2C
+// pass 1): the same columns, each stored with its k1 permuted (pair_k1).
+// MAP 2 (C2R pass 1): lane column c is column pair_col(g, c, 2^log_s) (d = Z).
+template <class C, int KIND, int MAP = 0>
 __device__ __forceinline__ void col_store(const float2 (&v)[C::E], float2* d, float2* lds, int tid, int c, int j,
-                                          int log_s, float scale) {
+                                          int log_s, float scale, int g = 0) {
     if constexpr (KIND == 0) {
         constexpr int HALVES = C::SPLIT ? 2 : 1;
         constexpr int CH = C::C / HALVES;  // columns staged per round
@@ -315,7 +340,13 @@ __device__ __forceinline__ void col_store(const float2 (&v)[C::E], float2* d, fl
                 const int e = tid + r.value * C::WG;
                 const int cc = e >> C::LOG_L;
                 const int k1 = e & (C::L - 1);
-                *byte_off(dh + r.value * C::WG, (uint32_t)tid * 8u) = lds[cc * C::PITCH + pad(k1)];
+                if constexpr (MAP == 2) {
+                    const int col = pair_col(g, h.value * CH + cc, 1 << log_s);
+                    d[((int64_t)col << C::LOG_L) + k1] = lds[cc * C::PITCH + pad(k1)];
+                } else {
+                    *byte_off(dh + r.value * C::WG, (uint32_t)tid * 8u) =
+                        lds[cc * C::PITCH + pad(MAP == 1 ? pair_k1<C::L>(k1) : k1)];
+                }
             });
         });
     } else {
@@ -363,6 +394,180 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_pass_
     });
     col_store<C, KIND>(v, KIND == 0 ? dst + base + ((int64_t)c0 << LOGL) : dst + base + c0, lds, tid, c, j,
                        log_s, scale);
+}
+
+// R2C pass 1: the column pass of the half-length core (forward), with Z
+// stored in the pair-permuted k1 order (MAP 1) for the stitching pass 2.
+template <int LOGL, int LOGE, int LOGC>
+__global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_r2c_pass1_kernel(
+    const float2* src, float2* dst, const float2* __restrict__ tw, const float2* __restrict__ tw_lo,
+    const float2* __restrict__ tw_hi, int tw_h, int logn, int log_s) {
+    using C = ColCfg<LOGL, LOGE, LOGC>;
+    __shared__ float2 lds[C::LDS_FLOAT2];
+    const int groups = (1 << log_s) >> LOGC;
+    const int bid = xcd_pair_block((int)blockIdx.x, (int)gridDim.x);
+    const int64_t row = bid / groups;
+    const int c0 = (bid - (int)(row * groups)) << LOGC;
+    const int tid = threadIdx.x;
+    const int c = tid & (C::C - 1);
+    const int j = tid >> LOGC;
+    const int64_t base = row << logn;
+    float2 v[C::E];
+    col_load<C>(v, src + base + c0, c, j, log_s);
+    col_passes<C, -1, 0, false>(v, lds, tw, c, j, [&] {
+        BigTw<C> f;
+        big_tw_load<C>(f, tw_lo, tw_hi, tw_h, (uint32_t)(c0 + c), j);
+        return f;
+    });
+    col_store<C, 0, 1>(v, dst + base + ((int64_t)c0 << LOGL), lds, tid, c, j, log_s, 1.0f);
+}
+
+// R2C pass 2 with the stitch (kernels.py:1127-1177 formula, r2c_bin): the
+// row pass of the half-length core over one aligned 16-column run of the
+// permuted Z (8 mirror pairs), then every output bin from its core value and
+// its mirror's, written to the n/2 + 1 bins of the row.  The mirror values
+// cross lanes through LDS in two rounds: lane columns 8..15 write and 0..7
+// read, then the other way round (a pair-0 column reads its own values in
+// the round it writes them).  A reading thread stitches and stores its bins
+// at once, so no thread needs room for the mirror values.  The bin twiddle
+// exp(-2 pi i k / n), k = k1 + N1 k2, is tw_a[k1] * tw_b[k2]; the thread
+// holding k = 0 also writes bin n/2.
+template <int LOGL, int LOGE, int LOGC>
+__global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_r2c_pass2_kernel(
+    const float2* src, float2* dst, const float2* __restrict__ tw, const float2* __restrict__ tw_a,
+    const float2* __restrict__ tw_b, int logn, int log_s, float scale) {
+    using C = ColCfg<LOGL, LOGE, LOGC>;
+    static_assert(LOGC == 4, "mirror pairs span 16 lane columns");
+    constexpr int N2 = C::L;
+    __shared__ float2 lds[C::LDS_FLOAT2];
+    const int n1 = 1 << log_s;
+    const int groups = n1 >> LOGC;
+    const int bid = xcd_pair_block((int)blockIdx.x, (int)gridDim.x);
+    const int64_t row = bid / groups;
+    const int g = bid - (int)(row * groups);
+    const int tid = threadIdx.x;
+    const int c = tid & (C::C - 1);
+    const int j = tid >> LOGC;
+    const int64_t np = (int64_t)1 << logn;  // core length L = n/2
+    float2 v[C::E];
+    col_load<C>(v, src + (row << logn) + (g << LOGC), c, j, log_s);
+    col_passes<C, -1, 1, false>(v, lds, tw, c, j, [&] { return BigTw<C>{}; });
+    const int mc = mirror_lane_col(g, c);
+    const int k1 = pair_col(g, c, n1);
+    const bool col0 = g == 0 && c == 0;  // k1 = 0: mirror rows N2 - k2 of its own column
+    const float2 ta = tw_a[k1];
+    float2* xo = dst + row * (np + 1);
+    static_for<0, 2>([&](auto rnd) {
+        __syncthreads();  // the previous readers of this LDS are done
+        if (rnd.value == 0 ? c >= 8 : c < 8) {
+            float2* lt = lds + (c & 7) * C::PITCH;
+            static_for<0, C::NB_LAST>([&](auto m) {
+                static_for<0, C::R_LAST>([&](auto q) {
+                    lt[pad(j + m.value * C::T + q.value * C::NS_LAST)] = v[m.value * C::R_LAST + q.value];
+                });
+            });
+        }
+        __syncthreads();
+        if (rnd.value == 0 ? mc >= 8 : mc < 8) {
+            const float2* lm = lds + (mc & 7) * C::PITCH;
+            static_for<0, C::NB_LAST>([&](auto m) {
+                static_for<0, C::R_LAST>([&](auto q) {
+                    const int k2 = j + m.value * C::T + q.value * C::NS_LAST;
+                    const int r = col0 ? ((N2 - k2) & (N2 - 1)) : (N2 - 1 - k2);
+                    const float2 z = v[m.value * C::R_LAST + q.value];
+                    const int64_t k = k1 + (int64_t)n1 * k2;
+                    xo[k] = r2c_bin(z, lm[pad(r)], cmul(ta, tw_b[k2]), scale, k == 0);
+                });
+            });
+            if (col0 && j == 0) xo[np] = r2c_bin(v[0], v[0], cmul(ta, tw_b[N2]), scale, true);
+        }
+    });
+}
+
+// C2R pass 1 with the pre-twiddle (kernels.py:1180-1229 formula,
+// c2r_pre_bin): the workgroup loads 8 columns of the n/2 + 1 bins and their
+// 8 mirror columns (pair_col), exchanges the mirror rows through LDS one
+// component at a time, turns every bin into its core input, then runs the
+// column pass of the half-length inverse core with its four-step twiddle and
+// stores Z in place of the output row (the row pass runs in place there).
+// The pre-twiddle root exp(-2 pi i n / n_real), n = n1 N2 + n2, is
+// tw_a[n2] * tw_b[n1]; bin n/2, the mirror of bin 0, is loaded by the thread
+// that holds bin 0, and the imaginary parts of both are ignored.
+template <int LOGL, int LOGE, int LOGC>
+__global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_c2r_pass1_kernel(
+    const float2* src, float2* dst, const float2* __restrict__ tw, const float2* __restrict__ tw_lo,
+    const float2* __restrict__ tw_hi, int tw_h, const float2* __restrict__ tw_a, const float2* __restrict__ tw_b,
+    int logn, int log_s) {
+    using C = ColCfg<LOGL, LOGE, LOGC>;
+    static_assert(LOGC == 4, "mirror pairs span 16 lane columns");
+    constexpr int N1 = C::L;
+    constexpr int R0 = 1 << C::logr(0);
+    constexpr int NB0 = C::E / R0;
+    __shared__ float2 lds[C::LDS_FLOAT2];
+    float* const ldsf = reinterpret_cast<float*>(lds);
+    const int n2n = 1 << log_s;
+    const int groups = n2n >> LOGC;
+    const int bid = xcd_pair_block((int)blockIdx.x, (int)gridDim.x);
+    const int64_t row = bid / groups;
+    const int g = bid - (int)(row * groups);
+    const int tid = threadIdx.x;
+    const int c = tid & (C::C - 1);
+    const int j = tid >> LOGC;
+    const int64_t np = (int64_t)1 << logn;
+    const int n2 = pair_col(g, c, n2n);
+    const int mc = mirror_lane_col(g, c);
+    const bool col0 = g == 0 && c == 0;  // n2 = 0: mirror rows N1 - n1 of its own column, bin n/2 for n1 = 0
+    const float2* xr = src + row * (np + 1);
+    float2 v[C::E];
+    // pass-0 operand rows n1 = j + m T + q N1/R0 of column n2 (non-temporal:
+    // each bin is read once)
+    const uint32_t lane = (uint32_t)(n2 + (j << log_s)) * 8u;
+    static_for<0, NB0>([&](auto m) {
+        static_for<0, R0>([&](auto q) {
+            const int r = m.value * C::T + q.value * (N1 / R0);
+            v[m.value * R0 + q.value] = load_nt(byte_off(xr + ((int64_t)r << log_s), lane));
+        });
+    });
+    const float2 xny = (col0 && j == 0) ? load_nt(xr + np) : make_float2(0.0f, 0.0f);
+    // mirror rows through LDS, real parts, then imaginary parts
+    float mre[C::E];
+    const int pf = C::PITCHF;
+    static_for<0, 2>([&](auto comp) {
+        if constexpr (comp.value > 0) __syncthreads();  // the real parts have been read
+        static_for<0, NB0>([&](auto m) {
+            static_for<0, R0>([&](auto q) {
+                const int n1 = j + m.value * C::T + q.value * (N1 / R0);
+                const float2 x = v[m.value * R0 + q.value];
+                ldsf[c * pf + pad32(n1)] = comp.value == 0 ? x.x : x.y;
+            });
+        });
+        __syncthreads();
+        static_for<0, NB0>([&](auto m) {
+            static_for<0, R0>([&](auto q) {
+                constexpr int e = m.value * R0 + q.value;
+                const int n1 = j + m.value * C::T + q.value * (N1 / R0);
+                const int r = col0 ? ((N1 - n1) & (N1 - 1)) : (N1 - 1 - n1);
+                const float y = ldsf[mc * pf + pad32(r)];
+                if constexpr (comp.value == 0) {
+                    mre[e] = y;
+                } else {
+                    float2 xk = v[e];
+                    float2 xj = make_float2(mre[e], y);
+                    if (col0 && n1 == 0) {  // bin 0 pairs with bin n/2; both imaginary parts ignored
+                        xj = make_float2(xny.x, 0.0f);
+                        xk.y = 0.0f;
+                    }
+                    v[e] = c2r_pre_bin(xk, xj, cmul(tw_a[n2], tw_b[n1]));
+                }
+            });
+        });
+    });
+    col_passes<C, 1, 0, true>(v, lds, tw, c, j, [&] {
+        BigTw<C> f;
+        big_tw_load<C>(f, tw_lo, tw_hi, tw_h, (uint32_t)n2, j);
+        return f;
+    });
+    col_store<C, 0, 2>(v, dst + (row << logn), lds, tid, c, j, log_s, 1.0f, g);
 }
 
 // Persistent form of the same pass: gridDim.x blocks, a multiple of the
@@ -610,6 +815,45 @@ hipError_t launch_pass(const float2* src, float2* dst, const mfft_plan* p, int64
     return hipGetLastError();
 }
 
+// KIND 0: R2C pass 1 (permuted Z); 1: R2C pass 2 with the stitch; 2: C2R
+// pass 1 with the pre-twiddle.  log_s: log2 of the columns of the pass.
+template <int LOGL, int KIND>
+hipError_t launch_real_pass(const float2* src, float2* dst, const mfft_plan* p, int64_t rows, int log_s,
+                            float scale, hipStream_t stream) {
+    constexpr int LOGE = col_loge(LOGL);
+    constexpr int LOGC = col_logc(LOGL);
+    using C = ColCfg<LOGL, LOGE, LOGC>;
+    const int logn = ilog2((int)p->core_n);
+    const int64_t tiles = rows * (((int64_t)1 << log_s) >> LOGC);
+    if constexpr (KIND == 0) {
+        fourstep_r2c_pass1_kernel<LOGL, LOGE, LOGC><<<(unsigned)tiles, C::WG, 0, stream>>>(
+            src, dst, p->tw_n1, p->tw_lo, p->tw_hi, p->tw_h, logn, log_s);
+    } else if constexpr (KIND == 1) {
+        fourstep_r2c_pass2_kernel<LOGL, LOGE, LOGC><<<(unsigned)tiles, C::WG, 0, stream>>>(
+            src, dst, p->tw_n2, p->tw_ra, p->tw_rb, logn, log_s, scale);
+    } else {
+        fourstep_c2r_pass1_kernel<LOGL, LOGE, LOGC><<<(unsigned)tiles, C::WG, 0, stream>>>(
+            src, dst, p->tw_n1, p->tw_lo, p->tw_hi, p->tw_h, p->tw_ra, p->tw_rb, logn, log_s);
+    }
+    mark(stream);
+    return hipGetLastError();
+}
+
+template <int KIND>
+hipError_t dispatch_real(int logl, const float2* src, float2* dst, const mfft_plan* p, int64_t rows, int log_s,
+                         float scale, hipStream_t stream) {
+    switch (logl) {
+        case 4: return launch_real_pass<4, KIND>(src, dst, p, rows, log_s, scale, stream);
+        case 5: return launch_real_pass<5, KIND>(src, dst, p, rows, log_s, scale, stream);
+        case 6: return launch_real_pass<6, KIND>(src, dst, p, rows, log_s, scale, stream);
+        case 7: return launch_real_pass<7, KIND>(src, dst, p, rows, log_s, scale, stream);
+        case 8: return launch_real_pass<8, KIND>(src, dst, p, rows, log_s, scale, stream);
+        case 9: return launch_real_pass<9, KIND>(src, dst, p, rows, log_s, scale, stream);
+        case 10: return launch_real_pass<10, KIND>(src, dst, p, rows, log_s, scale, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 template <int DIR, int KIND>
 hipError_t dispatch_len(int logl, const float2* src, float2* dst, const mfft_plan* p, int64_t rows,
                         int log_s, float scale, hipStream_t stream) {
@@ -699,6 +943,31 @@ hipError_t launch_fused(int dir, const float2* src, float2* dst, const mfft_plan
 
 bool fourstep_fused_supported(int l1, int l2) {
     return l1 >= 7 && l1 <= 9 && l2 >= 7 && l2 <= 9 && l1 - l2 <= 1 && l2 - l1 <= 1;
+}
+
+hipError_t launch_fourstep_real(const float2* src, float2* dst, float2* work, const mfft_plan* p, float scale,
+                                hipStream_t stream) {
+    const int l1 = ilog2((int)p->n1), l2 = ilog2((int)p->n2);
+    const int64_t rows = p->batch;
+    const int64_t chunk = p->chunk_rows > 0 ? p->chunk_rows : rows;
+    const int64_t np = p->core_n;
+    for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
+        const int64_t rc = rows - r0 < chunk ? rows - r0 : chunk;
+        hipError_t e;
+        if (p->transform_type == MFFT_R2C) {
+            // x (n reals = np complex per row) -> permuted Z in `work` -> n/2 + 1 bins
+            e = dispatch_real<0>(l1, src + r0 * np, work + r0 * np, p, rc, l2, 1.0f, stream);
+            if (e == hipSuccess)
+                e = dispatch_real<1>(l2, work + r0 * np, dst + r0 * (np + 1), p, rc, l1, scale, stream);
+        } else {
+            // n/2 + 1 bins -> pre-twiddled column pass into the output rows -> row pass in place
+            e = dispatch_real<2>(l1, src + r0 * (np + 1), dst + r0 * np, p, rc, l2, 1.0f, stream);
+            if (e == hipSuccess)
+                e = dispatch_len<1, 1>(l2, dst + r0 * np, dst + r0 * np, p, rc, l1, scale, stream);
+        }
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_fourstep(int dir, const float2* src, float2* dst, const mfft_plan* p, int64_t rows,

@@ -140,7 +140,8 @@ int upload(float2** dptr, const std::vector<float2>& h, int64_t* bytes, hipStrea
 }
 
 void release(mfft_plan* p) {
-    float2** bufs[] = {&p->tw, &p->tw_n1, &p->tw_n2, &p->tw_lo, &p->tw_hi, &p->tw_real, &p->ws_a, &p->ws_b};
+    float2** bufs[] = {&p->tw, &p->tw_n1, &p->tw_n2, &p->tw_lo,  &p->tw_hi,
+                       &p->tw_real, &p->tw_ra, &p->tw_rb, &p->ws_a, &p->ws_b};
     for (float2** b : bufs) {
         if (*b) (void)hipFree(*b);
         *b = nullptr;
@@ -265,6 +266,10 @@ int execute_impl(const mfft_plan* p, const void* in, void* out, const Work& w, v
                                   p->num_cus, p->stagger);
             return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
         }
+        if (p->real4_fused) {
+            he = mfft::launch_fourstep_real((const float2*)in, (float2*)out, w.a, p, p->scale, stream);
+            return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
+        }
         if (real_chunked(p)) {
             // chunk by chunk: the stitch reads the core output of its chunk
             // while that is still in the MALL
@@ -289,6 +294,10 @@ int execute_impl(const mfft_plan* p, const void* in, void* out, const Work& w, v
     if (p->c2r_fused) {
         he = mfft::launch_lds(2, 1, logc, p->elems, in, out, p->tw, p->tw_real, p->batch, p->scale, stream,
                               p->num_cus, p->stagger);
+        return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
+    }
+    if (p->real4_fused) {
+        he = mfft::launch_fourstep_real((const float2*)in, (float2*)out, nullptr, p, p->scale, stream);
         return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
     }
     if (real_chunked(p)) {
@@ -496,6 +505,10 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
     p->num_xcc = num_xcc > 0 ? num_xcc : 1;
     p->r2c_fused = transform_type == MFFT_R2C && flow == MFFT_FLOW_LDS_FUSED;
     p->c2r_fused = transform_type == MFFT_C2R && flow == MFFT_FLOW_LDS_FUSED;
+    // the stitch / pre-twiddle run inside the four-step passes (one column
+    // group per workgroup); the persistent and fused schedules keep them as
+    // a separate pass around the core
+    p->real4_fused = real && flow == MFFT_FLOW_FOUR_STEP && schedule == 0;
     // c2r: the half-length inverse core carries a factor 2 (entry.py:583-587)
     const double sc = norm_scale(n, transform_direction, norm) * (transform_type == MFFT_C2R ? 2.0 : 1.0);
     p->scale = (float)sc;
@@ -508,7 +521,7 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
         host.push_back(std::move(h));
         return upload(d, host.back(), &p->table_bytes, us);
     };
-    host.reserve(5);
+    host.reserve(7);
     if (rc == MFFT_OK && flow == MFFT_FLOW_FOUR_STEP) {
         const int lc = logc;
         const int l1 = mfft::ilog2((int)n1), l2 = mfft::ilog2((int)n2);
@@ -527,10 +540,23 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
         // exp(-2*pi*i*k/n), k in [0, n/2]  (runner.py:1650-1658 range)
         rc = put(&p->tw_real, roots(n, n / 2 + 1, 1));
     }
+    if (rc == MFFT_OK && p->real4_fused) {
+        // bin roots exp(-2 pi i k / n) as the product of two small tables:
+        // r2c k = k1 + n1 k2 (pass 2 grid), c2r k = n1 n2_len + n2 (pass 1 grid)
+        if (transform_type == MFFT_R2C) {
+            rc = put(&p->tw_ra, roots(n, n1, 1));
+            if (rc == MFFT_OK) rc = put(&p->tw_rb, roots(n, n2 + 1, n1));
+        } else {
+            rc = put(&p->tw_ra, roots(n, n2, 1));
+            if (rc == MFFT_OK) rc = put(&p->tw_rb, roots(n, n1, n2));
+        }
+    }
 
     // ---- workspace
     const size_t core_bytes = (size_t)batch * (size_t)core_n * sizeof(float2);
-    const bool need_a = real && !(p->r2c_fused || p->c2r_fused);
+    // the core output (r2c) / input (c2r) of a real flow that does not fuse
+    // both ends; the fused real four-step keeps only r2c's permuted Z there
+    const bool need_a = real && !(p->r2c_fused || p->c2r_fused) && !(p->real4_fused && transform_type == MFFT_C2R);
     const bool need_b = is_stage_flow(flow);
     p->need_a = need_a;
     p->need_b = need_b;
@@ -577,7 +603,7 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
     }
     // the stitch / pre-twiddle of a non-fused real flow: once, or once per
     // chunk of a chunked four-step core
-    const int64_t real_launches = !need_a ? 0 : real_chunked(p) ? (batch + chunk - 1) / chunk : 1;
+    const int64_t real_launches = (!need_a || p->real4_fused) ? 0 : real_chunked(p) ? (batch + chunk - 1) / chunk : 1;
     p->launches = core_launches + (int)real_launches;
 
     // the uploads are complete before the plan is handed out (and before the

@@ -27,7 +27,8 @@ struct mfft_plan {
     int num_cus = 0;     // compute units of `device` (persistent / fused grid size)
     int clock_khz = 0;   // constant wall-clock rate of `device` (fused schedule wait bound)
     int num_xcc = 8;     // XCDs of `device` (fused schedule work queues)
-    bool r2c_fused = false, c2r_fused = false;
+    bool r2c_fused = false, c2r_fused = false;  // LDS kernel with the real mode fused
+    bool real4_fused = false;  // real transform whose stitch / pre-twiddle is fused into the four-step passes
 
     // device memory owned by the plan
     float2* tw = nullptr;       // stage flows: W_core^m, m in [0, core_n); LDS flow: pass table
@@ -37,6 +38,8 @@ struct mfft_plan {
     float2* tw_hi = nullptr;    // W_core^(m*2^h)                (four-step twiddle, high digit)
     int tw_h = 0;
     float2* tw_real = nullptr;  // exp(-2*pi*i*k/n), k in [0, n/2]  (r2c stitch / c2r pre)
+    float2* tw_ra = nullptr;    // real four-step: r2c W_n^k1 (k1 < n1); c2r W_n^n2 (n2 < n2)
+    float2* tw_rb = nullptr;    // real four-step: r2c W_n^(n1 k2) (k2 <= n2); c2r W_n^(n2 n1) (n1 < n1)
     float2* ws_a = nullptr;     // core-sized scratch (real flows: core output / input)
     float2* ws_b = nullptr;     // core-sized scratch (stage-flow ping-pong)
     int* sync = nullptr;        // fused four-step counters (kFusedSlots, kFusedOverrun, kFusedHead)
@@ -119,5 +122,10 @@ int fourstep_col_loge(int logl);  // log2 elements per thread of a pass of lengt
 void fourstep_default_split(int log2n, int* log2n1, int* log2n2);
 hipError_t launch_fourstep(int dir, const float2* src, float2* dst, const mfft_plan* p,
                            int64_t rows, float scale, hipStream_t stream, int* launches);
+// A real transform with the stitch / pre-twiddle fused into the four-step
+// core (plans with real4_fused): R2C x -> permuted Z (work) -> bins;
+// C2R bins -> Z in the output rows -> the row pass in place.
+hipError_t launch_fourstep_real(const float2* src, float2* dst, float2* work, const mfft_plan* p, float scale,
+                                hipStream_t stream);
 
 }  // namespace mfft

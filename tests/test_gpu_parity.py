@@ -169,11 +169,14 @@ def test_four_step_split_and_chunk_neutral(gpu, n, n1, chunk):
 
 @pytest.mark.parametrize("tt", ["r2c", "c2r"])
 @pytest.mark.parametrize("n,n1,b,chunk", [(1 << 12, 32, 5, 2), (1 << 17, 256, 7, 3), (1 << 20, 1024, 3, 1)])
-def test_real_four_step_chunk_interleaved(gpu, tt, n, n1, b, chunk):
-    """A real transform over a chunked four-step core runs its stitch (r2c)
-    or pre-twiddle (c2r) chunk by chunk between the core's chunks, three
-    launches per chunk, the last chunk ragged.  Every row takes the same
-    arithmetic as without chunks, so the results are bit-identical."""
+@pytest.mark.parametrize("sched", [0, 1])
+def test_real_four_step_chunk_interleaved(gpu, tt, n, n1, b, chunk, sched):
+    """A real transform over a chunked four-step core runs chunk by chunk,
+    the last chunk ragged: with schedule 0 the stitch (r2c) or pre-twiddle
+    (c2r) is inside the two passes (two launches per chunk); with the
+    persistent schedule it is a separate launch between the core's chunks
+    (three per chunk).  Every row takes the same arithmetic as without
+    chunks, so the results are bit-identical."""
     td = "forward" if tt == "r2c" else "inverse"
     rng = np.random.default_rng(7100 + n + b)
     if tt == "r2c":
@@ -189,11 +192,12 @@ def test_real_four_step_chunk_interleaved(gpu, tt, n, n1, b, chunk):
     st = torch.cuda.current_stream(gpu).cuda_stream
     ys = []
     for ch in (0, chunk):
-        p = native.NativePlan(n, b, tt, td, "ortho", native.FLOW_FOUR_STEP, (n1, ch))
+        p = native.NativePlan(n, b, tt, td, "ortho", native.FLOW_FOUR_STEP, (n1, ch, sched))
         chunks = -(-b // ch) if ch else 1
-        assert p.info.launches == 3 * chunks
+        assert p.info.launches == (2 if sched == 0 else 3) * chunks
         y = out()
-        p.execute(x.data_ptr(), y.data_ptr(), st)
+        ws = torch.empty(max(p.ws_bytes, 1), dtype=torch.uint8, device=gpu)
+        p.execute_ws(x.data_ptr(), y.data_ptr(), ws.data_ptr(), p.ws_bytes, st)
         ys.append(y)
     torch.cuda.synchronize()
     assert torch.equal(ys[0], ys[1])
@@ -733,3 +737,61 @@ def test_plan_info_reports_flows(gpu):
     assert fs.flow_name == "four-step" and fs.info.launches == 2 and fs.info.workspace_bytes == 0
     r2 = native.NativePlan(1024, 2, flow=native.FLOW_RADIX2_DIT)
     assert r2.info.launches == 10 and r2.info.workspace_bytes == 2 * 1024 * 8
+
+
+# ------------------------------------------- real transforms fused into the four-step
+REAL4_SPLITS = [(512, 16), (1 << 12, 16), (1 << 12, 128), (1 << 15, 16), (1 << 15, 1024), (1 << 15, 128),
+                (1 << 17, 256), (1 << 18, 512), (1 << 19, 1024), (1 << 20, 512), (1 << 20, 1024)]
+
+
+@pytest.mark.parametrize("n,n1", REAL4_SPLITS)
+@pytest.mark.parametrize("b,chunk", [(1, 0), (3, 0), (5, 2)])
+def test_real_four_step_fused(gpu, n, n1, b, chunk):
+    """R2C with the stitch in pass 2 and C2R with the pre-twiddle in pass 1
+    (schedule 0): every split of the half-length core, the smallest column
+    groups (16 columns = 8 mirror pairs, pair 0 = columns 0 and n/2 of the
+    grid), ragged chunks, against numpy rfft / irfft; the plan makes two
+    launches per chunk and C2R takes no workspace."""
+    if n >= (1 << 19):
+        b, chunk = min(b, 3), min(chunk, 2)
+    xr = seeded_f32(n, b, session=12)
+    norm = "ortho" if chunk else "backward"
+    p = {"n1": n1, "chunk_rows": chunk}
+    r2c = mkplan("fft_four_step_batch" if b > 1 else "fft_four_step", n, b, tt="r2c", norm=norm, params=p)
+    X = execute_fft_plan(r2c, torch.from_numpy(xr).to(gpu))
+    check(X.cpu().numpy(), np.fft.rfft(xr.astype(np.float64), norm=norm), f"fused r2c N={n} n1={n1} B={b} c={chunk}")
+    c2r = mkplan("fft_four_step_batch" if b > 1 else "fft_four_step", n, b, tt="c2r", td="inverse", norm=norm,
+                 params=p)
+    h = X.cpu().numpy().astype(np.complex128)
+    y = execute_fft_plan(c2r, X).cpu().numpy()
+    check(y, np.fft.irfft(h, n=n, norm=norm), f"fused c2r N={n} n1={n1} B={b} c={chunk}")
+    nr, _ = _resolve(r2c, 0)
+    nc, _ = _resolve(c2r, 0)
+    chunks = -(-b // chunk) if chunk else 1
+    assert nr.info.launches == 2 * chunks and nc.info.launches == 2 * chunks
+    assert nc.ws_bytes == 0 and nr.ws_bytes == 8 * (n // 2) * b
+
+
+@pytest.mark.parametrize("n,n1", [(1 << 12, 64), (1 << 17, 256)])
+def test_real_four_step_fused_hermitian_edges(gpu, n, n1):
+    """C2R ignores the imaginary parts of bins 0 and n/2 (fused pre-twiddle
+    path), and special inputs (impulse, constant) stay exact."""
+    b = 2
+    rng = np.random.default_rng(99)
+    h = (rng.standard_normal((b, n // 2 + 1)) + 1j * rng.standard_normal((b, n // 2 + 1))).astype(np.complex64)
+    c2r = mkplan("fft_four_step_batch", n, b, tt="c2r", td="inverse", params={"n1": n1})
+    y = execute_fft_plan(c2r, torch.from_numpy(h).to(gpu)).cpu().numpy()
+    h2 = h.copy()
+    h2[:, 0] = h2[:, 0].real
+    h2[:, -1] = h2[:, -1].real
+    check(y, np.fft.irfft(h2.astype(np.complex128), n=n), f"fused c2r edges N={n}")
+    r2c = mkplan("fft_four_step_batch", n, b, tt="r2c", params={"n1": n1})
+    imp = np.zeros((b, n), np.float32)
+    imp[:, 0] = 1.0
+    X = execute_fft_plan(r2c, torch.from_numpy(imp).to(gpu)).cpu().numpy()
+    np.testing.assert_allclose(X, np.ones((b, n // 2 + 1)), atol=1e-6)
+    const = np.full((b, n), 3.0, np.float32)
+    X = execute_fft_plan(r2c, torch.from_numpy(const).to(gpu)).cpu().numpy()
+    ref = np.zeros((b, n // 2 + 1), np.complex128)
+    ref[:, 0] = 3.0 * n
+    assert np.abs(X - ref).max() <= 1e-5 * 3.0 * n
