@@ -249,6 +249,16 @@ int mfft_plan_sync_overruns(const mfft_plan* plan, int64_t* count);
  * (runner.bit_reverse_permute, runner.py:1542-1552); n a power of two. */
 int mfft_bit_reverse_permute(const void* in, void* out, int64_t n, int64_t batch, void* stream);
 
+/* The twiddle + transpose boundary of a composed four-step whose sub-FFTs
+ * run elsewhere (the reference's run_hybrid, adapter_hybrid.py:294-301, a
+ * fused "transpose + twiddle" pass between two vendor sub-FFT stages): for
+ * each of `batch` row-major rows x cols complex64 matrices S,
+ *   out[c][r] = S[r][c] * exp(-+2 pi i r c / (rows * cols))
+ * (- for MFFT_FORWARD, + for MFFT_INVERSE); rows and cols powers of two with
+ * rows * cols <= 2^20; in and out must not overlap. */
+int mfft_twiddle_transpose(const void* in, void* out, int64_t rows, int64_t cols, int64_t batch, int direction,
+                           void* stream);
+
 /* Device facts for the profile / environment fingerprint. */
 int mfft_device_props_get(int device, mfft_device_props* out);
 

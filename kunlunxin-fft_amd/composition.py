@@ -1,10 +1,16 @@
 """Exact-shape composition registry (reference src/xpu/composition.py).
 
 On the P800 the registry promoted one vendor-core 4-step composition
-(N=2048, B=16).  On MI355X the 4-step is a first-class kernel family chosen
-by the selector table itself, so no composition table ships: the lookup
-exists to keep the plan API's contract and fails closed -- it returns None
-unless a valid, profile- and environment-bound table is supplied.
+(N=2048, B=16).  Here a composition is a four-step whose sub-FFT stages run
+on a processing unit of the external-core registry (config/
+external_cores.json): rocFFT through torch.fft ("vendor"), or this library's
+own four-step ("local"); ``hybrid.run_hybrid`` executes it.
+``composition_builder.py`` measures candidate compositions against the
+selector's plan for exact shapes and writes config/composition_table.json,
+which holds only entries past the 2% guard (its measurements travel with it).
+The lookup fails closed: None unless a valid, profile- and environment-bound
+table has an entry for the exact shape and the c2c forward/backward
+semantic.
 """
 from __future__ import annotations
 
@@ -17,7 +23,7 @@ TABLE_PATH = os.path.join(CONFIG_DIR, "composition_table.json")
 KIND = "composition-promotion"
 TABLE_REQUIRED_KEYS = ("kind", "profile_hash", "env_hash", "precision", "guard_pct", "entries")
 ENTRY_REQUIRED_KEYS = ("N", "batch", "direction", "flow_id", "flow_realization",
-                       "processing_unit", "candidate_ms", "incumbent_ms", "guard_pct", "reason")
+                       "processing_unit", "candidate_ms", "incumbent_ms", "guard_pct", "reason", "tile", "core")
 
 
 def guard_pct_of(candidate_ms: float, incumbent_ms: float) -> float:
@@ -43,6 +49,8 @@ def table_violations(table: dict) -> list[str]:
         if key in seen:
             bad.append(f"duplicate exact-shape key {key}")
         seen.add(key)
+        if e["core"] not in ("vendor", "local"):
+            bad.append(f"entry {key}: unknown core {e['core']!r}")
         g = guard_pct_of(float(e["candidate_ms"]), float(e["incumbent_ms"]))
         if abs(g - float(e["guard_pct"])) > 1e-6:
             bad.append(f"entry {key}: guard_pct does not match its medians")
@@ -66,6 +74,46 @@ def load_composition_table(path: str = TABLE_PATH):
     if v:
         raise ConfigError("composition table violates its contract: " + "; ".join(v[:8]))
     return table
+
+
+CORES_PATH = os.path.join(CONFIG_DIR, "external_cores.json")
+CLASSIFICATIONS = ("local-core", "materialized-external-subtransform", "full-transform-only", "boundary",
+                   "reference-only", "unavailable")
+CORE_REQUIRED_KEYS = ("id", "source", "api", "classification", "device_resident", "selector_status")
+
+
+def load_external_cores(path: str = CORES_PATH) -> dict:
+    """The processing-unit registry (reference config/external_cores.json),
+    validated; ConfigError on a malformed registry."""
+    try:
+        with open(path) as f:
+            reg = json.load(f)
+    except (OSError, json.JSONDecodeError) as e:
+        raise ConfigError(f"external-core registry unreadable: {path}: {e}") from None
+    cores = reg.get("cores") if isinstance(reg, dict) else None
+    if not isinstance(cores, list) or not cores:
+        raise ConfigError("external-core registry: 'cores' must be a non-empty list")
+    seen = set()
+    for c in cores:
+        miss = [k for k in CORE_REQUIRED_KEYS if c.get(k) in (None, "")]
+        if miss:
+            raise ConfigError(f"external-core registry: core {c.get('id')!r} misses {miss}")
+        if c["classification"] not in CLASSIFICATIONS:
+            raise ConfigError(f"external-core registry: {c['id']}: classification {c['classification']!r} "
+                              f"not in {CLASSIFICATIONS}")
+        if c["id"] in seen:
+            raise ConfigError(f"external-core registry: duplicate id {c['id']!r}")
+        seen.add(c["id"])
+    return reg
+
+
+def composition_cores(reg: dict | None = None) -> dict:
+    """composition core name (HybridPlan.core) -> registry entry, for the
+    cores a composition may use for its sub-FFT stages."""
+    reg = reg if reg is not None else load_external_cores()
+    return {c["composition_core"]: c for c in reg["cores"]
+            if c.get("composition_core") and c["classification"] in ("local-core",
+                                                                    "materialized-external-subtransform")}
 
 
 def composition_select(direction: str, n: int, batch: int = 1, precision: str = "fp32",

@@ -1,0 +1,166 @@
+"""Build the MI355X composition table from live measurements.
+
+MI355X counterpart of the reference's composition promotion
+(scripts/promote_composition.py; table contract of src/xpu/composition.py:
+120-240).  For each exact shape (N, batch) of the reference's composition
+focus -- the shapes where its vendor-core four-step was measured, N in
+{1024, 2048, 4096} with B in {1, 16, 64}, plus config 4's N = 2^16, B = 256
+-- it times, as forward C2C complex64 with the default norm:
+
+* the incumbent: what ``plan_fft`` selects for the shape from the selector
+  table (with the device profile);
+* every composition of the external-core registry (config/
+  external_cores.json) that can run the shape: the vendor core (rocFFT
+  through torch.fft, with this library's twiddle-transpose boundary) and the
+  local core (this library's four-step), at each tile with tile and N/tile
+  of at least 16.
+
+A composition enters the table only when it beats the incumbent by at least
+the 2% guard; every measurement is written next to the entries, promoted or
+not, so a table without entries still records the evidence.  The table is
+bound to the device profile hash and the live environment fingerprint.
+
+Usage (on a GPU box):
+    python kunlunxin-fft_amd/composition_builder.py --out path/composition_table.json
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+
+SHAPES = [(n, b) for n in (1024, 2048, 4096) for b in (1, 16, 64)] + [(1 << 16, 256)]
+TILES = (16, 32, 64, 128, 256)
+
+
+def compositions(n: int, cores: dict):
+    """(core, tile) candidates for one length."""
+    out = []
+    for core in sorted(cores):
+        for tile in TILES:
+            t2 = n // tile
+            if n % tile or t2 < 16:
+                continue
+            if core == "local" and not (16 <= tile <= 1024 and 16 <= t2 <= 1024):
+                continue
+            out.append((core, tile))
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--out", required=True)
+    ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--rounds", type=int, default=5)
+    args = ap.parse_args()
+
+    import torch
+
+    sys.path.insert(0, ROOT)
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    from kunlunxin_fft_amd import composition, envcheck
+    from kunlunxin_fft_amd.config import DeviceProfile
+    from kunlunxin_fft_amd.hybrid import plan_hybrid, run_hybrid
+    from kunlunxin_fft_amd.selector import GUARD_PCT
+
+    env_hash = envcheck.current_env_hash()
+    if env_hash is None:
+        print("environment fingerprint unknown: refusing to build a table", file=sys.stderr)
+        return 1
+    prof = DeviceProfile.load().hash()
+    cores = composition.composition_cores()
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    stream = torch.cuda.current_stream(dev)
+
+    # the selector table's protocol (table_builder.py): cells of 64 MiB and
+    # more are timed one execute at a time, each after an untimed 256 MiB
+    # write elsewhere, so that no candidate gains from output lines that the
+    # previous repeat left in the MALL; smaller cells back to back
+    flush = torch.empty(1 << 26, dtype=torch.float32, device=dev)
+
+    def timed(fn, nbytes):
+        for _ in range(3):
+            fn()
+        res = []
+        if nbytes >= (64 << 20):
+            for _ in range(args.rounds):
+                for _ in range(max(3, args.reps // 4)):
+                    flush.fill_(1.0)
+                    s = torch.cuda.Event(enable_timing=True)
+                    e = torch.cuda.Event(enable_timing=True)
+                    s.record(stream)
+                    fn()
+                    e.record(stream)
+                    e.synchronize()
+                    res.append(s.elapsed_time(e))
+            return statistics.median(res)
+        for _ in range(args.rounds):
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record(stream)
+            for _ in range(args.reps):
+                fn()
+            e.record(stream)
+            e.synchronize()
+            res.append(s.elapsed_time(e) / args.reps)
+        return statistics.median(res)
+
+    entries, measurements = [], []
+    for n, b in SHAPES:
+        x = torch.randn((n,) if b == 1 else (b, n), dtype=torch.complex64, device=dev, generator=gen)
+        plan = pkg.plan_fft("dit", n, batch=b, profile_hash=prof)
+        inc_ms = timed(lambda: pkg.execute_fft_plan(plan, x), 8 * n * b)
+        ref = pkg.execute_fft_plan(plan, x)
+        row = {"N": n, "batch": b, "incumbent": plan.executed, "incumbent_ms": round(inc_ms, 5), "candidates": {}}
+        best = None
+        for core, tile in compositions(n, cores):
+            hp = plan_hybrid(n, b, tile=tile, core=core)
+            y = run_hybrid(x, hp)
+            err = (torch.linalg.vector_norm(y - ref) / torch.linalg.vector_norm(ref)).item()
+            if not err <= 1e-5:
+                raise RuntimeError(f"composition {core} tile={tile} N={n} B={b} differs from the incumbent: {err:.2e}")
+            ms = timed(lambda: run_hybrid(x, hp), 8 * n * b)
+            row["candidates"][f"{core}@{tile}"] = round(ms, 5)
+            if best is None or ms < best[0]:
+                best = (ms, core, tile)
+        measurements.append(row)
+        gain = composition.guard_pct_of(best[0], inc_ms) if best else -100.0
+        print(f"N={n:>6} B={b:>4} incumbent {plan.executed} {inc_ms * 1e3:8.2f} us, best composition "
+              f"{best[1]}@{best[2]} {best[0] * 1e3:8.2f} us ({gain:+.1f}%)", flush=True)
+        if best is not None and gain >= GUARD_PCT:
+            ms, core, tile = best
+            entries.append({
+                "N": n, "batch": b, "direction": "dit", "tile": tile, "core": core,
+                "flow_id": f"composition-{cores[core]['id']}", "flow_realization": "four-step-composition",
+                "processing_unit": cores[core]["id"], "candidate_ms": ms, "incumbent_ms": inc_ms,
+                "guard_pct": composition.guard_pct_of(ms, inc_ms),
+                "reason": f"{core}-core four-step at tile {tile} beats {plan.executed} by {gain:.1f}% "
+                          f"(>= {GUARD_PCT}%)"})
+        del x, ref
+    table = {"kind": composition.KIND, "profile_hash": prof, "env_hash": env_hash, "precision": "fp32",
+             "guard_pct": GUARD_PCT, "entries": entries,
+             "selection_semantics": "forward C2C complex64, norm backward, exact shapes; HIP events; cells under "
+                                    "64 MiB: median of rounds x (reps back-to-back executes / reps); cells of "
+                                    "64 MiB and more: median of single executes, each after an untimed 256 MiB "
+                                    "write; an entry only past the guard",
+             "measurements": measurements}
+    v = composition.table_violations(table)
+    if v:
+        raise RuntimeError("composition table violates its contract: " + "; ".join(v))
+    with open(args.out, "w") as f:
+        json.dump(table, f, indent=1)
+    print(f"wrote {args.out} ({len(entries)} entries, {len(measurements)} shapes measured)", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

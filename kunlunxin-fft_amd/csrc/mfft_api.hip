@@ -789,6 +789,27 @@ int mfft_bit_reverse_permute(const void* in, void* out, int64_t n, int64_t batch
     return e == hipSuccess ? MFFT_OK : hip_fail(e, "kernel launch");
 }
 
+int mfft_twiddle_transpose(const void* in, void* out, int64_t rows, int64_t cols, int64_t batch, int direction,
+                           void* stream) {
+    g_err.clear();
+    if (!in || !out) return fail(MFFT_ERR_VALUE, "in and out must not be NULL");
+    const int lr = log2_exact(rows), lc = log2_exact(cols);
+    if (lr < 0 || lc < 0 || lr + lc > mfft::kMaxLog2N)
+        return fail(MFFT_ERR_VALUE, "rows and cols must be powers of two with rows * cols <= 2^%d (got %lld x %lld)",
+                    mfft::kMaxLog2N, (long long)rows, (long long)cols);
+    if (batch < 1) return fail(MFFT_ERR_VALUE, "batch must be >= 1");
+    if (batch > ((int64_t)1 << 37) / (rows * cols)) return fail(MFFT_ERR_VALUE, "batch too large");
+    if (direction != MFFT_FORWARD && direction != MFFT_INVERSE)
+        return fail(MFFT_ERR_VALUE, "unsupported direction %d", direction);
+    const size_t bytes = (size_t)(rows * cols * batch) * 8;
+    if ((const char*)in < (const char*)out + bytes && (const char*)out < (const char*)in + bytes)
+        return fail(MFFT_ERR_VALUE, "in and out must not overlap");
+    if ((((uintptr_t)in) | ((uintptr_t)out)) & 7) return fail(MFFT_ERR_VALUE, "in and out must be 8-byte aligned");
+    const hipError_t e = mfft::launch_twiddle_transpose(direction == MFFT_FORWARD ? -1 : 1, (const float2*)in,
+                                                        (float2*)out, rows, cols, batch, (hipStream_t)stream);
+    return e == hipSuccess ? MFFT_OK : hip_fail(e, "kernel launch");
+}
+
 int mfft_device_props_get(int device, mfft_device_props* out) {
     g_err.clear();
     if (!out) return fail(MFFT_ERR_VALUE, "out must not be NULL");

@@ -83,6 +83,9 @@ hipError_t launch_radix4(bool dif, int dir, const float2* src, float2* dst, floa
                          const float2* tw, int64_t n, int64_t rows, float scale, int block,
                          hipStream_t stream, int* launches);
 hipError_t launch_bitrev(const float2* src, float2* dst, int64_t n, int64_t rows, hipStream_t stream);
+// G[c][r] = S[r][c] * W_(rows*cols)^(dir * r * c) for `batch` rows x cols matrices
+hipError_t launch_twiddle_transpose(int dir, const float2* s, float2* g, int64_t rows, int64_t cols, int64_t batch,
+                                    hipStream_t stream);
 // R2C stitch: z [rows][n/2] (unnormalised N/2 FFT of packed pairs) -> x [rows][n/2+1]
 hipError_t launch_r2c_stitch(const float2* z, float2* x, const float2* tw_real, int64_t n,
                              int64_t rows, float scale, hipStream_t stream);

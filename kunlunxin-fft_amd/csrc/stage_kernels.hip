@@ -201,6 +201,45 @@ __global__ __launch_bounds__(256) void c2r_pre_kernel(const float2* __restrict__
     if (k != 0 && k != half) zr[np - k] = c2r_pre_bin(xj, xk, tw_real[np - k]);
 }
 
+// Fused twiddle + transpose between the two sub-FFT stages of a composed
+// four-step (the reference's one-pass "transpose + twiddle" boundary of
+// run_hybrid, adapter_hybrid.py:294-301): for each of `batch` matrices
+// S[r][c] (rows x cols, n = rows * cols), G[c][r] = S[r][c] * W_n^(DIR r c).
+// 32 x 32 tiles through LDS (one pad column), so both the read of S and the
+// write of G are 256-byte runs.  The root comes from sinpi/cospi of the
+// index product reduced exactly modulo n (2 e / n is exact in float), not
+// from a table.
+template <int DIR>
+__global__ __launch_bounds__(256) void twiddle_transpose_kernel(const float2* __restrict__ s, float2* __restrict__ g,
+                                                               int rows, int cols, int tiles_r, int tiles_c,
+                                                               uint32_t nmask, float inv_half_n) {
+    __shared__ float2 tile[32][33];
+    const int t = blockIdx.x;
+    const int per = tiles_r * tiles_c;
+    const int64_t bt = t / per;
+    const int rem = t - (int)(bt * per);
+    const int tr = rem / tiles_c, tc = rem - tr * tiles_c;
+    const int r0 = tr * 32, c0 = tc * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8 threads
+    const float2* sb = s + bt * (int64_t)rows * cols;
+    float2* gb = g + bt * (int64_t)rows * cols;
+    for (int k = 0; k < 4; ++k) {
+        const int r = r0 + ty + 8 * k, c = c0 + tx;
+        if (r < rows && c < cols) {
+            const uint32_t e = ((uint32_t)r * (uint32_t)c) & nmask;
+            float sn, cs;
+            sincospif((float)e * inv_half_n, &sn, &cs);  // angle 2 pi e / n
+            const float2 w = make_float2(cs, DIR < 0 ? -sn : sn);
+            tile[ty + 8 * k][tx] = cmul(load_nt(sb + (int64_t)r * cols + c), w);
+        }
+    }
+    __syncthreads();
+    for (int k = 0; k < 4; ++k) {
+        const int c = c0 + ty + 8 * k, r = r0 + tx;
+        if (r < rows && c < cols) gb[(int64_t)c * rows + r] = tile[tx][ty + 8 * k];
+    }
+}
+
 inline unsigned grid_for(int64_t total, int block) { return (unsigned)((total + block - 1) / block); }
 
 }  // namespace
@@ -305,6 +344,24 @@ hipError_t launch_bitrev(const float2* src, float2* dst, int64_t n, int64_t rows
     const int64_t total = rows * n;
     if (total == 0) return hipSuccess;
     bitrev_kernel<<<grid_for(total, 256), 256, 0, stream>>>(src, dst, total, logn);
+    mark(stream);
+    return hipGetLastError();
+}
+
+hipError_t launch_twiddle_transpose(int dir, const float2* s, float2* g, int64_t rows, int64_t cols, int64_t batch,
+                                    hipStream_t stream) {
+    const int64_t n = rows * cols;
+    const int tiles_r = (int)((rows + 31) / 32), tiles_c = (int)((cols + 31) / 32);
+    const int64_t blocks = batch * tiles_r * tiles_c;
+    if (blocks == 0) return hipSuccess;
+    const uint32_t nmask = (uint32_t)(n - 1);
+    const float inv_half_n = 2.0f / (float)n;
+    if (dir < 0)
+        twiddle_transpose_kernel<-1><<<(unsigned)blocks, 256, 0, stream>>>(s, g, (int)rows, (int)cols, tiles_r,
+                                                                          tiles_c, nmask, inv_half_n);
+    else
+        twiddle_transpose_kernel<1><<<(unsigned)blocks, 256, 0, stream>>>(s, g, (int)rows, (int)cols, tiles_r,
+                                                                         tiles_c, nmask, inv_half_n);
     mark(stream);
     return hipGetLastError();
 }

@@ -6,8 +6,9 @@ Same contract as the reference:
    transform_type in {c2c, r2c, c2r}, transform_direction in {forward,
    inverse}, norm in {none, forward, backward, ortho}; r2c is forward-only
    and c2r inverse-only) and raise ``ValueError`` before any table query;
-2. look up the frozen MI355X table (``selector``), after the composition
-   registry (``composition``, which ships empty and fails closed);
+2. look up the frozen MI355X table (``selector``), after the exact-shape
+   composition table (``composition``: entries only past the 2% guard,
+   failing closed on any binding mismatch);
 3. resolve the runner name (``executed``), or fall back to M0 with the
    reason when the table abstains or names no lowering;
 4. ``execute_fft_plan`` checks the input's shape/dtype against the plan,
@@ -206,7 +207,7 @@ def _composition_plan(comp: dict, n, batch, direction, precision, transform_dire
                f"{comp['reason']}",
         fallback=False, executed="run_hybrid", block=None, flow_id=comp["flow_id"],
         flow_realization=comp["flow_realization"], processing_unit=comp["processing_unit"],
-        params={"flow_kind": "composition", "tile": comp.get("tile", 0)},
+        params={"flow_kind": "composition", "tile": comp.get("tile", 0), "core": comp.get("core", "local")},
         transform_type="c2c", transform_direction=transform_direction, norm=norm,
     )
 
@@ -359,6 +360,13 @@ def _execute_checked(plan: ExecutionPlan, x):
         if not x.is_contiguous():
             raise ValueError("x must be contiguous; call .contiguous() first")
     dev = x.device.index if x.device.index is not None else torch.cuda.current_device()
+    if plan.params.get("flow_kind") == "composition" and plan.params.get("core") == "vendor":
+        # a composition around the external (vendor) sub-FFT core
+        from .hybrid import plan_hybrid, run_hybrid
+
+        with phase("core-invoke"):
+            return run_hybrid(x, plan_hybrid(plan.n, plan.batch, int(plan.params["tile"]), "vendor",
+                                             plan.transform_direction, plan.norm))
     with phase("core-invoke"):
         nplan, (shape, dt) = _resolve(plan, dev)
         out = torch.empty(shape, dtype=dt, device=x.device)

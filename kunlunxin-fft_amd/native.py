@@ -39,7 +39,7 @@ EXPORTS = (
     "mfft_plan_create", "mfft_execute", "mfft_execute_timed", "mfft_plan_destroy", "mfft_plan_query",
     "mfft_bit_reverse_permute", "mfft_device_props_get", "mfft_last_error",
     "mfft_abi_version", "mfft_plan_sync_overruns", "mfft_plan_create_ex", "mfft_plan_workspace_size",
-    "mfft_execute_ws", "mfft_execute_noalloc",
+    "mfft_execute_ws", "mfft_execute_noalloc", "mfft_twiddle_transpose",
 )
 PLAN_CALLER_WORKSPACE = 1
 
@@ -117,6 +117,8 @@ def load() -> ctypes.CDLL:
         lib.mfft_plan_sync_overruns.restype = i32
         lib.mfft_bit_reverse_permute.argtypes = [vp, vp, i64, i64, vp]
         lib.mfft_bit_reverse_permute.restype = i32
+        lib.mfft_twiddle_transpose.argtypes = [vp, vp, i64, i64, i64, i32, vp]
+        lib.mfft_twiddle_transpose.restype = i32
         lib.mfft_device_props_get.argtypes = [i32, ctypes.POINTER(DeviceProps)]
         lib.mfft_device_props_get.restype = i32
         lib.mfft_last_error.argtypes = []
@@ -258,6 +260,13 @@ def release_retired(sync=None) -> int:
 def bit_reverse_permute(in_ptr: int, out_ptr: int, n: int, batch: int, stream_ptr: int) -> None:
     check(load().mfft_bit_reverse_permute(ctypes.c_void_p(in_ptr), ctypes.c_void_p(out_ptr),
                                           int(n), int(batch), ctypes.c_void_p(stream_ptr)))
+
+
+def twiddle_transpose(in_ptr: int, out_ptr: int, rows: int, cols: int, batch: int, direction: str,
+                      stream_ptr: int) -> None:
+    """out[c][r] = in[r][c] * W_(rows*cols)^(-+ r c) per rows x cols matrix."""
+    check(load().mfft_twiddle_transpose(ctypes.c_void_p(in_ptr), ctypes.c_void_p(out_ptr), int(rows), int(cols),
+                                        int(batch), DIR_IDS[direction], ctypes.c_void_p(stream_ptr)))
 
 
 def device_props(device: int = 0) -> dict:

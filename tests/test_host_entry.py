@@ -280,7 +280,18 @@ def test_select_abstains_without_profile():
 def test_composition_fails_closed():
     from kunlunxin_fft_amd.composition import composition_select, load_composition_table
 
-    assert load_composition_table() is None
+    from kunlunxin_fft_amd.selector import GUARD_PCT
+
+    # the shipped table was measured on MI355X: no composition beat its
+    # incumbent by the guard, so it holds no entry, only the measurements
+    t = load_composition_table()
+    assert t is not None and t["profile_hash"] == PROF and t["entries"] == []
+    assert len(t["measurements"]) == 10
+    for row in t["measurements"]:
+        best = min(row["candidates"].values())
+        assert (row["incumbent_ms"] - best) / row["incumbent_ms"] * 100.0 < GUARD_PCT, row
+        assert composition_select("dit", row["N"], batch=row["batch"], profile_hash=PROF,
+                                  env_hash=t["env_hash"]) is None
     assert composition_select("dit", 2048, batch=16, profile_hash=PROF, env_hash=ENV) is None
 
 
@@ -306,3 +317,61 @@ def test_env_fingerprint_unknown_without_gpu():
     if torch.cuda.is_available():
         pytest.skip("a GPU is present")
     assert envcheck.current_env_hash() is None
+
+
+def test_external_core_registry_and_composition_contract():
+    """The external-core registry loads and validates; a composition entry
+    must name its tile and core; composition_select honours the exact shape,
+    semantics, profile and environment binding; the plan it yields routes to
+    run_hybrid with the entry's tile and core."""
+    import copy
+
+    from kunlunxin_fft_amd import composition
+    from kunlunxin_fft_amd.config import ConfigError
+    from kunlunxin_fft_amd.entry import _composition_plan
+
+    reg = composition.load_external_cores()
+    cores = composition.composition_cores(reg)
+    assert set(cores) == {"vendor", "local"}
+    assert cores["vendor"]["classification"] == "materialized-external-subtransform"
+    bad = copy.deepcopy(reg)
+    bad["cores"][0]["classification"] = "magic"
+    import json
+    import tempfile
+    with tempfile.NamedTemporaryFile("w", suffix=".json", delete=False) as f:
+        json.dump(bad, f)
+    with pytest.raises(ConfigError, match="classification"):
+        composition.load_external_cores(f.name)
+    entry = {"N": 2048, "batch": 16, "direction": "dit", "tile": 64, "core": "vendor", "flow_id": "c",
+             "flow_realization": "four-step-composition", "processing_unit": "rocfft_torch_fft",
+             "candidate_ms": 0.01, "incumbent_ms": 0.02, "guard_pct": 50.0, "reason": "test"}
+    table = {"kind": composition.KIND, "profile_hash": PROF, "env_hash": ENV, "precision": "fp32",
+             "guard_pct": 2.0, "entries": [entry]}
+    assert composition.table_violations(table) == []
+    assert any("missing" in v for v in composition.table_violations(
+        dict(table, entries=[{k: v for k, v in entry.items() if k != "core"}])))
+    assert any("guard" in v for v in composition.table_violations(
+        dict(table, entries=[dict(entry, candidate_ms=0.0199, guard_pct=0.5)])))
+    sel = lambda **kw: composition.composition_select(  # noqa: E731
+        "dit", kw.pop("n", 2048), batch=kw.pop("batch", 16), profile_hash=kw.pop("prof", PROF),
+        env_hash=kw.pop("env", ENV), table=table, **kw)
+    assert sel() == entry
+    assert sel(batch=64) is None and sel(prof="0" * 16) is None and sel(env="1" * 16) is None
+    assert sel(transform_direction="inverse") is None and sel(normalization="ortho") is None
+    plan = _composition_plan(entry, 2048, 16, "dit", "fp32", "forward", "backward")
+    assert plan.executed == "run_hybrid" and plan.params["core"] == "vendor" and plan.params["tile"] == 64
+
+
+def test_hybrid_plan_contract():
+    from kunlunxin_fft_amd.hybrid import plan_hybrid
+
+    p = plan_hybrid(2048, 16, tile=64)
+    assert p.stage2_len == 32 and p.core == "vendor"
+    with pytest.raises(ValueError):
+        plan_hybrid(2048, 1, tile=48)
+    with pytest.raises(ValueError):
+        plan_hybrid(2048, 1, tile=4096)
+    with pytest.raises(ValueError):
+        plan_hybrid(2048, 1, tile=64, core="triton")
+    with pytest.raises(ValueError):
+        plan_hybrid(1 << 12, 1, tile=8, core="local")  # the local core needs tile >= 16
