@@ -37,7 +37,8 @@
  * device that was current at plan creation, which must be current at
  * execute.  `in` and `out` must not overlap; `in` is never written.
  * A plan is immutable after creation.  A plan that needs no workspace
- * (mfft_plan_workspace_size = 0: every LDS_FUSED plan and FOUR_STEP C2C) can
+ * (mfft_plan_workspace_size = 0: every LDS_FUSED plan and FOUR_STEP C2C with
+ * schedule 0 or 1) can
  * be executed from any number of host threads and streams at once.  Executes
  * of a plan that needs workspace and overlap in time (two streams or two
  * host threads) share the plan's workspace and race: serialise them, give
@@ -107,21 +108,26 @@ enum {
  *                                    resident wave of them) that load their
  *                                    next column group while transforming the
  *                                    current one; 2 = fused: both passes in
- *                                    one launch, each transform's pass 2 on
- *                                    the XCD whose L2 holds its pass-1 output
- *                                    (n1, n2 in [128, 512] within 2x; one
- *                                    execute of such a plan at a time: its
- *                                    counters live in the plan),
+ *                                    one launch, each transform's pass-1
+ *                                    output in a ring of slots per XCD in
+ *                                    the workspace, which stays in that XCD's
+ *                                    L2, and its pass 2 on the same XCD
+ *                                    (n1, n2 in [128, 512] within 2x; the
+ *                                    counters and the ring are workspace),
  *                        params[3] = schedules 0, 1: pass-2 row order: 0 =
  *                                    forward; 1 = reverse, so the batch rows
  *                                    pass 1 wrote last (the most likely still
  *                                    in the MALL) are read first; schedule 2:
- *                                    bits 0-7 = queue lag, 1..64 transforms
+ *                                    bits 0-7 = queue lag, 1..63 transforms
  *                                    that pass 1 runs ahead of pass 2 on an
  *                                    XCD (0 = one more than the XCD's resident
  *                                    blocks hold in flight), bits 8-15 = queue
  *                                    items a workgroup takes per dequeue,
- *                                    1..64 (0 = 2) */
+ *                                    1..64 (0 = 1), bits 16-23 = Z slots per
+ *                                    XCD, lag + 1..64 (0 = lag + 1 + the
+ *                                    transforms the resident blocks hold),
+ *                                    bits 24-30 = workgroups per CU, 1..16
+ *                                    (0 = as many as fit) */
 #define MFFT_MAX_PARAMS 4
 
 typedef struct mfft_plan mfft_plan;
@@ -173,13 +179,15 @@ int mfft_execute(const mfft_plan* plan, const void* in, void* out, void* stream)
  * workspace (its execute_fft_plan, src/xpu/entry.py:501-628, allocates per
  * call on the framework's stream); these entry points close that gap for
  * callers that manage device memory themselves.  A plan needs workspace only
- * for the stage flows (RADIX2/RADIX4: one batch x core_n complex64 buffer)
- * and for real transforms whose core is not fused into the LDS kernel (one
- * more such buffer); LDS_FUSED and FOUR_STEP C2C need none.
+ * for the stage flows (RADIX2/RADIX4: one batch x core_n complex64 buffer),
+ * for real transforms whose core is not fused into the LDS kernel (one more
+ * such buffer) and for the fused FOUR_STEP schedule (its launch counters and
+ * its ring of XCDs x slots x core_n complex64); LDS_FUSED and FOUR_STEP C2C
+ * with schedules 0 and 1 need none.
  *
  * mfft_plan_create_ex: mfft_plan_create with `flags`; with
  * MFFT_PLAN_CALLER_WORKSPACE the plan allocates only its twiddle tables (and
- * the fused four-step's counters), and every execute of a plan that needs
+ * the fused four-step's overrun count), and every execute of a plan that needs
  * workspace must go through mfft_execute_ws (mfft_execute refuses it). */
 #define MFFT_PLAN_CALLER_WORKSPACE 1
 int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform_type,
@@ -239,9 +247,10 @@ int mfft_plan_destroy(mfft_plan* plan);
 int mfft_plan_query(const mfft_plan* plan, mfft_plan_info* info);
 
 /* FOUR_STEP schedule 2 only (no counterpart in the reference: a diagnostic of
- * this library's fused schedule): how many pass-2 waits of this plan's
- * launches so far gave up at their poll limit instead of seeing pass 1
- * complete -- 0 unless something is wrong.  Copies one int from the device
+ * this library's fused schedule): how many waits of this plan's launches so
+ * far (pass 2 for its pass-1 output, pass 1 for its Z slot) gave up at their
+ * limit instead of seeing the work they wait for complete -- 0 unless
+ * something is wrong; a launch with such a wait writes NaN from then on.  Copies one int from the device
  * (synchronous); *count = 0 for plans of any other flow. */
 int mfft_plan_sync_overruns(const mfft_plan* plan, int64_t* count);
 

@@ -146,8 +146,10 @@ void release(mfft_plan* p) {
         if (*b) (void)hipFree(*b);
         *b = nullptr;
     }
-    if (p->sync) (void)hipFree(p->sync);
-    p->sync = nullptr;
+    if (p->overrun) (void)hipFree(p->overrun);
+    p->overrun = nullptr;
+    if (p->ws_f) (void)hipFree(p->ws_f);
+    p->ws_f = nullptr;
 }
 
 // Device address of `scratch` on device `dev` (current), looked up on the
@@ -182,7 +184,14 @@ constexpr int64_t kWorkAlign = 256;
 struct Work {
     float2* a;  // core-sized: the core output (r2c) or input (c2r) of a non-fused real flow
     float2* b;  // core-sized: stage-flow ping-pong
+    char* f;    // the fused four-step schedule's counters and Z ring
 };
+
+// The three scratch regions of a workspace (or of the static noalloc buffer)
+Work carve(const mfft_plan* p, char* w) {
+    return Work{p->need_a ? (float2*)w : nullptr, p->need_b ? (float2*)(w + p->work_b_off) : nullptr,
+                p->need_f ? w + p->work_f_off : nullptr};
+}
 
 // Enqueue the complex core of length p->core_n over `rows` rows.
 int run_core(const mfft_plan* p, const float2* src, float2* dst, int dir, float scale, const Work& w,
@@ -205,7 +214,7 @@ int run_core(const mfft_plan* p, const float2* src, float2* dst, int dir, float 
                                  p->batch, scale, stream, p->num_cus, p->stagger);
             break;
         case MFFT_FLOW_FOUR_STEP:
-            e = mfft::launch_fourstep(dir, src, dst, p, p->batch, scale, stream, &launches);
+            e = mfft::launch_fourstep(dir, src, dst, w.f, p, p->batch, scale, stream, &launches);
             break;
         case MFFT_FLOW_DENSE_MFMA:
             e = mfft::launch_mfma(dir, mfft::ilog2((int)p->core_n), src, dst, p->tw, p->batch, scale, stream);
@@ -276,8 +285,8 @@ int execute_impl(const mfft_plan* p, const void* in, void* out, const Work& w, v
             const int64_t cn = p->core_n;
             for (int64_t r0 = 0; r0 < p->batch; r0 += p->chunk_rows) {
                 const int64_t rc = p->batch - r0 < p->chunk_rows ? p->batch - r0 : p->chunk_rows;
-                he = mfft::launch_fourstep(-1, (const float2*)in + r0 * cn, w.a + r0 * cn, p, rc, 1.0f, stream,
-                                           nullptr);
+                he = mfft::launch_fourstep(-1, (const float2*)in + r0 * cn, w.a + r0 * cn, nullptr, p, rc, 1.0f,
+                                           stream, nullptr);
                 if (he == hipSuccess)
                     he = mfft::launch_r2c_stitch(w.a + r0 * cn, (float2*)out + r0 * (cn + 1), p->tw_real, p->n, rc,
                                                  p->scale, stream);
@@ -308,7 +317,8 @@ int execute_impl(const mfft_plan* p, const void* in, void* out, const Work& w, v
             const int64_t rc = p->batch - r0 < p->chunk_rows ? p->batch - r0 : p->chunk_rows;
             he = mfft::launch_c2r_pre((const float2*)in + r0 * (cn + 1), w.a + r0 * cn, p->tw_real, p->n, rc, stream);
             if (he == hipSuccess)
-                he = mfft::launch_fourstep(1, w.a + r0 * cn, (float2*)out + r0 * cn, p, rc, p->scale, stream, nullptr);
+                he = mfft::launch_fourstep(1, w.a + r0 * cn, (float2*)out + r0 * cn, nullptr, p, rc, p->scale,
+                                           stream, nullptr);
             if (he != hipSuccess) return hip_fail(he, "kernel launch");
         }
         return MFFT_OK;
@@ -377,7 +387,7 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
         flow = mfft::lds_supported(logc, 0, lds_mode) ? MFFT_FLOW_LDS_FUSED : MFFT_FLOW_FOUR_STEP;
     int block = 256, elems = 0, stagger = 0;
     int64_t n1 = 0, n2 = 0, chunk = 0;
-    int schedule = 0, pass2_rev = 0, fused_lag = 0, fused_take = 0;
+    int schedule = 0, pass2_rev = 0, fused_lag = 0, fused_take = 0, fused_ring = 0, fused_bpc = 0;
     switch (flow) {
         case MFFT_FLOW_RADIX2_DIT:
         case MFFT_FLOW_RADIX2_DIF:
@@ -430,25 +440,31 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
             schedule = prm[2];
             if (schedule != 2 && (prm[3] < 0 || prm[3] > 1))
                 return fail(MFFT_ERR_VALUE, "FOUR_STEP pass-2 row order must be 0 or 1, got %d", prm[3]);
-            if (schedule == 2 && (prm[3] & 0xff) > 64)
-                return fail(MFFT_ERR_VALUE, "FOUR_STEP fused queue lag (params[3] bits 0-7) must be in [0, 64], got %d",
-                            prm[3] & 0xff);
-            if (schedule == 2 && (prm[3] >> 8) > 64)
+            if (schedule == 2 && (prm[3] & 0xff) >= mfft::kFusedMaxRing)
+                return fail(MFFT_ERR_VALUE, "FOUR_STEP fused queue lag (params[3] bits 0-7) must be in [0, %d], got %d",
+                            mfft::kFusedMaxRing - 1, prm[3] & 0xff);
+            if (schedule == 2 && ((prm[3] >> 8) & 0xff) > 64)
                 return fail(MFFT_ERR_VALUE,
                             "FOUR_STEP fused items per dequeue (params[3] bits 8-15) must be in [0, 64], got %d",
-                            prm[3] >> 8);
+                            (prm[3] >> 8) & 0xff);
+            if (schedule == 2 && ((prm[3] >> 16) & 0xff) > mfft::kFusedMaxRing)
+                return fail(MFFT_ERR_VALUE,
+                            "FOUR_STEP fused Z slots per XCD (params[3] bits 16-23) must be in [0, %d], got %d",
+                            mfft::kFusedMaxRing, (prm[3] >> 16) & 0xff);
+            if (schedule == 2 && (prm[3] >> 24) > 16)
+                return fail(MFFT_ERR_VALUE,
+                            "FOUR_STEP fused blocks per CU (params[3] bits 24-30) must be in [0, 16], got %d",
+                            prm[3] >> 24);
             pass2_rev = schedule == 2 ? 0 : prm[3];
             fused_lag = schedule == 2 ? (prm[3] & 0xff) : 0;
-            fused_take = schedule == 2 ? (prm[3] >> 8) : 0;
+            fused_take = schedule == 2 ? ((prm[3] >> 8) & 0xff) : 0;
+            fused_ring = schedule == 2 ? ((prm[3] >> 16) & 0xff) : 0;
+            fused_bpc = schedule == 2 ? (prm[3] >> 24) : 0;
             if (schedule == 2 && !mfft::fourstep_fused_supported(l1, l2))
                 return fail(MFFT_ERR_UNSUPPORTED,
                             "the fused FOUR_STEP schedule needs n1, n2 in [128, 512] within a factor 2 "
                             "(got 2^%d x 2^%d)",
                             l1, l2);
-            // The fused schedule did not finish on the MI355X in two runs (N=2^14, B=1): its work
-            // loop had been compiled into an inner loop around the barriers that only thread 0
-            // could leave.  The loop now branches on wave-uniform values only and is bounded by
-            // its item count; until that has run on the GPU the schedule stays switched off.
             if (schedule == 2 && !mfft::kFusedScheduleEnabled)
                 return fail(MFFT_ERR_UNSUPPORTED,
                             "the fused FOUR_STEP schedule (params[2] = 2) is disabled in this build");
@@ -479,6 +495,37 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
     if (schedule == 2 && (num_xcc < 1 || num_xcc > mfft::kFusedSlots))
         return fail(MFFT_ERR_UNSUPPORTED, "the fused FOUR_STEP schedule needs 1..%d XCDs (device reports %d)",
                     mfft::kFusedSlots, num_xcc);
+    int fused_grid = 0;
+    if (schedule == 2) {
+        // one resident wave of blocks (at most fused_bpc per CU), a multiple
+        // of the XCD count: blocks go to the XCDs round-robin, so every XCD,
+        // and every queue, gets blocks
+        const int l1 = mfft::ilog2((int)n1), l2 = mfft::ilog2((int)n2);
+        int per_cu = mfft::fourstep_fused_occupancy(l1, l2);
+        if (per_cu < 1) return fail(MFFT_ERR_RUNTIME, "occupancy query of the fused four-step kernel failed");
+        if (fused_bpc > 0 && fused_bpc < per_cu) per_cu = fused_bpc;
+        const int nx = num_xcc, cus = num_cus > 0 ? num_cus : 1;
+        fused_grid = (per_cu * cus) / nx * nx;
+        if (fused_grid < nx) fused_grid = nx;
+        // defaults, the fastest of the measured settings at 2^16..2^18: one
+        // item per dequeue; pass 1 one transform more ahead of pass 2 than
+        // the blocks of one XCD hold items (wt transforms of G1 + G2 items),
+        // so pass 2 rarely waits for Z; and wt slots more than that, so pass 1
+        // rarely waits for its slot
+        if (fused_take == 0) fused_take = 1;
+        const int items = (int)((n2 >> 4) + (n1 >> 4));
+        const int wt = (fused_grid / nx * fused_take + items - 1) / items;
+        if (fused_lag == 0) fused_lag = wt + 1;
+        if (fused_lag >= mfft::kFusedMaxRing) fused_lag = mfft::kFusedMaxRing - 1;
+        // a ring slot is rewritten by pass 1 of transform k + R only after
+        // pass 2 of k has read it; R >= lag + 1 keeps that wait on a
+        // transform the queue handed out earlier
+        if (fused_ring == 0) fused_ring = fused_lag + 1 + wt;
+        if (fused_ring > mfft::kFusedMaxRing) fused_ring = mfft::kFusedMaxRing;
+        if (fused_ring < fused_lag + 1 || fused_ring > mfft::kFusedMaxRing)
+            return fail(MFFT_ERR_VALUE, "FOUR_STEP fused Z slots per XCD (%d) must be in [lag + 1 = %d, %d]",
+                        fused_ring, fused_lag + 1, mfft::kFusedMaxRing);
+    }
 
     mfft_plan* p = new (std::nothrow) mfft_plan();
     if (!p) return fail(MFFT_ERR_RUNTIME, "out of host memory");
@@ -500,6 +547,8 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
     p->pass2_rev = pass2_rev;
     p->fused_lag = fused_lag;
     p->fused_take = fused_take;
+    p->fused_ring = fused_ring;
+    p->fused_grid = fused_grid;
     p->num_cus = num_cus > 0 ? num_cus : 1;
     p->clock_khz = clock_khz > 0 ? clock_khz : 100000;
     p->num_xcc = num_xcc > 0 ? num_xcc : 1;
@@ -558,11 +607,25 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
     // both ends; the fused real four-step keeps only r2c's permuted Z there
     const bool need_a = real && !(p->r2c_fused || p->c2r_fused) && !(p->real4_fused && transform_type == MFFT_C2R);
     const bool need_b = is_stage_flow(flow);
+    const bool need_f = flow == MFFT_FLOW_FOUR_STEP && schedule == 2;
+    auto align = [](int64_t x) { return (x + kWorkAlign - 1) / kWorkAlign * kWorkAlign; };
     p->need_a = need_a;
     p->need_b = need_b;
+    p->need_f = need_f;
     p->core_bytes = (int64_t)core_bytes;
-    p->work_b_off = need_a ? (p->core_bytes + kWorkAlign - 1) / kWorkAlign * kWorkAlign : 0;
-    p->work_bytes = need_b ? p->work_b_off + p->core_bytes : (need_a ? p->core_bytes : 0);
+    p->work_b_off = need_a ? align(p->core_bytes) : 0;
+    const int64_t end_ab = need_b ? p->work_b_off + p->core_bytes : (need_a ? p->core_bytes : 0);
+    if (need_f) {
+        // counters of one launch (a chunk, or the batch), then num_xcc x
+        // fused_ring Z slots of one transform each
+        const int64_t rows = chunk > 0 && chunk < batch ? chunk : batch;
+        p->fused_ring_off = align((int64_t)(mfft::kFusedHead + 2 * rows) * (int64_t)sizeof(int));
+        p->fused_bytes = p->fused_ring_off + (int64_t)p->num_xcc * fused_ring * core_n * (int64_t)sizeof(float2);
+        p->work_f_off = align(end_ab);
+        p->work_bytes = p->work_f_off + p->fused_bytes;
+    } else {
+        p->work_bytes = end_ab;
+    }
     p->caller_ws = (flags & MFFT_PLAN_CALLER_WORKSPACE) != 0;
     if (rc == MFFT_OK && need_a && !p->caller_ws) {
         he = hipMalloc((void**)&p->ws_a, core_bytes);
@@ -574,15 +637,17 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
         if (he != hipSuccess) rc = hip_fail(he, "hipMalloc(workspace)");
         else p->ws_bytes += (int64_t)core_bytes;
     }
-    if (rc == MFFT_OK && schedule == 2) {
-        // fused four-step counters: the queues, the overrun count, and one
-        // per transform of a launch (a chunk, or the batch)
-        const int64_t rows = chunk > 0 && chunk < batch ? chunk : batch;
-        const size_t sb = (size_t)(mfft::kFusedHead + rows) * sizeof(int);
-        he = hipMalloc((void**)&p->sync, sb);
-        if (he == hipSuccess) he = hipMemsetAsync(p->sync, 0, sb, us);
-        if (he != hipSuccess) rc = hip_fail(he, "hipMalloc(four-step counters)");
-        else p->ws_bytes += (int64_t)sb;
+    if (rc == MFFT_OK && need_f && !p->caller_ws) {
+        he = hipMalloc((void**)&p->ws_f, (size_t)p->fused_bytes);
+        if (he != hipSuccess) rc = hip_fail(he, "hipMalloc(four-step Z ring)");
+        else p->ws_bytes += p->fused_bytes;
+    }
+    if (rc == MFFT_OK && need_f) {
+        // the plan's count of fused-schedule waits that gave up (all launches)
+        he = hipMalloc((void**)&p->overrun, sizeof(int));
+        if (he == hipSuccess) he = hipMemsetAsync(p->overrun, 0, sizeof(int), us);
+        if (he != hipSuccess) rc = hip_fail(he, "hipMalloc(four-step overrun count)");
+        else p->ws_bytes += (int64_t)sizeof(int);
     }
 
     // ---- launch count (per execute)
@@ -630,7 +695,7 @@ int mfft_execute(const mfft_plan* p, const void* in, void* out, void* stream_v) 
                     "the plan was created with MFFT_PLAN_CALLER_WORKSPACE and needs %lld bytes of workspace: "
                     "use mfft_execute_ws",
                     (long long)p->work_bytes);
-    return execute_impl(p, in, out, Work{p->ws_a, p->ws_b}, stream_v);
+    return execute_impl(p, in, out, Work{p->ws_a, p->ws_b, p->ws_f}, stream_v);
 }
 
 int mfft_plan_workspace_size(const mfft_plan* p, int64_t* bytes) {
@@ -645,17 +710,14 @@ int mfft_execute_ws(const mfft_plan* p, const void* in, void* out, void* workspa
     g_err.clear();
     if (!p) return fail(MFFT_ERR_VALUE, "plan must not be NULL");
     if (workspace_bytes < 0) return fail(MFFT_ERR_VALUE, "workspace_bytes must be >= 0");
-    if (p->work_bytes == 0) return execute_impl(p, in, out, Work{nullptr, nullptr}, stream_v);
+    if (p->work_bytes == 0) return execute_impl(p, in, out, Work{nullptr, nullptr, nullptr}, stream_v);
     if (!workspace) return fail(MFFT_ERR_VALUE, "this plan needs %lld bytes of workspace", (long long)p->work_bytes);
     if (workspace_bytes < p->work_bytes)
         return fail(MFFT_ERR_VALUE, "workspace of %lld bytes is smaller than the plan's %lld",
                     (long long)workspace_bytes, (long long)p->work_bytes);
     if (((uintptr_t)workspace) % kWorkAlign)
         return fail(MFFT_ERR_VALUE, "workspace must be %d-byte aligned", (int)kWorkAlign);
-    char* w = (char*)workspace;
-    return execute_impl(p, in, out,
-                        Work{p->need_a ? (float2*)w : nullptr, p->need_b ? (float2*)(w + p->work_b_off) : nullptr},
-                        stream_v, workspace, p->work_bytes);
+    return execute_impl(p, in, out, carve(p, (char*)workspace), stream_v, workspace, p->work_bytes);
 }
 
 int mfft_execute_noalloc(const mfft_plan* p, const void* in, void* out, void* stream_v) {
@@ -666,7 +728,7 @@ int mfft_execute_noalloc(const mfft_plan* p, const void* in, void* out, void* st
                     "this plan needs %lld bytes of scratch, more than the %lld-byte static buffer of "
                     "mfft_execute_noalloc: use mfft_execute or mfft_execute_ws",
                     (long long)p->work_bytes, (long long)MFFT_NOALLOC_SCRATCH_BYTES);
-    if (p->work_bytes == 0) return execute_impl(p, in, out, Work{nullptr, nullptr}, stream_v);
+    if (p->work_bytes == 0) return execute_impl(p, in, out, Work{nullptr, nullptr, nullptr}, stream_v);
     int dev = -1;
     const hipError_t he = hipGetDevice(&dev);
     if (he != hipSuccess) return hip_fail(he, "hipGetDevice");
@@ -675,10 +737,7 @@ int mfft_execute_noalloc(const mfft_plan* p, const void* in, void* out, void* st
     void* ws = nullptr;
     const int rc = noalloc_scratch(dev, &ws);
     if (rc != MFFT_OK) return rc;
-    char* w = (char*)ws;
-    return execute_impl(p, in, out,
-                        Work{p->need_a ? (float2*)w : nullptr, p->need_b ? (float2*)(w + p->work_b_off) : nullptr},
-                        stream_v, ws, p->work_bytes);
+    return execute_impl(p, in, out, carve(p, (char*)ws), stream_v, ws, p->work_bytes);
 }
 
 int mfft_execute_timed(const mfft_plan* p, const void* in, void* out, void* workspace, int64_t workspace_bytes,
@@ -767,9 +826,9 @@ int mfft_plan_sync_overruns(const mfft_plan* p, int64_t* count) {
     g_err.clear();
     if (!p || !count) return fail(MFFT_ERR_VALUE, "plan and count must not be NULL");
     *count = 0;
-    if (!p->sync) return MFFT_OK;
+    if (!p->overrun) return MFFT_OK;
     int v = 0;
-    hipError_t he = hipMemcpy(&v, p->sync + mfft::kFusedOverrun, sizeof(int), hipMemcpyDeviceToHost);
+    hipError_t he = hipMemcpy(&v, p->overrun, sizeof(int), hipMemcpyDeviceToHost);
     if (he != hipSuccess) return hip_fail(he, "hipMemcpy(four-step counters)");
     *count = v;
     return MFFT_OK;

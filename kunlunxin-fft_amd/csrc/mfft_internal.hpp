@@ -22,8 +22,10 @@ struct mfft_plan {
     int64_t n1 = 0, n2 = 0, chunk_rows = 0;
     int schedule = 0;    // FOUR_STEP: 0 one column group per block, 1 persistent, 2 fused (one launch)
     int pass2_rev = 0;   // FOUR_STEP: pass 2 walks the batch rows in reverse order (schedules 0, 1)
-    int fused_lag = 0;   // FOUR_STEP schedule 2: transforms pass 1 runs ahead of pass 2 (0 = from occupancy)
-    int fused_take = 0;  // FOUR_STEP schedule 2: queue items a block takes per dequeue (0 = default)
+    int fused_lag = 0;   // FOUR_STEP schedule 2: transforms pass 1 runs ahead of pass 2
+    int fused_take = 0;  // FOUR_STEP schedule 2: queue items a block takes per dequeue
+    int fused_ring = 0;  // FOUR_STEP schedule 2: Z slots per XCD (>= fused_lag + 1)
+    int fused_grid = 0;  // FOUR_STEP schedule 2: blocks of the launch (resident, a multiple of num_xcc)
     int num_cus = 0;     // compute units of `device` (persistent / fused grid size)
     int clock_khz = 0;   // constant wall-clock rate of `device` (fused schedule wait bound)
     int num_xcc = 8;     // XCDs of `device` (fused schedule work queues)
@@ -42,13 +44,16 @@ struct mfft_plan {
     float2* tw_rb = nullptr;    // real four-step: r2c W_n^(n1 k2) (k2 <= n2); c2r W_n^(n2 n1) (n1 < n1)
     float2* ws_a = nullptr;     // core-sized scratch (real flows: core output / input)
     float2* ws_b = nullptr;     // core-sized scratch (stage-flow ping-pong)
-    int* sync = nullptr;        // fused four-step counters (kFusedSlots, kFusedOverrun, kFusedHead)
+    int* overrun = nullptr;     // fused four-step: waits that gave up, over all launches of the plan
+    char* ws_f = nullptr;       // fused four-step: launch counters, then the Z ring
     int64_t ws_bytes = 0, table_bytes = 0;  // device memory held by the plan
-    // Scratch an execute needs: ws_a and/or ws_b, each core_bytes; caller
-    // workspaces hold ws_a at offset 0 and ws_b at work_b_off.
-    bool need_a = false, need_b = false;
-    int64_t core_bytes = 0, work_b_off = 0, work_bytes = 0;
-    bool caller_ws = false;  // created with MFFT_PLAN_CALLER_WORKSPACE: holds no ws_a / ws_b
+    // Scratch an execute needs: ws_a and/or ws_b, each core_bytes, and the
+    // fused schedule's ws_f (fused_bytes: counters, then the ring at
+    // fused_ring_off); caller workspaces hold ws_a at offset 0, ws_b at
+    // work_b_off and ws_f at work_f_off.
+    bool need_a = false, need_b = false, need_f = false;
+    int64_t core_bytes = 0, work_b_off = 0, work_f_off = 0, fused_bytes = 0, fused_ring_off = 0, work_bytes = 0;
+    bool caller_ws = false;  // created with MFFT_PLAN_CALLER_WORKSPACE: holds no ws_a / ws_b / ws_f
 };
 
 namespace mfft {
@@ -116,14 +121,20 @@ bool fourstep_fused_supported(int log2n1, int log2n2);  // schedule 2: n1, n2 in
 constexpr int kMaxStagger = 16;  // LDS_FUSED start stagger limit (16 x 8128 clocks)
 constexpr int kFusedWaitMs = 20;  // longest pass-2 wait of the fused schedule before it gives up
 constexpr bool kFusedScheduleEnabled = true;
-// fused-schedule counters: [0, kFusedSlots) work queues (one per XCD),
-// [kFusedOverrun] wait overruns, then one per transform of a launch
+// fused-schedule launch counters: [0, kFusedSlots) work queues (one per
+// XCD), [kFusedFail] the launch's failure word, then two per transform of a
+// launch (pass-1 groups done, pass-2 groups done)
 constexpr int kFusedSlots = 16;
-constexpr int kFusedOverrun = kFusedSlots;
+constexpr int kFusedFail = kFusedSlots;
 constexpr int kFusedHead = kFusedSlots + 1;
+constexpr int kFusedFailMark = 1 << 20;  // added to a pass-1 count by a group that skipped its store
+constexpr int kFusedMaxRing = 64;        // Z slots per XCD
+int fourstep_fused_occupancy(int log2n1, int log2n2);  // resident blocks per CU of the fused kernel
 int fourstep_col_loge(int logl);  // log2 elements per thread of a pass of length 2^logl
 void fourstep_default_split(int log2n, int* log2n1, int* log2n2);
-hipError_t launch_fourstep(int dir, const float2* src, float2* dst, const mfft_plan* p,
+// fws: the fused schedule's scratch (counters, then the Z ring), or NULL for
+// the other schedules
+hipError_t launch_fourstep(int dir, const float2* src, float2* dst, char* fws, const mfft_plan* p,
                            int64_t rows, float scale, hipStream_t stream, int* launches);
 // A real transform with the stitch / pre-twiddle fused into the four-step
 // core (plans with real4_fused): R2C x -> permuted Z (work) -> bins;

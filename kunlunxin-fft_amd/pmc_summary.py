@@ -131,6 +131,17 @@ def real_keys(name: str, grid: int, real_sizes) -> list:
             if (rows * core == (grid << loge) and (n1 if kind == 0 else n2) == (1 << logl)
                     and t[3] == (-1 if tt == "r2c" else 1)):
                 keys.append(f"{tt} pass {kind + 1}|N={n}|rows={rows}")
+        elif (name.startswith(("fourstep_r2c_pass", "fourstep_c2r_pass")) and t is not None
+              and s["flow"] == "four-step" and s.get("split")):
+            # the fused real passes: R2C pass 1 / pass 2 (stitch) and C2R
+            # pass 1 (pre-twiddle); <LOGL, LOGE, LOGC>, one block per LOGC
+            # columns of a row, so grid << LOGE points per launch
+            n1, n2, rows = s["split"]
+            logl, loge = t[0], t[1]
+            want, p = {"fourstep_r2c_pass1_kernel": ("r2c", 1), "fourstep_r2c_pass2_kernel": ("r2c", 2),
+                       "fourstep_c2r_pass1_kernel": ("c2r", 1)}[name.split("<")[0]]
+            if tt == want and rows * core == (grid << loge) and (n1 if p == 1 else n2) == (1 << logl):
+                keys.append(f"{tt} pass {p}|N={n}|rows={rows}")
         elif name.startswith(("r2c_stitch_kernel", "c2r_pre_kernel")) and s["flow"] != "lds-fused":
             # around a non-fused core: once per execute, or once per chunk of
             # a chunked four-step core

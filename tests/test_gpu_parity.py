@@ -268,15 +268,20 @@ def test_four_step_fused(gpu, n, n1, b, chunk):
     assert nplan.sync_overruns() == 0
 
 
-@pytest.mark.parametrize("lag,take", [(1, 1), (1, 8), (3, 2), (12, 4), (64, 64)])
-def test_four_step_fused_queue_settings(gpu, lag, take):
-    """The fused schedule's queue lag (params[3] bits 0-7) and items per
-    dequeue (bits 8-15) only reorder work: results are bitwise the same as
-    the default settings, including lags beyond the transforms of a slot."""
+@pytest.mark.parametrize("lag,take,ring,bpc", [(1, 1, 0, 0), (1, 8, 0, 0), (3, 2, 0, 0), (12, 4, 0, 0),
+                                                (63, 64, 0, 0), (1, 1, 2, 1), (2, 2, 6, 2), (3, 1, 4, 3),
+                                                (1, 2, 2, 0), (4, 2, 9, 1)])
+def test_four_step_fused_queue_settings(gpu, lag, take, ring, bpc):
+    """The fused schedule's queue lag (params[3] bits 0-7), items per dequeue
+    (bits 8-15), Z slots per XCD (bits 16-23, at least lag + 1) and blocks
+    per CU (bits 24-30) only reorder work and move Z: results are bitwise the
+    same as the default settings, including lags beyond the transforms of a
+    slot and rings as small as lag + 1 (pass 1 then waits for its slot)."""
     n, b = 1 << 16, 21
     x = torch.from_numpy(seeded_c64(n, b, session=7)).to(gpu)
     ref = execute_fft_plan(mkplan("fft_four_step_batch", n, b, params={"n1": 256, "schedule": 2}), x)
-    p = native.NativePlan(n, b, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 2, lag | (take << 8)))
+    word = lag | (take << 8) | (ring << 16) | (bpc << 24)
+    p = native.NativePlan(n, b, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 2, word))
     y = torch.empty_like(x)
     p.execute(x.data_ptr(), y.data_ptr(), torch.cuda.current_stream(gpu).cuda_stream)
     torch.cuda.synchronize()
@@ -321,6 +326,18 @@ def test_four_step_fused_range(gpu):
         native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 2, 65))
     with pytest.raises(ValueError, match="dequeue"):
         native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 2, 65 << 8))
+    # a ring smaller than lag + 1, or beyond 64 slots; more than 16 blocks per CU
+    with pytest.raises(ValueError, match="Z slots"):
+        native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP,
+                          (256, 0, 2, 3 | (3 << 16)))
+    with pytest.raises(ValueError, match="Z slots"):
+        native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 2, 65 << 16))
+    with pytest.raises(ValueError, match="blocks per CU"):
+        native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 2, 17 << 24))
+    # the ring lives in the workspace: num_xcc x slots x N complex values
+    q = native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP,
+                          (256, 0, 2, 1 | (5 << 16)), caller_workspace=True)
+    assert q.workspace_size() >= 8 * 5 * (1 << 16) * 8
 
 
 # ---------------------------------------------------------------- real flows

@@ -107,6 +107,24 @@ def test_stats_labels_real_transform_launches(tmp_path):
     assert text.count("r2c N=65536") == 2  # pass 1 and the stitch
 
 
+def test_real_keys_label_the_fused_real_passes():
+    """R2C pass 1 / pass 2 (stitch) and C2R pass 1 (pre-twiddle) of the
+    fused real four-step: labelled by transform and pass from their length
+    template argument and the points they cover, never across transforms."""
+    from kunlunxin_fft_amd.pmc_summary import real_keys
+
+    n, b = 1 << 16, 512                  # core 2^15 = n1 256 x n2 128
+    real = [{"n": n, "batch": b, "transform": t, "flow": "four-step", "split": [256, 128, b]}
+            for t in ("r2c", "c2r")]
+    pts = (n // 2) * b
+    assert real_keys("fourstep_r2c_pass1_kernel<8, 4, 4>", pts >> 4, real) == [f"r2c pass 1|N={n}|rows={b}"]
+    assert real_keys("fourstep_r2c_pass2_kernel<7, 3, 4>", pts >> 3, real) == [f"r2c pass 2|N={n}|rows={b}"]
+    assert real_keys("fourstep_c2r_pass1_kernel<8, 4, 4>", pts >> 4, real) == [f"c2r pass 1|N={n}|rows={b}"]
+    # wrong length for the pass, or a grid that covers other points: no label
+    assert real_keys("fourstep_r2c_pass2_kernel<8, 4, 4>", pts >> 4, real) == []
+    assert real_keys("fourstep_r2c_pass1_kernel<8, 4, 4>", pts >> 5, real) == []
+
+
 def test_execute_rows_sum_every_launch_of_one_execute():
     """Per-execute traffic: each launch key counts batch / rows-per-launch
     times, against 16 N (C2C) or 4 N + 8 (N/2+1) (real) bytes per row."""
