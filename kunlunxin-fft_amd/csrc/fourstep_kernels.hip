@@ -55,16 +55,6 @@ __device__ __forceinline__ int pad32_add(int pi, int i) {
     else return pad32(i + K);
 }
 
-// p + bytes for a wave-uniform p and a 32-bit lane offset: the address then
-// takes the scalar-base + 32-bit vector-offset form (one VGPR per access, no
-// 64-bit address arithmetic per element).  Offsets stay below 2^23 bytes
-// because they never leave one transform of at most 2^20 points.
-template <typename T>
-__device__ __forceinline__ T* byte_off(T* p, uint32_t bytes) {
-    using B = std::conditional_t<std::is_const<T>::value, const char, char>;
-    return reinterpret_cast<T*>(reinterpret_cast<B*>(p) + bytes);
-}
-
 // Workgroups are dispatched to the 8 XCDs round-robin (block p -> XCD p % 8),
 // and each XCD has its own L2.  With 8 columns per block a 128-byte row
 // segment is shared by logical blocks 2k and 2k+1; this map puts both on the
@@ -124,13 +114,6 @@ __device__ __forceinline__ int opaque(int x) {
 }
 __device__ __forceinline__ float2 opaque(float2 x) {
     asm volatile("" : "+v"(x.x), "+v"(x.y));
-    return x;
-}
-// For a wave-uniform element offset (kept in SGPRs): stops the loop optimizer
-// from turning per-element addresses into one 64-bit pointer register per
-// access.  (An offset, not a pointer, so the pointer stays a known global one.)
-__device__ __forceinline__ int64_t opaque_uniform(int64_t x) {
-    asm volatile("" : "+s"(x));
     return x;
 }
 

@@ -206,9 +206,27 @@ __device__ __forceinline__ float2 c2r_pre_bin(float2 xk, float2 xj, float2 t) {
     return make_float2(ar - (wr * ci + wi * cr), ai + (wr * cr - wi * ci));
 }
 
+// p + bytes for a wave-uniform p and a 32-bit lane offset: the address then
+// takes the scalar-base + 32-bit vector-offset form (one VGPR per access, no
+// 64-bit address arithmetic per element).  Offsets stay below 2^23 bytes
+// because they never leave one transform of at most 2^20 points (or one
+// twiddle table).
+template <typename T>
+__device__ __forceinline__ T* byte_off(T* p, uint32_t bytes) {
+    using B = std::conditional_t<std::is_const<T>::value, const char, char>;
+    return reinterpret_cast<T*>(reinterpret_cast<B*>(p) + bytes);
+}
+// For a wave-uniform element offset (kept in SGPRs): stops the loop optimizer
+// from turning per-element addresses into one 64-bit pointer register per
+// access.  (An offset, not a pointer, so the pointer stays a known global one.)
+__device__ __forceinline__ int64_t opaque_uniform(int64_t x) {
+    asm volatile("" : "+s"(x));
+    return x;
+}
+
 // Multiply v[OFF + q] (q = 1..R-1) by W^(q*k) of a pass whose table rows
 // `tp[i*NS + k]` hold W^(2^i * k): loads the log2(R) power-of-two roots
-// (coalesced across lanes) and composes the rest, w_q = w_(q - hb) * w_hb,
+// (coalesced across lanes, each a table row plus the lane's offset) and composes the rest, w_q = w_(q - hb) * w_hb,
 // one complex product each.
 // Radix 32 instead multiplies v[q] by w_(2^i) for every set bit i of q, so
 // only log2(R) roots are live (the composed form would hold R of them).
@@ -217,7 +235,9 @@ __device__ __forceinline__ void pass_twiddle(float2 (&v)[E], const float2* __res
     constexpr int LOGR = ilog2(R);
     if constexpr (R <= 16) {
         float2 w[R];
-        static_for<0, LOGR>([&](auto i) { w[1 << i.value] = tp[i.value * ns + k]; });
+        static_for<0, LOGR>([&](auto i) {
+            w[1 << i.value] = *byte_off(tp + opaque_uniform((int64_t)i.value * ns), (uint32_t)k * 8u);
+        });
         static_for<3, R>([&](auto q) {
             constexpr int hb = high_bit(q.value);
             if constexpr (hb != q.value) w[q.value] = cmul(w[q.value - hb], w[hb]);
@@ -225,7 +245,7 @@ __device__ __forceinline__ void pass_twiddle(float2 (&v)[E], const float2* __res
         static_for<1, R>([&](auto q) { v[OFF + q.value] = cmul_tw<DIR>(v[OFF + q.value], w[q.value]); });
     } else {
         static_for<0, LOGR>([&](auto i) {
-            const float2 w = tp[i.value * ns + k];
+            const float2 w = *byte_off(tp + opaque_uniform((int64_t)i.value * ns), (uint32_t)k * 8u);
             static_for<1, R>([&](auto q) {
                 if constexpr ((q.value >> i.value) & 1) v[OFF + q.value] = cmul_tw<DIR>(v[OFF + q.value], w);
             });
