@@ -67,6 +67,22 @@ __device__ __forceinline__ int xcd_pair_block(int p, int total) {
     return (p & ~15) + ((r & 7) << 1) + (r >> 3);
 }
 
+// Whole transforms per XCD: within every full chunk of 8 x `groups` blocks,
+// XCD x (physical blocks 8i + x) takes the `groups` column groups of
+// transform x of the chunk, in order.  For the real passes, whose bin rows
+// hold n/2 + 1 complex values, transform b's grid starts 8b bytes into a
+// 128-byte line, so every column run straddles lines it shares with the
+// neighbouring groups; with all groups of a transform on one XCD, dispatched
+// together, those lines meet in one L2 (measured at N = 2^17: C2R pass-1
+// fetch 298 -> 204 MiB, R2C pass-2 write 162 -> 129 MiB).  A bijection on
+// every full chunk; the tail keeps its order.
+__device__ __forceinline__ int xcd_row_block(int p, int total, int groups) {
+    const int chunk = 8 * groups;
+    if (p >= total - total % chunk) return p;
+    const int local = p % chunk;
+    return (p - local) + (local & 7) * groups + (local >> 3);
+}
+
 template <int LOGL, int LOGE, int LOGC>
 struct ColCfg {
     static_assert(LOGE < LOGL, "a column pass needs more than one thread per column");
@@ -443,7 +459,7 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_r2c_p
     __shared__ float2 lds[C::LDS_FLOAT2];
     const int n1 = 1 << log_s;
     const int groups = n1 >> LOGC;
-    const int bid = xcd_pair_block((int)blockIdx.x, (int)gridDim.x);
+    const int bid = xcd_row_block((int)blockIdx.x, (int)gridDim.x, groups);
     const int64_t row = bid / groups;
     const int g = bid - (int)(row * groups);
     const int tid = threadIdx.x;
@@ -508,7 +524,7 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_c2r_p
     float* const ldsf = reinterpret_cast<float*>(lds);
     const int n2n = 1 << log_s;
     const int groups = n2n >> LOGC;
-    const int bid = xcd_pair_block((int)blockIdx.x, (int)gridDim.x);
+    const int bid = xcd_row_block((int)blockIdx.x, (int)gridDim.x, groups);
     const int64_t row = bid / groups;
     const int g = bid - (int)(row * groups);
     const int tid = threadIdx.x;
