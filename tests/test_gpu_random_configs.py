@@ -7,7 +7,8 @@ row order) from their published ranges (N <= 2^20), then checks the GPU result
 to the north-star gate (rel-L2 and peak-normalised worst element <= 1e-5).
 Sizes stay small enough (N * B <= 2^21) that the whole set runs in seconds.
 A second set drives the real LDS modes through the C ABI with an explicit
-16 or 32 elements per thread.
+16 or 32 elements per thread, and a third the fused four-step schedule with
+random queue and ring settings.
 """
 import numpy as np
 import pytest
@@ -127,6 +128,54 @@ def test_random_real_lds_through_abi(gpu, case, tt, elems, n, b, norm, stagger):
     p.execute(x.data_ptr(), y.data_ptr(), torch.cuda.current_stream(gpu).cuda_stream)
     ref = _reference(h, tt, td, norm, n)
     got = y.cpu().numpy()
+    l2 = oracle.rel_l2(got, ref)
+    mx = oracle.max_rel_error(got, ref)
+    assert l2 <= TOL and mx <= TOL, f"rel_l2={l2:.3e} max_rel={mx:.3e}"
+
+
+def _fused_cases(count=60, seed=77001):
+    """The fused four-step schedule (params[2] = 2) through the C ABI: every
+    split it takes (n1, n2 in [128, 512] within a factor 2), C2C both ways
+    and the real transforms on it, a ragged or chunked batch, a norm, and
+    random queue lag, items per dequeue, Z slots per XCD and workgroups per
+    CU (params[3] bits 0-7, 8-15, 16-23, 24-30)."""
+    rng = np.random.default_rng(seed)
+    splits = ((7, 7), (7, 8), (8, 7), (8, 8), (8, 9), (9, 8), (9, 9))
+    out = []
+    for i in range(count):
+        l1, l2 = splits[int(rng.integers(len(splits)))]
+        tt = ("c2c", "c2c", "r2c", "c2r")[int(rng.integers(4))]
+        logn = l1 + l2 + (1 if tt != "c2c" else 0)
+        b = int(rng.integers(1, min(24, max(1, (1 << 21) >> logn)) + 1))
+        td = "forward" if tt == "r2c" else ("inverse" if tt == "c2r" else ("forward", "inverse")[int(rng.integers(2))])
+        norm = NORMS[int(rng.integers(4))]
+        lag = int(rng.integers(0, 7))
+        take = int(rng.integers(0, 4))
+        ring = 0 if lag == 0 else lag + 1 + int(rng.integers(0, 4))
+        bpc = int(rng.integers(0, 5))
+        chunk = (0, 0, 2, 5)[int(rng.integers(4))]
+        word = lag | (take << 8) | (ring << 16) | (bpc << 24)
+        out.append(pytest.param(i, tt, td, norm, 1 << logn, b, 1 << l1, chunk, word,
+                                id=f"{i}-{tt}-{td}-{norm}-N{1 << logn}-B{b}-n1_{1 << l1}-c{chunk}-w{word:x}"))
+    return out
+
+
+@pytest.mark.parametrize("case,tt,td,norm,n,b,n1,chunk,word", _fused_cases())
+def test_random_fused_schedule(gpu, case, tt, td, norm, n, b, n1, chunk, word):
+    rng = np.random.default_rng(11000 + case)
+    p = native.NativePlan(n, b, tt, td, norm, native.FLOW_FOUR_STEP, (n1, chunk, 2, word))
+    if tt == "r2c":
+        h = rng.standard_normal((b, n)).astype(np.float32)
+        y = torch.full((b, n // 2 + 1), float("nan"), dtype=torch.complex64, device=gpu)
+    else:
+        m = n // 2 + 1 if tt == "c2r" else n
+        h = (rng.standard_normal((b, m)) + 1j * rng.standard_normal((b, m))).astype(np.complex64)
+        y = torch.full((b, n), float("nan"), dtype=torch.float32 if tt == "c2r" else torch.complex64, device=gpu)
+    x = torch.from_numpy(h).to(gpu)
+    p.execute(x.data_ptr(), y.data_ptr(), torch.cuda.current_stream(gpu).cuda_stream)
+    got = y.cpu().numpy()
+    assert p.sync_overruns() == 0
+    ref = _reference(h, tt, td, norm, n)
     l2 = oracle.rel_l2(got, ref)
     mx = oracle.max_rel_error(got, ref)
     assert l2 <= TOL and mx <= TOL, f"rel_l2={l2:.3e} max_rel={mx:.3e}"
