@@ -34,7 +34,8 @@ Also reported (on the same JSON line):
 * ``per_size[].vendor_*``: torch.fft.fft (rocFFT) on the same inputs, a
   comparison column only;
 * ``config5``: the selector sweep (N = 16 .. 2^14, B in {1, 16, 64, 256}):
-  per cell the selected plan's and the M0 incumbent's time per execute and
+  per cell the selected plan's and the M0 incumbent's device time per execute
+  (executes replayed back to back from a HIP graph) and
   whether the selected plan clears the 2% promotion guard in this run;
 * ``cpu_baseline``: the reference's own CPU FFT (butterfly::fft_dit built
   into oracle/_ref; the C restatement when that build is absent) on one core,
@@ -422,8 +423,10 @@ def main() -> int:
 
     # ---- config 5: the selector sweep, N = 16 .. 2^14 x B in {1, 16, 64, 256},
     # forward C2C.  Per cell: the selected plan and the M0 incumbent (fft_dit /
-    # fft_dit_batch), each timed as the table builder times a cell (back-to-back
-    # executes between HIP events, median of rounds), and whether the selected
+    # fft_dit_batch), each timed as the table builder times a cell (20
+    # back-to-back executes replayed from a HIP graph between HIP events,
+    # median of 5 replays: device time, since a host loop of enqueues would
+    # time the host in these launch-bound cells), and whether the selected
     # plan still clears the reference's 2% promotion guard
     # (src/xpu/selector.py:59-63) in this run.
     cfg5 = []
@@ -434,19 +437,7 @@ def main() -> int:
             nplan, (shape, dt) = _resolve(plan, 0)
             out = torch.empty(shape, dtype=dt, device=dev)
             ws = runner.workspace_for(nplan, dev)
-            for _ in range(3):
-                run_native(nplan, x, out, ws)
-            res = []
-            for _ in range(rounds):
-                s = torch.cuda.Event(enable_timing=True)
-                e = torch.cuda.Event(enable_timing=True)
-                s.record(stream)
-                for _ in range(reps):
-                    run_native(nplan, x, out, ws)
-                e.record(stream)
-                e.synchronize()
-                res.append(s.elapsed_time(e) / reps)
-            return statistics.median(res), nplan.flow_name
+            return runner.time_native_graph(nplan, x, out, ws, reps=reps, rounds=rounds), nplan.flow_name
 
         for n in [1 << k for k in range(4, 15)]:
             for b in (1, 16, 64, 256):

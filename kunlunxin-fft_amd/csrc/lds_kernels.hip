@@ -307,7 +307,7 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
             if constexpr (NS > 1) {
                 const int b = j + m.value * T;
                 constexpr int TW_OFF = sched_tw_off(LOGL, C::LE, p, C::RF);
-                pass_twiddle<R, DIR, m.value * R>(v, tw + TW_OFF, NS, b & (NS - 1));
+                pass_twiddle<R, DIR, m.value * R, (C::WG == 1024 && E == 32)>(v, tw + TW_OFF, NS, b & (NS - 1));
             }
             dft<R, DIR, m.value * R, 1>(v);
         });

@@ -226,18 +226,26 @@ __device__ __forceinline__ int64_t opaque_uniform(int64_t x) {
 
 // Multiply v[OFF + q] (q = 1..R-1) by W^(q*k) of a pass whose table rows
 // `tp[i*NS + k]` hold W^(2^i * k): loads the log2(R) power-of-two roots
-// (coalesced across lanes, each a table row plus the lane's offset) and composes the rest, w_q = w_(q - hb) * w_hb,
+// (coalesced across lanes) and composes the rest, w_q = w_(q - hb) * w_hb,
 // one complex product each.
 // Radix 32 instead multiplies v[q] by w_(2^i) for every set bit i of q, so
 // only log2(R) roots are live (the composed form would hold R of them).
-template <int R, int DIR, int OFF, int E>
+// SROW: address each table row as a scalar base plus the lane's 32-bit
+// offset.  Otherwise the compiler forms a 64-bit per-lane pointer per row
+// (row offsets beyond the load's immediate range), which costs the 16-wave
+// 32768-point kernels, at their 128-VGPR budget, a spilled register; where
+// registers are not that scarce the default form schedules better (measured
+// 1-3% faster at 2^10-2^17).
+template <int R, int DIR, int OFF, bool SROW = false, int E>
 __device__ __forceinline__ void pass_twiddle(float2 (&v)[E], const float2* __restrict__ tp, int ns, int k) {
     constexpr int LOGR = ilog2(R);
+    auto root = [&](int i) -> float2 {
+        if constexpr (SROW) return *byte_off(tp + opaque_uniform((int64_t)i * ns), (uint32_t)k * 8u);
+        else return tp[i * ns + k];
+    };
     if constexpr (R <= 16) {
         float2 w[R];
-        static_for<0, LOGR>([&](auto i) {
-            w[1 << i.value] = *byte_off(tp + opaque_uniform((int64_t)i.value * ns), (uint32_t)k * 8u);
-        });
+        static_for<0, LOGR>([&](auto i) { w[1 << i.value] = root(i.value); });
         static_for<3, R>([&](auto q) {
             constexpr int hb = high_bit(q.value);
             if constexpr (hb != q.value) w[q.value] = cmul(w[q.value - hb], w[hb]);
@@ -245,7 +253,7 @@ __device__ __forceinline__ void pass_twiddle(float2 (&v)[E], const float2* __res
         static_for<1, R>([&](auto q) { v[OFF + q.value] = cmul_tw<DIR>(v[OFF + q.value], w[q.value]); });
     } else {
         static_for<0, LOGR>([&](auto i) {
-            const float2 w = *byte_off(tp + opaque_uniform((int64_t)i.value * ns), (uint32_t)k * 8u);
+            const float2 w = root(i.value);
             static_for<1, R>([&](auto q) {
                 if constexpr ((q.value >> i.value) & 1) v[OFF + q.value] = cmul_tw<DIR>(v[OFF + q.value], w);
             });

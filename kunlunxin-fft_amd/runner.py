@@ -487,3 +487,44 @@ def time_call_detailed(fn, *args, warmup: int = 5, trials: int = 50, **kwargs) -
     ev.sort()
     return {"wall_ms_p50": wall[len(wall) // 2], "event_ms_p50": ev[len(ev) // 2],
             "wall_ms_min": wall[0], "trials": trials}
+
+
+def time_native_graph(nplan: native.NativePlan, x: torch.Tensor, out: torch.Tensor, ws, reps: int = 20,
+                      rounds: int = 5) -> float:
+    """Median device time (ms) of one execute of ``nplan``: ``reps`` executes
+    recorded into one HIP graph on a side stream, the graph replayed
+    ``rounds`` times between HIP events on the current stream.
+
+    For launch-bound shapes (a few microseconds per execute) a host loop of
+    enqueues measures the host's enqueue rate instead: the GPU idles between
+    kernels whenever one enqueue takes longer than one kernel.  Replaying a
+    graph launches the executes back to back.  An execute records only
+    kernel launches (no allocation, memset or host sync), so it captures as
+    is; ``ws`` (or None) must be allocated before the call."""
+    dev = x.device
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    wp = ws.data_ptr() if ws is not None else 0
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            nplan.execute_ws(x.data_ptr(), out.data_ptr(), wp, nplan.ws_bytes, side.cuda_stream)
+        side.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            for _ in range(reps):
+                nplan.execute_ws(x.data_ptr(), out.data_ptr(), wp, nplan.ws_bytes, side.cuda_stream)
+    torch.cuda.synchronize(dev)
+    cur = torch.cuda.current_stream(dev)
+    graph.replay()
+    res = []
+    for _ in range(rounds):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record(cur)
+        graph.replay()
+        e.record(cur)
+        e.synchronize()
+        res.append(s.elapsed_time(e) / reps)
+    del graph
+    res.sort()
+    return res[len(res) // 2]

@@ -21,9 +21,10 @@ flow, and stored as exact-semantic entries: the real modes of the LDS kernel
 and the four-step around a half-length core have their own best settings.
 
 Timing: forward C2C complex64 (and the real cells), inputs resident on the GPU.  Cells under
-64 MiB: ``reps`` back-to-back executes bracketed by HIP events on the launch
-stream, median of ``rounds`` such groups (ms per execute, launch gaps
-included).  Larger cells: each execute timed alone after an untimed 256 MiB
+64 MiB: ``reps`` back-to-back executes recorded into one HIP graph, the graph
+replayed between HIP events, median of ``rounds`` replays (ms per execute of
+device time; a host loop of enqueues would time the host in the launch-bound
+cells).  Larger cells: each execute timed alone after an untimed 256 MiB
 write elsewhere, median of ``rounds`` x ``reps / 4``.
 
 Usage (on a GPU box):
@@ -199,7 +200,7 @@ def main() -> int:
     from kunlunxin_fft_amd import envcheck
     from kunlunxin_fft_amd.config import DesignSpace, DeviceProfile
     from kunlunxin_fft_amd.entry import ExecutionPlan
-    from kunlunxin_fft_amd.runner import get_native_plan, output_spec, workspace_for
+    from kunlunxin_fft_amd.runner import get_native_plan, output_spec, time_native_graph, workspace_for
     from kunlunxin_fft_amd.selector import GUARD_PCT
 
     space = DesignSpace.load()
@@ -246,16 +247,10 @@ def main() -> int:
                     e.synchronize()
                     res.append(s.elapsed_time(e))
             return statistics.median(res)
-        for _ in range(args.rounds):
-            s = torch.cuda.Event(enable_timing=True)
-            e = torch.cuda.Event(enable_timing=True)
-            s.record(stream)
-            for _ in range(args.reps):
-                execute()
-            e.record(stream)
-            e.synchronize()
-            res.append(s.elapsed_time(e) / args.reps)
-        return statistics.median(res)
+        # below 64 MiB: device time of back-to-back executes replayed from a
+        # HIP graph (a host loop would time the host's enqueue rate in the
+        # launch-bound cells)
+        return time_native_graph(np_, x, out, ws, reps=args.reps, rounds=args.rounds)
 
     def confirm(timed, n, b, x, row, tt="c2c", td="forward"):
         """The fastest candidate, confirmed: when the runner-up is within
@@ -362,7 +357,8 @@ def main() -> int:
         "profile_hash": DeviceProfile.load().hash(), "env_hash": env_hash,
         "env": {**env, "device_model": env["gfx_arch"]},
         "precision": "fp32", "guard_pct": GUARD_PCT,
-        "selection_semantics": "median of rounds x (reps back-to-back executes / reps), HIP events; "
+        "selection_semantics": "median of rounds x (reps back-to-back executes replayed from a HIP graph / reps), "
+                               "HIP events; "
                                "cells of 64 MiB and more: each execute after an untimed 256 MiB write; "
                                "forward C2C complex64 (legacy entries, answering every semantic), plus "
                                "exact-semantic R2C / C2R entries (norm backward) at the roofline rows",

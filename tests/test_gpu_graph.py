@@ -51,3 +51,34 @@ def test_graph_replay_matches_eager(gpu, n, b, tt, td):
            "r2c": lambda h: np.fft.rfft(h.astype(np.float64)),
            "c2r": lambda h: np.fft.irfft(h.astype(np.complex128), n=n)}[tt](x.cpu().numpy())
     assert oracle.rel_l2(outs[-1].cpu().numpy(), ref) <= 1e-5
+
+
+@pytest.mark.parametrize("name,n,b,params", [("fft_lds_fused", 2048, 1, {}), ("fft_lds_fused_batch", 4096, 64, {}),
+                                             ("fft_dit_batch", 1024, 16, {}),
+                                             ("fft_four_step_batch", 1 << 14, 16, {"n1": 128}),
+                                             ("fft_four_step_batch", 1 << 16, 5, {"n1": 256, "schedule": 2}),
+                                             ("fft_dit_matrix_batch", 4096, 16, {})])
+def test_graph_timer_leaves_the_eager_result(gpu, name, n, b, params):
+    """The table builder's and bench's timer for launch-bound cells
+    (runner.time_native_graph) replays a graph of back-to-back executes into
+    one output: that output must equal an eager execute bit for bit, for every
+    flow the timer meets (stage flow with workspace, LDS, four-step, the fused
+    schedule with its counters and Z ring, dense MFMA)."""
+    from kunlunxin_fft_amd import runner
+
+    nplan = runner.get_native_plan(name, n, b, "c2c", "forward", "backward", None, params, 0)
+    g = torch.Generator(gpu).manual_seed(n + b)
+    x = torch.randn((b, n), dtype=torch.complex64, device=gpu, generator=g)
+    ref = torch.empty_like(x)
+    ws = runner.workspace_for(nplan, gpu)
+    nplan.execute_ws(x.data_ptr(), ref.data_ptr(), ws.data_ptr() if ws is not None else 0, nplan.ws_bytes,
+                     torch.cuda.current_stream(gpu).cuda_stream)
+    torch.cuda.synchronize()
+    out = torch.full_like(x, float("nan"))
+    ms = runner.time_native_graph(nplan, x, out, ws, reps=8, rounds=3)
+    torch.cuda.synchronize()
+    assert ms > 0
+    assert torch.equal(out, ref)
+    check_ref = oracle.c2c(x.cpu().numpy()[:2], "forward", "backward") if n <= 4096 else None
+    if check_ref is not None:
+        assert oracle.rel_l2(out.cpu().numpy()[:2], check_ref) <= 1e-5
