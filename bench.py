@@ -19,7 +19,9 @@ Also reported (on the same JSON line):
   committed rocprofv3 PMC summary (profiles/pmc_traffic.json) when present,
   else null, and its ratio to the algorithmic bytes;
 * ``per_size``: GB/s, fraction of peak and GFLOP/s (5 N log2 N per transform)
-  per N, from HIP events;
+  per N: the median of 100 executes of each size (HIP events, in the step's
+  cyclic order, after the timed steps as warm-up), and each launch's median
+  duration over 20 timed executes;
 * ``latency_n2048_b1``: the reference protocol (warmup 5, 5 x 32 trials,
   device sync per trial, pooled p50, scripts/issue10_wp3_holdout.py:176-190)
   for execute_fft_plan, plus the kernel-only event p50 and the per-transform
@@ -34,9 +36,10 @@ Also reported (on the same JSON line):
 * ``per_size[].vendor_*``: torch.fft.fft (rocFFT) on the same inputs, a
   comparison column only;
 * ``config5``: the selector sweep (N = 16 .. 2^14, B in {1, 16, 64, 256}):
-  per cell the selected plan's and the M0 incumbent's device time per execute
-  (executes replayed back to back from a HIP graph) and
-  whether the selected plan clears the 2% promotion guard in this run;
+  per cell the device time per execute (executes replayed back to back from
+  a HIP graph) of the selected plan, the M0 incumbent and the dense-dot MFMA
+  candidate (the reference's M2 flow), and whether the selected plan clears
+  the 2% promotion guard in this run;
 * ``cpu_baseline``: the reference's own CPU FFT (butterfly::fft_dit built
   into oracle/_ref; the C restatement when that build is absent) on one core,
   on a bounded sample -- 16 transforms of each N = 2^10..2^20 -- median of 5,
@@ -188,8 +191,10 @@ def main() -> int:
         nplan.execute_ws(x.data_ptr(), out.data_ptr(), ws.data_ptr() if ws is not None else 0,
                          nplan.ws_bytes, stream.cuda_stream)
 
+    # 100 cycles (each size's median over 100 executes; the timed steps
+    # before them are the warm-up)
     evs = [[] for _ in work]
-    for _ in range(10):
+    for _ in range(100):
         for i, (n, b, x, plan) in enumerate(work):
             nplan, out, ws = natives[i]
             s = torch.cuda.Event(enable_timing=True)
@@ -203,7 +208,7 @@ def main() -> int:
     # GPU is busy when the timed launches are queued (no host enqueue gap in
     # the first timed interval) and the caches hold other sizes' data
     launch_runs = [[] for _ in work]
-    for _ in range(5):
+    for _ in range(20):
         for i, (n, b, x, plan) in enumerate(work):
             pn, pout, pws = natives[i - 1]
             run_native(pn, work[i - 1][2], pout, pws)
@@ -444,16 +449,26 @@ def main() -> int:
                 x = torch.randn((n,) if b == 1 else (b, n), dtype=torch.complex64, device=dev, generator=gen)
                 sel = pkg.plan_fft("dit", n, batch=b, profile_hash=prof)
                 m0 = pkg.plan_fft("dit", n, batch=b)  # no profile: the M0 closure
+                # the dense-dot MFMA candidate (the reference's M2 flow) in every cell
+                mname = "fft_dit_matrix" + ("_batch" if b > 1 else "")
+                mf = pkg.ExecutionPlan(n=n, batch=b, direction="dit", precision="fp32", selection_source="table",
+                                       reason="bench.py config-5 MFMA candidate", fallback=False, executed=mname,
+                                       block=256, flow_id="bench", flow_realization="bench",
+                                       processing_unit="bench", params={})
                 sel_ms, sel_flow = cell_ms(sel, x)
                 m0_ms, _ = cell_ms(m0, x)
+                mf_ms, mf_flow = cell_ms(mf, x)
                 row = {"n": n, "batch": b, "selected": sel.executed, "selected_flow": sel_flow,
                        "selection_source": sel.selection_source, "selected_us": round(sel_ms * 1e3, 2),
                        "m0": m0.executed, "m0_us": round(m0_ms * 1e3, 2),
                        "speedup_vs_m0": round(m0_ms / sel_ms, 2),
+                       "mfma_candidate": mname, "mfma_flow": mf_flow, "mfma_us": round(mf_ms * 1e3, 2),
+                       "mfma_over_selected": round(mf_ms / sel_ms, 2),
                        "guard_pct": guard, "clears_guard": bool(sel_ms <= m0_ms * (1 - guard / 100.0))}
                 cfg5.append(row)
                 log(f"config5 N={n:>6} B={b:>4} {sel.executed:>22} {row['selected_us']:8.2f} us "
-                    f"M0 {row['m0_us']:8.2f} us  x{row['speedup_vs_m0']:.2f} guard={'ok' if row['clears_guard'] else 'NO'}")
+                    f"M0 {row['m0_us']:8.2f} us  x{row['speedup_vs_m0']:.2f} guard={'ok' if row['clears_guard'] else 'NO'}"
+                    f"  MFMA {row['mfma_us']:8.2f} us")
                 del x
         torch.cuda.synchronize()
 
