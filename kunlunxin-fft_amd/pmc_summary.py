@@ -127,10 +127,12 @@ def real_keys(name: str, grid: int, real_sizes) -> list:
         elif name.startswith("fourstep_pass_kernel") and t is not None and s["flow"] == "four-step" and s.get("split"):
             n1, n2, rows = s["split"]
             logl, loge, kind = t[0], t[1], t[4]
-            # r2c runs a forward core (DIR -1), c2r an inverse one (DIR +1)
-            if (rows * core == (grid << loge) and (n1 if kind == 0 else n2) == (1 << logl)
-                    and t[3] == (-1 if tt == "r2c" else 1)):
-                keys.append(f"{tt} pass {kind + 1}|N={n}|rows={rows}")
+            # the plain pass serves one real launch: C2R's pass 2, the
+            # inverse (DIR +1) row pass; R2C's passes and C2R's pass 1 are
+            # the fused real kernels below
+            if (tt == "c2r" and kind == 1 and t[3] == 1 and rows * core == (grid << loge)
+                    and n2 == (1 << logl)):
+                keys.append(f"{tt} pass 2|N={n}|rows={rows}")
         elif (name.startswith(("fourstep_r2c_pass", "fourstep_c2r_pass")) and t is not None
               and s["flow"] == "four-step" and s.get("split")):
             # the fused real passes: R2C pass 1 / pass 2 (stitch) and C2R

@@ -76,17 +76,19 @@ def test_stats_one_row_per_launch_shape(tmp_path):
 def test_stats_labels_real_transform_launches(tmp_path):
     """The real-transform leg: LDS R2C/C2R instances, four-step passes over
     the half-length core and the standalone stitch kernel are labelled from
-    real_per_size."""
+    real_per_size; a plain forward pass of the same shape is not an R2C
+    launch."""
     d = tmp_path / "trace"
     d.mkdir()
     r2c = "void mfft::(anonymous namespace)::lds_fft_kernel<9, 4, -1, 1>(void const*, void*, float)"
-    p1 = "void mfft::(anonymous namespace)::fourstep_pass_kernel<8, 4, 4, -1, 0>(float2 const*, int)"
+    p1 = "void mfft::(anonymous namespace)::fourstep_r2c_pass1_kernel<8, 4, 4>(float2 const*, int)"
+    plain = "void mfft::(anonymous namespace)::fourstep_pass_kernel<8, 4, 4, -1, 0>(float2 const*, int)"
     st = "void mfft::(anonymous namespace)::r2c_stitch_kernel(float2 const*, float2*, float2 const*, long, int, float)"
     n_lds, b_lds = 1024, 32768           # core 512: 2^24 points, 16 per thread
     n_fs, b_fs = 1 << 16, 512            # core 2^15 = 256 x 128
     bpr = ((n_fs // 4) + 1 + 255) // 256
     rows = [(r2c, (n_lds // 2) * b_lds // 16, 50_000), (p1, (n_fs // 2) * b_fs // 16, 60_000),
-            (st, bpr * b_fs * 256, 53_000)]
+            (st, bpr * b_fs * 256, 53_000), (plain, (n_fs // 2) * b_fs // 16, 61_000)]
     with open(d / "run_kernel_trace.csv", "w", newline="") as f:
         w = csv.writer(f)
         w.writerow(["Kernel_Name", "Start_Timestamp", "End_Timestamp", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z"])
@@ -105,6 +107,7 @@ def test_stats_labels_real_transform_launches(tmp_path):
     assert "| r2c N=1024\\|rows=32768 |" in text
     assert "| r2c N=65536\\|rows=512 |" in text
     assert text.count("r2c N=65536") == 2  # pass 1 and the stitch
+    assert "| fourstep_pass_kernel<8, 4, 4, -1, 0> | 1048576 | - |" in text
 
 
 def test_real_keys_label_the_fused_real_passes():
@@ -123,6 +126,11 @@ def test_real_keys_label_the_fused_real_passes():
     # wrong length for the pass, or a grid that covers other points: no label
     assert real_keys("fourstep_r2c_pass2_kernel<8, 4, 4>", pts >> 4, real) == []
     assert real_keys("fourstep_r2c_pass1_kernel<8, 4, 4>", pts >> 5, real) == []
+    # the plain row pass: C2R's inverse pass 2 only; a forward one of the
+    # same shape is a C2C launch, not an R2C pass
+    assert real_keys("fourstep_pass_kernel<7, 3, 4, 1, 1>", pts >> 3, real) == [f"c2r pass 2|N={n}|rows={b}"]
+    assert real_keys("fourstep_pass_kernel<7, 3, 4, -1, 1>", pts >> 3, real) == []
+    assert real_keys("fourstep_pass_kernel<8, 4, 4, 1, 0>", pts >> 4, real) == []
 
 
 def test_execute_rows_sum_every_launch_of_one_execute():
