@@ -37,6 +37,7 @@ from __future__ import annotations
 import math
 import threading
 import time
+import weakref
 from collections import OrderedDict
 
 import torch
@@ -279,7 +280,10 @@ def run(executed: str, x: torch.Tensor, batch: int, n: int, transform_type: str 
 # counts as those roots: the reference builds them from a float32 angle
 # (runner.py:93-97), which is off by up to ~2e-7 at N = 2^20.
 TWIDDLE_TOL = 1e-6
-_TWIDDLE_OK: dict = {}  # (ptrs, versions, n, device) of tables already checked
+# tables already checked: (ptrs, versions, n, device) -> weak references to
+# the two tensors, so that a later table at a reused address is not taken
+# for the one that was checked
+_TWIDDLE_OK: dict = {}
 
 
 def check_twiddle(twiddle, x) -> None:
@@ -289,14 +293,16 @@ def check_twiddle(twiddle, x) -> None:
     table of those roots (built once per plan); any other table would ask
     for a different transform, which the library does not run, so it raises
     ValueError instead of silently using its own.  The value check costs one
-    device round trip per distinct table and is then remembered."""
+    device round trip per distinct table and is then remembered for the same
+    two tensor objects at the same version (an in-place write bumps it)."""
     if twiddle is None:
         return
     n = x.numel() if x.dim() == 1 else int(x.shape[-1])
     validate_twiddle(twiddle, n, x.device)
     wr, wi = twiddle
     key = (wr.data_ptr(), wi.data_ptr(), wr._version, wi._version, n, str(x.device))
-    if key in _TWIDDLE_OK:
+    seen = _TWIDDLE_OK.get(key)
+    if seen is not None and seen[0]() is wr and seen[1]() is wi:
         return
     idx = torch.arange(n >> 1, dtype=torch.float64, device=x.device)
     ang = -2.0 * math.pi * idx / n
@@ -308,7 +314,7 @@ def check_twiddle(twiddle, x) -> None:
                          "builds and keeps its own table of them)")
     if len(_TWIDDLE_OK) > 64:
         _TWIDDLE_OK.clear()
-    _TWIDDLE_OK[key] = True
+    _TWIDDLE_OK[key] = (weakref.ref(wr), weakref.ref(wi))
 
 
 def _single(name, x, block, params=None, twiddle=None):

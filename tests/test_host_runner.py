@@ -149,7 +149,17 @@ def test_twiddle_contract_on_host_tensors():
         if n > 2:
             with pytest.raises(ValueError, match="differs"):
                 check_twiddle((wr, -twiddle_tables(n, "cpu")[1]), x)
+    # a checked table is remembered for its own tensor objects only: another
+    # tensor at the same address and version (here a detached alias, written
+    # through .data, which leaves the version alone) is checked again
     x = torch.zeros(16, dtype=torch.complex64)
+    wr, wi = twiddle_tables(16, "cpu")
+    check_twiddle((wr, wi), x)
+    alias = wi.detach()
+    assert alias.data_ptr() == wi.data_ptr() and alias._version == wi._version
+    alias.data[1] += 10 * TWIDDLE_TOL
+    with pytest.raises(ValueError, match="differs"):
+        check_twiddle((wr, alias), x)
     wr, wi = twiddle_tables(16, "cpu")
     with pytest.raises(ValueError, match="length"):
         check_twiddle((wr[:4], wi[:4]), x)
