@@ -319,6 +319,20 @@ __device__ __forceinline__ int pair_col(int g, int c, int n) {
 }
 // lane column that holds the mirror values of lane column c
 __device__ __forceinline__ int mirror_lane_col(int g, int c) { return (g == 0 && (c & 7) == 0) ? c : (c ^ 8); }
+// Thread layout of the real passes: the four 16-lane row sets of wave w are
+// 2w, 2w + 1, T - 1 - 2w and T - 2 - 2w (jj = tid >> 4), so that the rows of
+// thread j and of its mirror thread T - 1 - j sit in lanes l and l ^ 32 of one
+// wave (and their mirror columns c and c ^ 8 in lanes l and l ^ 40).
+template <int T>
+__device__ __forceinline__ int mirror_row_set(int jj) {
+    static_assert(T % 4 == 0, "a wave holds four 16-lane row sets");
+    return (jj & 2) ? T - 1 - 2 * (jj >> 2) - (jj & 1) : 2 * (jj >> 2) + (jj & 1);
+}
+// x as held by the lane at byte address `from` (lane * 4) of this wave
+__device__ __forceinline__ float2 lane_value(float2 x, int from) {
+    return make_float2(__int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(x.x))),
+                       __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(x.y))));
+}
 // R2C: pass 1 stores Z with its k1 positions permuted so that position
 // 16g + c holds k1 = pair_col(g, c, N1): pass 2 then reads 8 mirror pairs
 // as one aligned 16-column run.  k1 stored at position `pos`:
@@ -441,20 +455,24 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_r2c_p
 // R2C pass 2 with the stitch (kernels.py:1127-1177 formula, r2c_bin): the
 // row pass of the half-length core over one aligned 16-column run of the
 // permuted Z (8 mirror pairs), then every output bin from its core value and
-// its mirror's, written to the n/2 + 1 bins of the row.  The mirror values
-// cross lanes through LDS in two rounds: lane columns 8..15 write and 0..7
-// read, then the other way round (a pair-0 column reads its own values in
-// the round it writes them).  A reading thread stitches and stores its bins
-// at once, so no thread needs room for the mirror values.  The bin twiddle
-// exp(-2 pi i k / n), k = k1 + N1 k2, is tw_a[k1] * tw_b[k2]; the thread
-// holding k = 0 also writes bin n/2.
+// its mirror's, written to the n/2 + 1 bins of the row.  After the last
+// Stockham pass thread j holds k2 = j + m T + q NS (element e = m R + q); the
+// mirror of (k1, k2) is (n1 - k1, N2 - 1 - k2): element E - 1 - e of thread
+// T - 1 - j in lane column c ^ 8, which the thread layout (mirror_row_set)
+// puts at lane ^ 40 of the same wave, one ds_bpermute per component away.
+// Two columns of group 0 mirror onto themselves: k1 = n1/2 (lane column 8;
+// partner lane ^ 32) and k1 = 0 (lane column 0), whose k2 pairs with
+// N2 - k2 of another wave: its lanes store their bins again from a copy of
+// the column in LDS, and the thread holding k = 0 also writes bin n/2.
+// The bin twiddle exp(-2 pi i k / n), k = k1 + n1 k2, is
+// tw_a[k1] tw_b[j] exp(-2 pi i K / (2 N2)), K = k2 - j.
 template <int LOGL, int LOGE, int LOGC>
 __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_r2c_pass2_kernel(
     const float2* src, float2* dst, const float2* __restrict__ tw, const float2* __restrict__ tw_a,
     const float2* __restrict__ tw_b, int logn, int log_s, float scale) {
     using C = ColCfg<LOGL, LOGE, LOGC>;
     static_assert(LOGC == 4, "mirror pairs span 16 lane columns");
-    constexpr int N2 = C::L;
+    constexpr int N2 = C::L, E = C::E;
     __shared__ float2 lds[C::LDS_FLOAT2];
     const int n1 = 1 << log_s;
     const int groups = n1 >> LOGC;
@@ -463,52 +481,69 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_r2c_p
     const int g = bid - (int)(row * groups);
     const int tid = threadIdx.x;
     const int c = tid & (C::C - 1);
-    const int j = tid >> LOGC;
+    const int j = mirror_row_set<C::T>(tid >> LOGC);
     const int64_t np = (int64_t)1 << logn;  // core length L = n/2
-    float2 v[C::E];
+    float2 v[E];
     col_load<C>(v, src + (row << logn) + (g << LOGC), c, j, log_s);
     col_passes<C, -1, 1, false>(v, lds, tw, c, j, [&] { return BigTw<C>{}; });
-    const int mc = mirror_lane_col(g, c);
     const int k1 = pair_col(g, c, n1);
-    const bool col0 = g == 0 && c == 0;  // k1 = 0: mirror rows N2 - k2 of its own column
-    const float2 ta = tw_a[k1];
-    float2* xo = dst + row * (np + 1);
-    static_for<0, 2>([&](auto rnd) {
-        __syncthreads();  // the previous readers of this LDS are done
-        if (rnd.value == 0 ? c >= 8 : c < 8) {
-            float2* lt = lds + (c & 7) * C::PITCH;
-            static_for<0, C::NB_LAST>([&](auto m) {
-                static_for<0, C::R_LAST>([&](auto q) {
-                    lt[pad(j + m.value * C::T + q.value * C::NS_LAST)] = v[m.value * C::R_LAST + q.value];
-                });
-            });
+    const bool col0 = g == 0 && c == 0;
+    float2* xo = dst + row * (np + 1) + k1;
+    // K = k2 - j of element e
+    auto kof = [](int e) { return (e / C::R_LAST) * C::T + (e % C::R_LAST) * C::NS_LAST; };
+    if (g == 0) {  // block-uniform: column 0's values to LDS
+        __syncthreads();  // the last pass's LDS reads are done
+        if (c == 0) {
+            static_for<0, E>([&](auto e) { lds[j + kof(e.value)] = v[e.value]; });
         }
         __syncthreads();
-        if (rnd.value == 0 ? mc >= 8 : mc < 8) {
-            const float2* lm = lds + (mc & 7) * C::PITCH;
-            static_for<0, C::NB_LAST>([&](auto m) {
-                static_for<0, C::R_LAST>([&](auto q) {
-                    const int k2 = j + m.value * C::T + q.value * C::NS_LAST;
-                    const int r = col0 ? ((N2 - k2) & (N2 - 1)) : (N2 - 1 - k2);
-                    const float2 z = v[m.value * C::R_LAST + q.value];
-                    const int64_t k = k1 + (int64_t)n1 * k2;
-                    xo[k] = r2c_bin(z, lm[pad(r)], cmul(ta, tw_b[k2]), scale, k == 0);
-                });
-            });
-            if (col0 && j == 0) xo[np] = r2c_bin(v[0], v[0], cmul(ta, tw_b[N2]), scale, true);
-        }
+    }
+    const int from = ((tid & 63) ^ (g == 0 && c == 8 ? 32 : 40)) << 2;
+    const float2 tj = cmul(tw_a[k1], tw_b[j]);
+    // every lane stitches with its partner's values, without branches (column
+    // 0's lanes store bins that they overwrite below)
+    static_for<0, E / 2>([&](auto h) {
+        constexpr int e0 = h.value, e1 = E - 1 - h.value;
+        constexpr int K0 = kof(e0), K1 = kof(e1);
+        const float2 m0 = lane_value(v[e1], from);  // the partner's element e1: the mirror of this e0
+        const float2 m1 = lane_value(v[e0], from);
+        xo[(int64_t)n1 * (j + K0)] = r2c_bin(v[e0], m0, rot<2 * N2, K0, -1>(tj), scale, false);
+        xo[(int64_t)n1 * (j + K1)] = r2c_bin(v[e1], m1, rot<2 * N2, K1, -1>(tj), scale, false);
     });
+    if (col0) {
+        // addresses from an opaque copy of j: shared with the loop above, all
+        // of them would stay in registers across it
+        const int jc = opaque(j);
+        static_for<0, E>([&](auto e) {
+            constexpr int K = kof(e.value);
+            const int k2 = jc + K;
+            xo[(int64_t)n1 * k2] = r2c_bin(v[e.value], lds[(N2 - k2) & (N2 - 1)], rot<2 * N2, K, -1>(tj), scale,
+                                           K == 0 && jc == 0);
+            __builtin_amdgcn_sched_barrier(0);  // one element's read at a time
+        });
+        if (j == 0) xo[np] = r2c_bin(v[0], v[0], cmul(tw_a[0], tw_b[N2]), scale, true);
+    }
 }
 
 // C2R pass 1 with the pre-twiddle (kernels.py:1180-1229 formula,
 // c2r_pre_bin): the workgroup loads 8 columns of the n/2 + 1 bins and their
-// 8 mirror columns (pair_col), exchanges the mirror rows through LDS one
-// component at a time, turns every bin into its core input, then runs the
-// column pass of the half-length inverse core with its four-step twiddle and
-// stores Z in place of the output row (the row pass runs in place there).
-// The pre-twiddle root exp(-2 pi i n / n_real), n = n1 N2 + n2, is
-// tw_a[n2] * tw_b[n1]; bin n/2, the mirror of bin 0, is loaded by the thread
+// 8 mirror columns (pair_col), turns every bin into its core input with its
+// mirror's value, then runs the column pass of the half-length inverse core
+// with its four-step twiddle and stores Z in place of the output row (the row
+// pass runs in place there).
+// The mirror of bin (n1, n2) is (N1 - 1 - n1, N2 - n2), and thread j's rows
+// j + m T + q N1/R0 (element e = m R0 + q) have their mirrors in element
+// E - 1 - e of thread T - 1 - j, lane column c ^ 8.  Threads are laid out so
+// that a wave holds the row sets 2w, 2w + 1, T - 1 - 2w and T - 2 - 2w (16
+// lanes each), so that partner is lane ^ 40 of the same wave and each mirror
+// value is one ds_bpermute per component away: no LDS round and no copy of
+// the mirror values in registers.  Two columns of group 0 mirror onto
+// themselves: column N2/2 (lane column 8; partner lane ^ 32) and column 0
+// (lane column 0), whose row n1 pairs with row N1 - n1 of another wave and
+// goes through LDS; bin n/2, the mirror of bin 0, is loaded by the thread
 // that holds bin 0, and the imaginary parts of both are ignored.
+// The pre-twiddle root exp(-2 pi i n / n_real), n = n1 N2 + n2, is
+// tw_a[n2] * tw_b[n1].
 template <int LOGL, int LOGE, int LOGC>
 __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_c2r_pass1_kernel(
     const float2* src, float2* dst, const float2* __restrict__ tw, const float2* __restrict__ tw_lo,
@@ -519,8 +554,8 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_c2r_p
     constexpr int N1 = C::L;
     constexpr int R0 = 1 << C::logr(0);
     constexpr int NB0 = C::E / R0;
+    constexpr int E = C::E;
     __shared__ float2 lds[C::LDS_FLOAT2];
-    float* const ldsf = reinterpret_cast<float*>(lds);
     const int n2n = 1 << log_s;
     const int groups = n2n >> LOGC;
     const int bid = xcd_row_block((int)blockIdx.x, (int)gridDim.x, groups);
@@ -528,13 +563,12 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_c2r_p
     const int g = bid - (int)(row * groups);
     const int tid = threadIdx.x;
     const int c = tid & (C::C - 1);
-    const int j = tid >> LOGC;
+    const int j = mirror_row_set<C::T>(tid >> LOGC);
     const int64_t np = (int64_t)1 << logn;
     const int n2 = pair_col(g, c, n2n);
-    const int mc = mirror_lane_col(g, c);
     const bool col0 = g == 0 && c == 0;  // n2 = 0: mirror rows N1 - n1 of its own column, bin n/2 for n1 = 0
     const float2* xr = src + row * (np + 1);
-    float2 v[C::E];
+    float2 v[E];
     // pass-0 operand rows n1 = j + m T + q N1/R0 of column n2 (non-temporal:
     // each bin is read once)
     const uint32_t lane = (uint32_t)(n2 + (j << log_s)) * 8u;
@@ -545,39 +579,46 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_c2r_p
         });
     });
     const float2 xny = (col0 && j == 0) ? load_nt(xr + np) : make_float2(0.0f, 0.0f);
-    // mirror rows through LDS, real parts, then imaginary parts
-    float mre[C::E];
-    const int pf = C::PITCHF;
-    static_for<0, 2>([&](auto comp) {
-        if constexpr (comp.value > 0) __syncthreads();  // the real parts have been read
-        static_for<0, NB0>([&](auto m) {
-            static_for<0, R0>([&](auto q) {
-                const int n1 = j + m.value * C::T + q.value * (N1 / R0);
-                const float2 x = v[m.value * R0 + q.value];
-                ldsf[c * pf + pad32(n1)] = comp.value == 0 ? x.x : x.y;
-            });
-        });
+    // K of element e: its row is n1 = j + K
+    auto kof = [](int e) { return (e / R0) * C::T + (e % R0) * (N1 / R0); };
+    if (g == 0) {  // block-uniform: column 0's rows through LDS
+        if (c == 0) {
+            static_for<0, E>([&](auto e) { lds[j + kof(e.value)] = v[e.value]; });
+        }
         __syncthreads();
-        static_for<0, NB0>([&](auto m) {
-            static_for<0, R0>([&](auto q) {
-                constexpr int e = m.value * R0 + q.value;
-                const int n1 = j + m.value * C::T + q.value * (N1 / R0);
-                const int r = col0 ? ((N1 - n1) & (N1 - 1)) : (N1 - 1 - n1);
-                const float y = ldsf[mc * pf + pad32(r)];
-                if constexpr (comp.value == 0) {
-                    mre[e] = y;
-                } else {
-                    float2 xk = v[e];
-                    float2 xj = make_float2(mre[e], y);
-                    if (col0 && n1 == 0) {  // bin 0 pairs with bin n/2; both imaginary parts ignored
-                        xj = make_float2(xny.x, 0.0f);
-                        xk.y = 0.0f;
-                    }
-                    v[e] = c2r_pre_bin(xk, xj, cmul(tw_a[n2], tw_b[n1]));
-                }
-            });
-        });
+    }
+    const int from = ((tid & 63) ^ (g == 0 && c == 8 ? 32 : 40)) << 2;
+    // the root of row j + K is tw_a[n2] tw_b[j] exp(-2 pi i K / (2 N1)): one
+    // table product per thread, then compile-time rotations (K = m T + q N1/R0)
+    const float2 tj = cmul(tw_a[n2], tw_b[j]);
+    // every lane from its partner's values, without branches (a branch per
+    // pair lets the compiler sink each pair's arithmetic below the last one,
+    // holding every mirror value at once) ...
+    static_for<0, E / 2>([&](auto h) {
+        constexpr int e0 = h.value, e1 = E - 1 - h.value;
+        constexpr int k0 = kof(e0), k1 = kof(e1);
+        const float2 m0 = lane_value(v[e1], from);  // the partner's element e1: the mirror of this e0
+        const float2 m1 = lane_value(v[e0], from);
+        v[e0] = c2r_pre_bin(v[e0], m0, rot<2 * N1, k0, -1>(tj));
+        v[e1] = c2r_pre_bin(v[e1], m1, rot<2 * N1, k1, -1>(tj));
     });
+    // ... then column 0 again, from the copy of its rows in LDS
+    if (col0) {
+        static_for<0, E>([&](auto e) {
+            constexpr int k = kof(e.value);
+            const int r = j + k;
+            float2 x = lds[r];
+            float2 m = lds[(N1 - r) & (N1 - 1)];
+            if constexpr (k == 0) {
+                if (j == 0) {  // bin 0 pairs with bin n/2; both imaginary parts ignored
+                    m = make_float2(xny.x, 0.0f);
+                    x.y = 0.0f;
+                }
+            }
+            v[e.value] = c2r_pre_bin(x, m, rot<2 * N1, k, -1>(tj));
+            __builtin_amdgcn_sched_barrier(0);  // one element's reads at a time
+        });
+    }
     col_passes<C, 1, 0, true>(v, lds, tw, c, j, [&] {
         BigTw<C> f;
         big_tw_load<C>(f, tw_lo, tw_hi, tw_h, (uint32_t)n2, j);
