@@ -317,8 +317,6 @@ __device__ __forceinline__ int pair_col(int g, int c, int n) {
     const int p = 8 * g + (c & 7);
     return c < 8 ? p : (p ? n - p : n >> 1);
 }
-// lane column that holds the mirror values of lane column c
-__device__ __forceinline__ int mirror_lane_col(int g, int c) { return (g == 0 && (c & 7) == 0) ? c : (c ^ 8); }
 // Thread layout of the real passes: the four 16-lane row sets of wave w are
 // 2w, 2w + 1, T - 1 - 2w and T - 2 - 2w (jj = tid >> 4), so that the rows of
 // thread j and of its mirror thread T - 1 - j sit in lanes l and l ^ 32 of one

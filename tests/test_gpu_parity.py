@@ -757,7 +757,8 @@ def test_plan_info_reports_flows(gpu):
 
 
 # ------------------------------------------- real transforms fused into the four-step
-REAL4_SPLITS = [(512, 16), (1 << 12, 16), (1 << 12, 128), (1 << 15, 16), (1 << 15, 1024), (1 << 15, 128),
+REAL4_SPLITS = [(512, 16), (1 << 11, 32), (1 << 13, 64), (1 << 12, 16), (1 << 12, 128), (1 << 15, 16),
+                (1 << 15, 1024), (1 << 15, 128),
                 (1 << 17, 256), (1 << 18, 512), (1 << 19, 1024), (1 << 20, 512), (1 << 20, 1024)]
 
 
