@@ -491,20 +491,26 @@ def main() -> int:
             kinds.add(kind_mt)
             tot_mt += s_mt
             tot_bytes += 16 * n * rows
-        model = "unknown"
+        # the first processor's identity: a virtual machine's model name can
+        # be as short as "AMD EPYC", so vendor, family, model and clock too
+        info = {}
         try:
             for ln in open("/proc/cpuinfo"):
-                if ln.startswith("model name"):
-                    model = ln.split(":", 1)[1].strip()
+                if not ln.strip():
                     break
+                k, _, v = ln.partition(":")
+                info.setdefault(k.strip(), v.strip())
         except OSError:
             pass
+        model = info.get("model name", "unknown")
+        cpu_id = " ".join(f"{k} {info[k]}" for k in ("vendor_id", "cpu family", "model", "stepping", "cpu MHz")
+                          if k in info)
         try:
             usable = len(os.sched_getaffinity(0))
         except (AttributeError, OSError):
             usable = os.cpu_count() or 1
         cpu = {"value": round(tot_bytes / tot_s / 1e9, 4), "unit": "GB/s", "cores": 1,
-               "cpu_model": model, "host_cpus": os.cpu_count(), "usable_cpus": usable,
+               "cpu_model": model, "cpu_id": cpu_id, "host_cpus": os.cpu_count(), "usable_cpus": usable,
                "kind": "reference" if kinds == {"reference"} else "port",
                "sample": f"{rows} transforms of each N = 2^10..2^20 (complex<double>, butterfly::fft_dit "
                          f"with its per-stage twiddle rebuild), median of 5 passes, {tot_s:.1f} s per pass",
