@@ -160,6 +160,50 @@ def _fused_cases(count=60, seed=77001):
     return out
 
 
+def _real4_cases(count=80, seed=31337):
+    """R2C / C2R on the four-step with the stitch and the pre-twiddle inside
+    the passes (schedule 0): a random valid split of the half-length core
+    (both passes 16..1024 points), a random norm, a ragged batch, and random
+    batch chunks."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        tt = ("r2c", "c2r")[int(rng.integers(2))]
+        logn = int(rng.integers(9, 21))
+        logc = logn - 1
+        l1 = int(rng.integers(max(4, logc - 10), min(10, logc - 4) + 1))
+        b = int(rng.integers(1, min(24, max(1, (1 << 22) >> logn)) + 1))
+        chunk = (0, 0, 1, 2, 3, 5)[int(rng.integers(6))]
+        norm = NORMS[int(rng.integers(4))]
+        td = "forward" if tt == "r2c" else "inverse"
+        out.append(pytest.param(i, tt, td, norm, 1 << logn, b, 1 << l1, chunk,
+                                id=f"{i}-{tt}-{norm}-N{1 << logn}-B{b}-n1_{1 << l1}-c{chunk}"))
+    return out
+
+
+@pytest.mark.parametrize("case,tt,td,norm,n,b,n1,chunk", _real4_cases())
+def test_random_real_four_step(gpu, case, tt, td, norm, n, b, n1, chunk):
+    """Every bin written (outputs start as NaN), against numpy, through the
+    C ABI, with the two fused passes per chunk."""
+    rng = np.random.default_rng(13000 + case)
+    p = native.NativePlan(n, b, tt, td, norm, native.FLOW_FOUR_STEP, (n1, chunk, 0))
+    chunks = -(-b // chunk) if chunk and chunk < b else 1
+    assert p.info.launches == 2 * chunks
+    if tt == "r2c":
+        h = rng.standard_normal((b, n)).astype(np.float32)
+        y = torch.full((b, n // 2 + 1), float("nan"), dtype=torch.complex64, device=gpu)
+    else:
+        h = (rng.standard_normal((b, n // 2 + 1)) + 1j * rng.standard_normal((b, n // 2 + 1))).astype(np.complex64)
+        y = torch.full((b, n), float("nan"), dtype=torch.float32, device=gpu)
+    x = torch.from_numpy(h).to(gpu)
+    p.execute(x.data_ptr(), y.data_ptr(), torch.cuda.current_stream(gpu).cuda_stream)
+    got = y.cpu().numpy()
+    ref = _reference(h, tt, td, norm, n)
+    l2 = oracle.rel_l2(got, ref)
+    mx = oracle.max_rel_error(got, ref)
+    assert l2 <= TOL and mx <= TOL, f"rel_l2={l2:.3e} max_rel={mx:.3e}"
+
+
 @pytest.mark.parametrize("case,tt,td,norm,n,b,n1,chunk,word", _fused_cases())
 def test_random_fused_schedule(gpu, case, tt, td, norm, n, b, n1, chunk, word):
     rng = np.random.default_rng(11000 + case)
