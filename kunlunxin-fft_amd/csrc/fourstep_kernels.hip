@@ -309,22 +309,30 @@ __device__ __forceinline__ void col_passes(float2 (&v)[C::E], float2* lds, const
 // (0, N2 - k2); on the (n1, n2) grid of pass 1 (n = n1 N2 + n2) the mirror of
 // (n1, n2) is (N1 - 1 - n1, N2 - n2), and of (n1, 0) it is (N1 - n1, 0).  The
 // columns pair up as (p, N - p) for p = 1 .. N/2 - 1, plus (0, N/2), both of
-// which are their own mirror columns.  A workgroup of 16 lane columns takes 8
-// pairs: lane column c < 8 holds member 0 of pair 8g + c, and c ^ 8 its
-// partner, so every mirror value is in the same workgroup.
-// Column (member c >> 3 of pair 8g + (c & 7)) of an N-column grid:
+// which are their own mirror columns.  A workgroup of 2 CP lane columns takes
+// CP pairs (8 or 16): lane column c < CP holds member 0 of pair CP g + c, and
+// c ^ CP its partner, so every mirror value is in the same workgroup.
+// Column (member c / CP of pair CP g + c mod CP) of an N-column grid:
+template <int CP = 8>
 __device__ __forceinline__ int pair_col(int g, int c, int n) {
-    const int p = 8 * g + (c & 7);
-    return c < 8 ? p : (p ? n - p : n >> 1);
+    const int p = CP * g + (c & (CP - 1));
+    return c < CP ? p : (p ? n - p : n >> 1);
 }
-// Thread layout of the real passes: the four 16-lane row sets of wave w are
-// 2w, 2w + 1, T - 1 - 2w and T - 2 - 2w (jj = tid >> 4), so that the rows of
-// thread j and of its mirror thread T - 1 - j sit in lanes l and l ^ 32 of one
-// wave (and their mirror columns c and c ^ 8 in lanes l and l ^ 40).
-template <int T>
+// Thread layout of the real passes, so that the rows of thread j and of its
+// mirror thread T - 1 - j sit in lanes l and l ^ 32 of one wave: with 16 lane
+// columns (jj = tid >> 4) the four row sets of wave w are 2w, 2w + 1,
+// T - 1 - 2w and T - 2 - 2w (mirror column c ^ 8: lane l ^ 40); with 32 lane
+// columns (jj = tid >> 5) the two row sets are w and T - 1 - w (mirror
+// column c ^ 16: lane l ^ 48).
+template <int T, int LOGC = 4>
 __device__ __forceinline__ int mirror_row_set(int jj) {
-    static_assert(T % 4 == 0, "a wave holds four 16-lane row sets");
-    return (jj & 2) ? T - 1 - 2 * (jj >> 2) - (jj & 1) : 2 * (jj >> 2) + (jj & 1);
+    if constexpr (LOGC == 4) {
+        static_assert(T % 4 == 0, "a wave holds four 16-lane row sets");
+        return (jj & 2) ? T - 1 - 2 * (jj >> 2) - (jj & 1) : 2 * (jj >> 2) + (jj & 1);
+    } else {
+        static_assert(LOGC == 5 && T % 2 == 0, "a wave holds two 32-lane row sets");
+        return (jj & 1) ? T - 1 - (jj >> 1) : (jj >> 1);
+    }
 }
 // x as held by the lane at byte address `from` (lane * 4) of this wave
 __device__ __forceinline__ float2 lane_value(float2 x, int from) {
@@ -332,17 +340,18 @@ __device__ __forceinline__ float2 lane_value(float2 x, int from) {
                        __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(x.y))));
 }
 // R2C: pass 1 stores Z with its k1 positions permuted so that position
-// 16g + c holds k1 = pair_col(g, c, N1): pass 2 then reads 8 mirror pairs
-// as one aligned 16-column run.  k1 stored at position `pos`:
-template <int N1>
-__device__ __forceinline__ int pair_k1(int pos) { return pair_col(pos >> 4, pos & 15, N1); }
+// 2CP g + c holds k1 = pair_col<CP>(g, c, N1): pass 2 then reads CP mirror
+// pairs as one aligned 2CP-column run.  k1 stored at position `pos`:
+template <int N1, int CP = 8>
+__device__ __forceinline__ int pair_k1(int pos) { return pair_col<CP>(pos / (2 * CP), pos % (2 * CP), N1); }
 
 // MAP 0: column c of the group is column c0 + c (d = Z + c0 N1).  MAP 1 (R2C
-// pass 1): the same columns, each stored with its k1 permuted (pair_k1).
+// pass 1): the same columns, each stored with its k1 permuted (pair_k1, CP
+// pairs per group of pass 2).
 // MAP 2 (C2R pass 1): lane column c is column pair_col(g, c, 2^log_s) (d = Z).
 // NTS (KIND 1): non-temporal stores, for output that nothing in this launch
 // reads again (it then does not displace lines the launch still uses).
-template <class C, int KIND, int MAP = 0, bool NTS = false>
+template <class C, int KIND, int MAP = 0, bool NTS = false, int CP = 8>
 __device__ __forceinline__ void col_store(const float2 (&v)[C::E], float2* d, float2* lds, int tid, int c, int j,
                                           int log_s, float scale, int g = 0) {
     if constexpr (KIND == 0) {
@@ -366,11 +375,11 @@ __device__ __forceinline__ void col_store(const float2 (&v)[C::E], float2* d, fl
                 const int cc = e >> C::LOG_L;
                 const int k1 = e & (C::L - 1);
                 if constexpr (MAP == 2) {
-                    const int col = pair_col(g, h.value * CH + cc, 1 << log_s);
+                    const int col = pair_col<C::C / 2>(g, h.value * CH + cc, 1 << log_s);
                     d[((int64_t)col << C::LOG_L) + k1] = lds[cc * C::PITCH + pad(k1)];
                 } else {
                     *byte_off(dh + r.value * C::WG, (uint32_t)tid * 8u) =
-                        lds[cc * C::PITCH + pad(MAP == 1 ? pair_k1<C::L>(k1) : k1)];
+                        lds[cc * C::PITCH + pad(MAP == 1 ? pair_k1<C::L, CP>(k1) : k1)];
                 }
             });
         });
@@ -425,8 +434,9 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_pass_
 }
 
 // R2C pass 1: the column pass of the half-length core (forward), with Z
-// stored in the pair-permuted k1 order (MAP 1) for the stitching pass 2.
-template <int LOGL, int LOGE, int LOGC>
+// stored in the pair-permuted k1 order (MAP 1) for the stitching pass 2 and
+// its CP mirror pairs per workgroup.
+template <int LOGL, int LOGE, int LOGC, int CP = 8>
 __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_r2c_pass1_kernel(
     const float2* src, float2* dst, const float2* __restrict__ tw, const float2* __restrict__ tw_lo,
     const float2* __restrict__ tw_hi, int tw_h, int logn, int log_s) {
@@ -447,19 +457,20 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_r2c_p
         big_tw_load<C>(f, tw_lo, tw_hi, tw_h, (uint32_t)(c0 + c), j);
         return f;
     });
-    col_store<C, 0, 1>(v, dst + base + ((int64_t)c0 << LOGL), lds, tid, c, j, log_s, 1.0f);
+    col_store<C, 0, 1, false, CP>(v, dst + base + ((int64_t)c0 << LOGL), lds, tid, c, j, log_s, 1.0f);
 }
 
 // R2C pass 2 with the stitch (kernels.py:1127-1177 formula, r2c_bin): the
-// row pass of the half-length core over one aligned 16-column run of the
-// permuted Z (8 mirror pairs), then every output bin from its core value and
-// its mirror's, written to the n/2 + 1 bins of the row.  After the last
-// Stockham pass thread j holds k2 = j + m T + q NS (element e = m R + q); the
-// mirror of (k1, k2) is (n1 - k1, N2 - 1 - k2): element E - 1 - e of thread
-// T - 1 - j in lane column c ^ 8, which the thread layout (mirror_row_set)
-// puts at lane ^ 40 of the same wave, one ds_bpermute per component away.
-// Two columns of group 0 mirror onto themselves: k1 = n1/2 (lane column 8;
-// partner lane ^ 32) and k1 = 0 (lane column 0), whose k2 pairs with
+// row pass of the half-length core over one aligned run of 2 CP columns of
+// the permuted Z (CP = 8 or 16 mirror pairs), then every output bin from its
+// core value and its mirror's, written to the n/2 + 1 bins of the row.  After
+// the last Stockham pass thread j holds k2 = j + m T + q NS (element
+// e = m R + q); the mirror of (k1, k2) is (n1 - k1, N2 - 1 - k2): element
+// E - 1 - e of thread T - 1 - j in lane column c ^ CP, which the thread layout
+// (mirror_row_set) puts at lane ^ (32 + CP) of the same wave, one ds_bpermute
+// per component away.  Two columns of group 0 mirror onto themselves:
+// k1 = n1/2 (lane column CP; partner lane ^ 32) and k1 = 0 (lane column 0),
+// whose k2 pairs with
 // N2 - k2 of another wave: its lanes store their bins again from a copy of
 // the column in LDS, and the thread holding k = 0 also writes bin n/2.
 // The bin twiddle exp(-2 pi i k / n), k = k1 + n1 k2, is
@@ -469,7 +480,8 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_r2c_p
     const float2* src, float2* dst, const float2* __restrict__ tw, const float2* __restrict__ tw_a,
     const float2* __restrict__ tw_b, int logn, int log_s, float scale) {
     using C = ColCfg<LOGL, LOGE, LOGC>;
-    static_assert(LOGC == 4, "mirror pairs span 16 lane columns");
+    static_assert(LOGC == 4 || LOGC == 5, "8 or 16 mirror pairs per workgroup");
+    constexpr int CP = C::C / 2;  // mirror pairs per workgroup
     constexpr int N2 = C::L, E = C::E;
     __shared__ float2 lds[C::LDS_FLOAT2];
     const int n1 = 1 << log_s;
@@ -479,12 +491,12 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_r2c_p
     const int g = bid - (int)(row * groups);
     const int tid = threadIdx.x;
     const int c = tid & (C::C - 1);
-    const int j = mirror_row_set<C::T>(tid >> LOGC);
+    const int j = mirror_row_set<C::T, LOGC>(tid >> LOGC);
     const int64_t np = (int64_t)1 << logn;  // core length L = n/2
     float2 v[E];
     col_load<C>(v, src + (row << logn) + (g << LOGC), c, j, log_s);
     col_passes<C, -1, 1, false>(v, lds, tw, c, j, [&] { return BigTw<C>{}; });
-    const int k1 = pair_col(g, c, n1);
+    const int k1 = pair_col<CP>(g, c, n1);
     const bool col0 = g == 0 && c == 0;
     float2* xo = dst + row * (np + 1) + k1;
     // K = k2 - j of element e
@@ -496,7 +508,7 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_r2c_p
         }
         __syncthreads();
     }
-    const int from = ((tid & 63) ^ (g == 0 && c == 8 ? 32 : 40)) << 2;
+    const int from = ((tid & 63) ^ (g == 0 && c == CP ? 32 : 32 + CP)) << 2;
     const float2 tj = cmul(tw_a[k1], tw_b[j]);
     // every lane stitches with its partner's values, without branches (column
     // 0's lanes store bins that they overwrite below)
@@ -524,19 +536,20 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_r2c_p
 }
 
 // C2R pass 1 with the pre-twiddle (kernels.py:1180-1229 formula,
-// c2r_pre_bin): the workgroup loads 8 columns of the n/2 + 1 bins and their
-// 8 mirror columns (pair_col), turns every bin into its core input with its
+// c2r_pre_bin): the workgroup loads CP = 8 or 16 columns of the n/2 + 1 bins
+// and their CP mirror columns (pair_col; with 16, 128 B runs of the bin rows,
+// which are not line-aligned, so fewer lines are shared with the neighbouring
+// workgroups), turns every bin into its core input with its
 // mirror's value, then runs the column pass of the half-length inverse core
 // with its four-step twiddle and stores Z in place of the output row (the row
 // pass runs in place there).
 // The mirror of bin (n1, n2) is (N1 - 1 - n1, N2 - n2), and thread j's rows
 // j + m T + q N1/R0 (element e = m R0 + q) have their mirrors in element
-// E - 1 - e of thread T - 1 - j, lane column c ^ 8.  Threads are laid out so
-// that a wave holds the row sets 2w, 2w + 1, T - 1 - 2w and T - 2 - 2w (16
-// lanes each), so that partner is lane ^ 40 of the same wave and each mirror
-// value is one ds_bpermute per component away: no LDS round and no copy of
-// the mirror values in registers.  Two columns of group 0 mirror onto
-// themselves: column N2/2 (lane column 8; partner lane ^ 32) and column 0
+// E - 1 - e of thread T - 1 - j, lane column c ^ CP.  Threads are laid out
+// (mirror_row_set) so that partner is lane ^ (32 + CP) of the same wave and
+// each mirror value is one ds_bpermute per component away: no LDS round and
+// no copy of the mirror values in registers.  Two columns of group 0 mirror
+// onto themselves: column N2/2 (lane column CP; partner lane ^ 32) and column 0
 // (lane column 0), whose row n1 pairs with row N1 - n1 of another wave and
 // goes through LDS; bin n/2, the mirror of bin 0, is loaded by the thread
 // that holds bin 0, and the imaginary parts of both are ignored.
@@ -548,7 +561,8 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_c2r_p
     const float2* __restrict__ tw_hi, int tw_h, const float2* __restrict__ tw_a, const float2* __restrict__ tw_b,
     int logn, int log_s) {
     using C = ColCfg<LOGL, LOGE, LOGC>;
-    static_assert(LOGC == 4, "mirror pairs span 16 lane columns");
+    static_assert(LOGC == 4 || LOGC == 5, "8 or 16 mirror pairs per workgroup");
+    constexpr int CP = C::C / 2;  // mirror pairs per workgroup
     constexpr int N1 = C::L;
     constexpr int R0 = 1 << C::logr(0);
     constexpr int NB0 = C::E / R0;
@@ -561,9 +575,9 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_c2r_p
     const int g = bid - (int)(row * groups);
     const int tid = threadIdx.x;
     const int c = tid & (C::C - 1);
-    const int j = mirror_row_set<C::T>(tid >> LOGC);
+    const int j = mirror_row_set<C::T, LOGC>(tid >> LOGC);
     const int64_t np = (int64_t)1 << logn;
-    const int n2 = pair_col(g, c, n2n);
+    const int n2 = pair_col<CP>(g, c, n2n);
     const bool col0 = g == 0 && c == 0;  // n2 = 0: mirror rows N1 - n1 of its own column, bin n/2 for n1 = 0
     const float2* xr = src + row * (np + 1);
     float2 v[E];
@@ -585,7 +599,7 @@ __global__ __launch_bounds__((ColCfg<LOGL, LOGE, LOGC>::WG)) void fourstep_c2r_p
         }
         __syncthreads();
     }
-    const int from = ((tid & 63) ^ (g == 0 && c == 8 ? 32 : 40)) << 2;
+    const int from = ((tid & 63) ^ (g == 0 && c == CP ? 32 : 32 + CP)) << 2;
     // the root of row j + K is tw_a[n2] tw_b[j] exp(-2 pi i K / (2 N1)): one
     // table product per thread, then compile-time rotations (K = m T + q N1/R0)
     const float2 tj = cmul(tw_a[n2], tw_b[j]);
@@ -920,15 +934,42 @@ hipError_t launch_real_pass(const float2* src, float2* dst, const mfft_plan* p, 
     using C = ColCfg<LOGL, LOGE, LOGC>;
     const int logn = ilog2((int)p->core_n);
     const int64_t tiles = rows * (((int64_t)1 << log_s) >> LOGC);
+    // 16 mirror pairs per workgroup (128 B runs of the bins) where the grid of
+    // bins has 32 columns or more and the mirror pass is at most 512 points
+    // (at 1024 the doubled workgroup's LDS leaves one per CU); R2C's two
+    // passes take the same choice, since pass 1 permutes Z for pass 2's pairs
+    using C5 = ColCfg<LOGL, LOGE, 5>;
     if constexpr (KIND == 0) {
-        fourstep_r2c_pass1_kernel<LOGL, LOGE, LOGC><<<(unsigned)tiles, C::WG, 0, stream>>>(
-            src, dst, p->tw_n1, p->tw_lo, p->tw_hi, p->tw_h, logn, log_s);
+        if (LOGL >= 5 && log_s <= 9)
+            fourstep_r2c_pass1_kernel<LOGL, LOGE, LOGC, 16><<<(unsigned)tiles, C::WG, 0, stream>>>(
+                src, dst, p->tw_n1, p->tw_lo, p->tw_hi, p->tw_h, logn, log_s);
+        else
+            fourstep_r2c_pass1_kernel<LOGL, LOGE, LOGC><<<(unsigned)tiles, C::WG, 0, stream>>>(
+                src, dst, p->tw_n1, p->tw_lo, p->tw_hi, p->tw_h, logn, log_s);
     } else if constexpr (KIND == 1) {
-        fourstep_r2c_pass2_kernel<LOGL, LOGE, LOGC><<<(unsigned)tiles, C::WG, 0, stream>>>(
-            src, dst, p->tw_n2, p->tw_ra, p->tw_rb, logn, log_s, scale);
+        bool pairs16 = false;
+        if constexpr (LOGL <= 9) {
+            if (log_s >= 5) {
+                pairs16 = true;
+                fourstep_r2c_pass2_kernel<LOGL, LOGE, 5><<<(unsigned)(tiles >> 1), C5::WG, 0, stream>>>(
+                    src, dst, p->tw_n2, p->tw_ra, p->tw_rb, logn, log_s, scale);
+            }
+        }
+        if (!pairs16)
+            fourstep_r2c_pass2_kernel<LOGL, LOGE, LOGC><<<(unsigned)tiles, C::WG, 0, stream>>>(
+                src, dst, p->tw_n2, p->tw_ra, p->tw_rb, logn, log_s, scale);
     } else {
-        fourstep_c2r_pass1_kernel<LOGL, LOGE, LOGC><<<(unsigned)tiles, C::WG, 0, stream>>>(
-            src, dst, p->tw_n1, p->tw_lo, p->tw_hi, p->tw_h, p->tw_ra, p->tw_rb, logn, log_s);
+        bool pairs16 = false;
+        if constexpr (LOGL <= 9) {
+            if (log_s >= 5) {
+                pairs16 = true;
+                fourstep_c2r_pass1_kernel<LOGL, LOGE, 5><<<(unsigned)(tiles >> 1), C5::WG, 0, stream>>>(
+                    src, dst, p->tw_n1, p->tw_lo, p->tw_hi, p->tw_h, p->tw_ra, p->tw_rb, logn, log_s);
+            }
+        }
+        if (!pairs16)
+            fourstep_c2r_pass1_kernel<LOGL, LOGE, LOGC><<<(unsigned)tiles, C::WG, 0, stream>>>(
+                src, dst, p->tw_n1, p->tw_lo, p->tw_hi, p->tw_h, p->tw_ra, p->tw_rb, logn, log_s);
     }
     mark(stream);
     return hipGetLastError();
