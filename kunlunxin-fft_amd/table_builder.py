@@ -190,7 +190,6 @@ def main() -> int:
     ap.add_argument("--rounds", type=int, default=3)
     args = ap.parse_args()
 
-    import numpy as np  # noqa: F401
     import torch
 
     sys.path.insert(0, ROOT)

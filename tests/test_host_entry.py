@@ -2,7 +2,6 @@
 tests/test_entry.py, test_selector.py and test_semantic_key.py contracts
 against this package's plan_fft / select / load_table."""
 import json
-import os
 
 import pytest
 
