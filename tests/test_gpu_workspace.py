@@ -196,3 +196,30 @@ def test_plan_api_two_streams_share_cached_plans(gpu):
     torch.cuda.synchronize()
     for key, y in outs.items():
         assert torch.equal(y.cpu(), eager[key]), key
+
+
+def test_clear_native_cache_keeps_plans_working(gpu):
+    """runner.clear_native_cache drops every cached native plan and destroys
+    those nothing holds (after a device sync); a plan executed before keeps
+    its own native plan, a new one of the same shape gets a fresh one, and
+    both give the same result as before."""
+    from kunlunxin_fft_amd import ExecutionPlan, execute_fft_plan, runner
+
+    def mk(n, b):
+        return ExecutionPlan(n=n, batch=b, direction="dit", precision="fp32", selection_source="table",
+                             reason="test", fallback=False, executed="fft_lds_fused_batch", block=256,
+                             flow_id="test", flow_realization="test", processing_unit="test", params={})
+
+    rng = np.random.default_rng(77)
+    h = (rng.standard_normal((8, 1024)) + 1j * rng.standard_normal((8, 1024))).astype(np.complex64)
+    x = torch.from_numpy(h).to(gpu)
+    plan = mk(1024, 8)
+    before = execute_fft_plan(plan, x).cpu()
+    # a second shape, so that the cache holds a plan no ExecutionPlan refers to
+    execute_fft_plan(mk(2048, 4), torch.zeros((4, 2048), dtype=torch.complex64, device=gpu))
+    runner.clear_native_cache()
+    assert native.retired_count() == 0
+    assert torch.equal(execute_fft_plan(plan, x).cpu(), before)
+    assert torch.equal(execute_fft_plan(mk(1024, 8), x).cpu(), before)
+    ref = np.fft.fft(h.astype(np.complex128))
+    assert oracle.rel_l2(before.numpy(), ref) <= TOL
