@@ -509,7 +509,7 @@ hipError_t dispatch_elems(int loge, int mode, int dir, const LdsArgs& a) {
 
 }  // namespace
 
-bool lds_supported(int log2l, int elems, int mode) {
+bool lds_supported(int log2l, int elems) {
     if (log2l < 0 || log2l > kMaxLdsLog2) return false;
     if (elems != 0 && elems != 4 && elems != 8 && elems != 16 && elems != 32) return false;
     // 32 elements per thread (split exchange) exist for 2^10..2^15 (the r2c

@@ -381,10 +381,8 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
     const int dir = transform_direction == MFFT_FORWARD ? -1 : 1;
 
     // ---- resolve and check the flow
-    // LDS kernel mode: 0 c2c core (also the non-fused real cores), 1 r2c, 2 c2r
-    const int lds_mode = transform_type == MFFT_R2C ? 1 : (transform_type == MFFT_C2R ? 2 : 0);
     if (flow == MFFT_FLOW_AUTO)
-        flow = mfft::lds_supported(logc, 0, lds_mode) ? MFFT_FLOW_LDS_FUSED : MFFT_FLOW_FOUR_STEP;
+        flow = mfft::lds_supported(logc, 0) ? MFFT_FLOW_LDS_FUSED : MFFT_FLOW_FOUR_STEP;
     int block = 256, elems = 0, stagger = 0;
     int64_t n1 = 0, n2 = 0, chunk = 0;
     int schedule = 0, pass2_rev = 0, fused_lag = 0, fused_take = 0, fused_ring = 0, fused_bpc = 0;
@@ -406,7 +404,7 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
             break;
         }
         case MFFT_FLOW_LDS_FUSED:
-            if (!mfft::lds_supported(logc, prm[0], lds_mode))
+            if (!mfft::lds_supported(logc, prm[0]))
                 return fail(MFFT_ERR_UNSUPPORTED,
                             "LDS_FUSED runs core lengths up to 2^%d with 4, 8, 16 or 32 "
                             "elements per thread (32 from 2^10; 2^13, 2^14: 16 or 32; 2^15: 32) "

@@ -101,7 +101,7 @@ hipError_t launch_c2r_pre(const float2* x, float2* z, const float2* tw_real, int
 // ---- lds_kernels.hip: single-pass LDS-resident Stockham kernel ------------
 // mode 0: c2c core; 1: r2c (core forward + fused stitch); 2: c2r (fused
 // pre-twiddle + inverse core).  `log2l` is the core length's log2.
-bool lds_supported(int log2l, int elems, int mode);  // mode as launch_lds
+bool lds_supported(int log2l, int elems);  // every mode (C2C, R2C, C2R) alike
 int lds_default_elems(int log2l);
 int lds_threads_per_block(int log2l, int elems);
 hipError_t launch_lds(int mode, int dir, int log2l, int elems, const void* src, void* dst,
