@@ -166,7 +166,9 @@ typedef struct {
 /* Create a plan on the current device.  Validates everything before any
  * allocation: n a power of two (c2c 1..2^20, r2c/c2r 2..2^20), batch >= 1,
  * enums in range, r2c forward-only and c2r inverse-only (entry.py:157-172),
- * and that `flow` can run the shape.  Uploads the twiddle tables and
+ * and that `flow` can run the shape: at most 2^40 bytes of complex64 rows,
+ * and no launch of 2^32 work-items or more (one dispatch's count is 32-bit;
+ * MFFT_ERR_UNSUPPORTED, split the batch).  Uploads the twiddle tables and
  * allocates the workspace (the only allocations the library makes). */
 int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_type,
                      int transform_direction, int norm, int flow,

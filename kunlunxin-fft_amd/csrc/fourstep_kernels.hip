@@ -905,6 +905,7 @@ hipError_t launch_pass(const float2* src, float2* dst, const mfft_plan* p, int64
     const int logn = ilog2((int)p->core_n);
     const int64_t groups = ((int64_t)1 << log_s) >> LOGC;
     const int64_t tiles = rows * groups;
+    if (!launch_fits(tiles, C::WG)) return hipErrorInvalidConfiguration;
     const float2* tw = KIND == 0 ? p->tw_n1 : p->tw_n2;
     if (p->schedule == 1) {
         // a multiple of the column groups (fixed c0 per block) and of 16,
@@ -934,6 +935,8 @@ hipError_t launch_real_pass(const float2* src, float2* dst, const mfft_plan* p, 
     using C = ColCfg<LOGL, LOGE, LOGC>;
     const int logn = ilog2((int)p->core_n);
     const int64_t tiles = rows * (((int64_t)1 << log_s) >> LOGC);
+    // (the 32-column forms below run half the blocks at twice the threads)
+    if (!launch_fits(tiles, C::WG)) return hipErrorInvalidConfiguration;
     // 16 mirror pairs per workgroup (128 B runs of the bins) where the grid of
     // bins has 32 columns or more and the mirror pass is at most 512 points
     // (at 1024 the doubled workgroup's LDS leaves one per CU); R2C's two

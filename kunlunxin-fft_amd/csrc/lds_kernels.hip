@@ -457,6 +457,7 @@ hipError_t launch_one(const LdsArgs& a) {
     using C = LdsCfg<LOGL, LOGE>;
     const int64_t blocks = (a.rows + C::TPB - 1) / C::TPB;
     if (blocks <= 0) return hipSuccess;
+    if (!launch_fits(blocks, C::WG)) return hipErrorInvalidConfiguration;
     int wave_blocks = 0, n = 0;
     if (a.stagger > 0 && a.num_cus >= 16) {
         // blocks one wave of the grid holds (occupancy query, once per kernel)

@@ -478,6 +478,42 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
             return fail(MFFT_ERR_VALUE, "unknown flow id %d", flow);
     }
 
+    // ---- every launch of the plan must fit one dispatch: an upper bound on
+    // the work-items of its largest launch, from each flow's threads per
+    // transform (checked again at every launch)
+    {
+        int64_t items = 0;
+        auto most = [&](int64_t v) { items = v > items ? v : items; };
+        switch (flow) {
+            case MFFT_FLOW_LDS_FUSED: {
+                const int e = elems ? elems : mfft::lds_default_elems(logc);
+                const int64_t t = core_n / e > 0 ? core_n / e : 1;  // threads per transform
+                most(batch * t + 1024);
+                break;
+            }
+            case MFFT_FLOW_FOUR_STEP: {
+                const int e1 = 1 << mfft::fourstep_col_loge(mfft::ilog2((int)n1));
+                const int e2 = 1 << mfft::fourstep_col_loge(mfft::ilog2((int)n2));
+                most(batch * (core_n / (e1 < e2 ? e1 : e2)) + 1024);
+                break;
+            }
+            case MFFT_FLOW_DENSE_MFMA:
+                most((batch * core_n + 15) / 16 + 4096);  // L/16 threads per transform
+                break;
+            default:  // stage flows: radix-2 stages (also the radix-4 flows' odd tail)
+                most(batch * (core_n >> 1) + block);
+        }
+        // a real transform whose core does not carry the stitch / pre-twiddle
+        // runs it as its own launch: 256 threads per 512 bins of a row
+        const bool real_fused = flow == MFFT_FLOW_LDS_FUSED || (flow == MFFT_FLOW_FOUR_STEP && schedule == 0);
+        if (real && !real_fused) most(batch * ((((core_n >> 1) + 1 + 255) / 256) * 256));
+        if (items > mfft::kMaxLaunchItems)
+            return fail(MFFT_ERR_UNSUPPORTED,
+                        "batch=%lld of n=%lld: a launch of this flow would run %lld work-items, above the "
+                        "%lld one dispatch holds; split the batch",
+                        (long long)batch, (long long)n, (long long)items, (long long)mfft::kMaxLaunchItems);
+    }
+
     int dev = 0;
     hipError_t he = hipGetDevice(&dev);
     if (he != hipSuccess) return hip_fail(he, "hipGetDevice");

@@ -75,6 +75,14 @@ inline void mark(hipStream_t s) {
 }
 
 constexpr int kMaxLog2N = 20;        // reference range: 8 .. 2^20 (docs/user-guide/transforms.md)
+// A dispatch packet carries its launch's work-item count in 32 bits, and
+// the runtime takes some larger launches with the count wrapped (2^32 + 1024
+// work-items ran as 1024, without an error, on MI355X), so every launch
+// checks its size and a plan refuses shapes whose launches would not fit.
+constexpr int64_t kMaxLaunchItems = ((int64_t)1 << 32) - 1;
+inline bool launch_fits(int64_t blocks, int64_t threads_per_block) {
+    return blocks >= 0 && threads_per_block > 0 && blocks <= kMaxLaunchItems / threads_per_block;
+}
 constexpr int kMaxLdsLog2 = 15;      // single-pass LDS kernel: core length <= 32768
 constexpr int kMinFourStepLog2 = 8;  // four-step needs n1, n2 >= 16
 

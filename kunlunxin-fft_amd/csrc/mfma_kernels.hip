@@ -182,6 +182,7 @@ hipError_t launch_one(const float2* src, float2* dst, const float2* tw, int64_t 
     using C = MfmaCfg<LOGL>;
     const int64_t blocks = (rows + C::TPB - 1) / C::TPB;
     if (blocks <= 0) return hipSuccess;
+    if (!launch_fits(blocks, C::WG)) return hipErrorInvalidConfiguration;
     mfma_fft_kernel<LOGL, DIR><<<(unsigned)blocks, C::WG, 0, stream>>>(src, dst, tw, rows, scale);
     mark(stream);
     return hipGetLastError();

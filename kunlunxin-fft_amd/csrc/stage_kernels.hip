@@ -249,6 +249,7 @@ hipError_t launch_radix2(bool dif, int dir, const float2* src, float2* dst, floa
                          hipStream_t stream, int* launches) {
     const int logn = ilog2((int)n);
     const int64_t total = rows * (n >> 1);
+    if (!launch_fits((total + block - 1) / block, block)) return hipErrorInvalidConfiguration;
     const unsigned grid = grid_for(total, block);
     const float2* cur = src;
     int count = 0;
@@ -292,6 +293,7 @@ hipError_t launch_radix4(bool dif, int dir, const float2* src, float2* dst, floa
     const int stages = n4 + (tail ? 1 : 0);
     const int64_t total4 = rows * (n >> 2);
     const int64_t total2 = rows * (n >> 1);
+    if (!launch_fits((total2 + block - 1) / block, block)) return hipErrorInvalidConfiguration;
     const unsigned grid4 = grid_for(total4, block);
     const unsigned grid2 = grid_for(total2, block);
     const float2* cur = src;
@@ -343,6 +345,7 @@ hipError_t launch_bitrev(const float2* src, float2* dst, int64_t n, int64_t rows
     const int logn = ilog2((int)n);
     const int64_t total = rows * n;
     if (total == 0) return hipSuccess;
+    if (!launch_fits((total + 255) / 256, 256)) return hipErrorInvalidConfiguration;
     bitrev_kernel<<<grid_for(total, 256), 256, 0, stream>>>(src, dst, total, logn);
     mark(stream);
     return hipGetLastError();
@@ -354,6 +357,7 @@ hipError_t launch_twiddle_transpose(int dir, const float2* s, float2* g, int64_t
     const int tiles_r = (int)((rows + 31) / 32), tiles_c = (int)((cols + 31) / 32);
     const int64_t blocks = batch * tiles_r * tiles_c;
     if (blocks == 0) return hipSuccess;
+    if (!launch_fits(blocks, 256)) return hipErrorInvalidConfiguration;
     const uint32_t nmask = (uint32_t)(n - 1);
     const float inv_half_n = 2.0f / (float)n;
     if (dir < 0)
@@ -370,7 +374,7 @@ hipError_t launch_r2c_stitch(const float2* z, float2* x, const float2* tw_real, 
                              int64_t rows, float scale, hipStream_t stream) {
     const int64_t np = n >> 1;
     const int bpr = (int)(((np >> 1) + 1 + 255) / 256);  // blocks per row: pairs k in [0, np/2]
-    if ((int64_t)bpr * rows > 0x7fffffff) return hipErrorInvalidValue;
+    if (!launch_fits((int64_t)bpr * rows, 256)) return hipErrorInvalidConfiguration;
     r2c_stitch_kernel<<<(unsigned)(bpr * rows), 256, 0, stream>>>(z, x, tw_real, np, bpr, scale);
     mark(stream);
     return hipGetLastError();
@@ -380,7 +384,7 @@ hipError_t launch_c2r_pre(const float2* x, float2* z, const float2* tw_real, int
                           int64_t rows, hipStream_t stream) {
     const int64_t np = n >> 1;
     const int bpr = (int)(((np >> 1) + 1 + 255) / 256);
-    if ((int64_t)bpr * rows > 0x7fffffff) return hipErrorInvalidValue;
+    if (!launch_fits((int64_t)bpr * rows, 256)) return hipErrorInvalidConfiguration;
     c2r_pre_kernel<<<(unsigned)(bpr * rows), 256, 0, stream>>>(x, z, tw_real, np, bpr);
     mark(stream);
     return hipGetLastError();

@@ -689,12 +689,17 @@ def test_input_validation_raises_before_launch(gpu):
 
 
 def test_native_rejects_oversized_batch(gpu):
-    """Plans cover at most 2^40 bytes of complex64 rows (no byte count or
-    grid can overflow); the largest legal batch still plans."""
+    """Plans cover at most 2^40 bytes of complex64 rows (no byte count can
+    overflow), and no launch of 2^32 work-items or more (one dispatch's
+    limit): at n = 1024 the LDS kernel runs 64 threads per transform, so 2^27
+    rows are refused and the largest batch whose launch fits still plans."""
     for n in (1, 1024, 1 << 20):
         with pytest.raises(ValueError, match="2\\^40"):
             native.NativePlan(n, ((1 << 37) // n) + 1)
-    assert native.NativePlan(1024, (1 << 37) // 1024, flow=native.FLOW_LDS_FUSED).info.batch == 1 << 27
+    with pytest.raises(ValueError, match="dispatch"):
+        native.NativePlan(1024, (1 << 37) // 1024, flow=native.FLOW_LDS_FUSED)
+    big = ((1 << 32) - 1 - 1024) // 64
+    assert native.NativePlan(1024, big, flow=native.FLOW_LDS_FUSED).info.batch == big
 
 
 def test_native_rejects_overlap_and_misalignment(gpu):

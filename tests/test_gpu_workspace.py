@@ -223,3 +223,16 @@ def test_clear_native_cache_keeps_plans_working(gpu):
     assert torch.equal(execute_fft_plan(mk(1024, 8), x).cpu(), before)
     ref = np.fft.fft(h.astype(np.complex128))
     assert oracle.rel_l2(before.numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("n,batch,flow,params", [
+    (1024, 1 << 25, native.FLOW_LDS_FUSED, ()),          # 2^31 work-items per launch
+    (1 << 20, 1 << 16, native.FLOW_FOUR_STEP, (1024,)),  # 2^31 per pass
+])
+def test_plans_below_the_dispatch_limit_are_created(gpu, n, batch, flow, params):
+    """A dispatch holds fewer than 2^32 work-items, so plan creation refuses
+    shapes whose largest launch would reach that (CPU tests); shapes below it
+    are accepted.  These plans take no workspace and are only created:
+    executing them would need 256 GiB of buffers."""
+    p = native.NativePlan(n, batch, "c2c", "forward", "backward", flow, params)
+    assert p.info.batch == batch and p.ws_bytes == 0

@@ -51,6 +51,13 @@ def test_struct_layouts():
     (dict(n=2, batch=1, flow=native.FLOW_RADIX4_DIT), "core length"),
     (dict(n=64, batch=1, flow=native.FLOW_RADIX2_DIT, params=(32,)), "threads per block"),
     (dict(n=64, batch=1, flow=99), "unknown flow"),
+    # a launch of 2^32 work-items or more does not fit one dispatch
+    (dict(n=1024, batch=1 << 23, flow=native.FLOW_RADIX2_DIT), "dispatch"),
+    (dict(n=1024, batch=1 << 26, flow=native.FLOW_LDS_FUSED), "dispatch"),
+    (dict(n=1 << 20, batch=1 << 17, flow=native.FLOW_FOUR_STEP, params=(1024,)), "dispatch"),
+    (dict(n=1 << 14, batch=1 << 23, flow=native.FLOW_DENSE_MFMA), "dispatch"),
+    # the stitch launch, not the 4-point core, is the one that would not fit
+    (dict(n=8, batch=(1 << 24) + 1, transform_type="r2c", flow=native.FLOW_RADIX2_DIT), "dispatch"),
 ])
 def test_plan_create_rejects_before_device_work(kwargs, match):
     if not os.path.exists(native.LIB_PATH):
