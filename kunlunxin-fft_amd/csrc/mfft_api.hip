@@ -875,6 +875,10 @@ int mfft_bit_reverse_permute(const void* in, void* out, int64_t n, int64_t batch
     if (logn < 0 || logn > mfft::kMaxLog2N)
         return fail(MFFT_ERR_VALUE, "size must be a power of two in [1, 2^%d], got %lld", mfft::kMaxLog2N, (long long)n);
     if (batch < 1) return fail(MFFT_ERR_VALUE, "batch must be >= 1");
+    if (batch > ((int64_t)1 << 37) / n) return fail(MFFT_ERR_VALUE, "batch too large (over 2^40 bytes)");
+    if (!mfft::launch_fits((n * batch + 255) / 256, 256))  // one thread per element
+        return fail(MFFT_ERR_UNSUPPORTED, "batch=%lld of n=%lld needs a launch of 2^32 work-items or more; "
+                    "split the batch", (long long)batch, (long long)n);
     const size_t bytes = (size_t)n * (size_t)batch * 8;
     if ((const char*)in < (const char*)out + bytes && (const char*)out < (const char*)in + bytes)
         return fail(MFFT_ERR_VALUE, "in and out must not overlap");
@@ -892,6 +896,9 @@ int mfft_twiddle_transpose(const void* in, void* out, int64_t rows, int64_t cols
                     mfft::kMaxLog2N, (long long)rows, (long long)cols);
     if (batch < 1) return fail(MFFT_ERR_VALUE, "batch must be >= 1");
     if (batch > ((int64_t)1 << 37) / (rows * cols)) return fail(MFFT_ERR_VALUE, "batch too large");
+    if (!mfft::launch_fits(batch * ((rows + 31) / 32) * ((cols + 31) / 32), 256))  // 256 threads per 32 x 32 tile
+        return fail(MFFT_ERR_UNSUPPORTED, "batch=%lld of %lld x %lld needs a launch of 2^32 work-items or more; "
+                    "split the batch", (long long)batch, (long long)rows, (long long)cols);
     if (direction != MFFT_FORWARD && direction != MFFT_INVERSE)
         return fail(MFFT_ERR_VALUE, "unsupported direction %d", direction);
     const size_t bytes = (size_t)(rows * cols * batch) * 8;

@@ -82,3 +82,18 @@ def test_plan_create_ex_rejects_unknown_flags():
     rc = lib.mfft_plan_create_ex(ctypes.byref(h), 1024, 1, native.C2C, native.FORWARD, native.NORM_IDS["backward"],
                                  native.FLOW_AUTO, arr, 0, 2)
     assert rc == native.ERR_VALUE and b"flags" in lib.mfft_last_error() and not h.value
+
+
+def test_standalone_kernels_refuse_oversized_batches():
+    """mfft_bit_reverse_permute and mfft_twiddle_transpose validate their
+    sizes before any device work: at most 2^40 bytes, and no launch of 2^32
+    work-items or more (the pointers are never touched)."""
+    lib = native.load()
+    a, b = ctypes.c_void_p(1 << 20), ctypes.c_void_p(1 << 40)
+    assert lib.mfft_bit_reverse_permute(a, b, 1024, 1 << 28, None) == native.ERR_VALUE
+    assert b"too large" in lib.mfft_last_error()
+    assert lib.mfft_bit_reverse_permute(a, b, 1024, 1 << 22, None) == native.ERR_UNSUPPORTED
+    assert b"2^32" in lib.mfft_last_error()
+    # 16 x 16 matrices fill a quarter of a 32 x 32 tile: 256 threads per 256 values
+    assert lib.mfft_twiddle_transpose(a, b, 16, 16, 1 << 24, native.FORWARD, None) == native.ERR_UNSUPPORTED
+    assert b"2^32" in lib.mfft_last_error()
