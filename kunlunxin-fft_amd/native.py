@@ -234,7 +234,12 @@ class NativePlan:
 
 
 # Native plans dropped by their owners, not yet destroyed: (handle, device).
+# __del__ only appends (atomic under the GIL, and it must not wait on a lock
+# a collection could interrupt); release_retired takes items out under
+# _RETIRED_LOCK, from the front, so two threads releasing at once never
+# take (and destroy) the same handle, and handles appended meanwhile stay.
 _RETIRED: list = []
+_RETIRED_LOCK = threading.Lock()
 
 
 def retired_count() -> int:
@@ -244,11 +249,14 @@ def retired_count() -> int:
 def release_retired(sync=None) -> int:
     """Destroy every retired plan; ``sync(device)`` is called once per
     device first, to make sure none of their executes is pending.  Returns
-    how many plans were destroyed."""
+    how many plans were destroyed.  Safe to call from several threads."""
     if not _RETIRED or _lib is None:
         return 0
-    items = _RETIRED[:]
-    del _RETIRED[:len(items)]
+    with _RETIRED_LOCK:
+        items = _RETIRED[:]
+        del _RETIRED[:len(items)]
+    if not items:
+        return 0
     if sync is not None:
         for dev in sorted({d for _, d in items}):
             sync(dev)

@@ -180,3 +180,43 @@ def test_semantic_families():
     assert all(family_allows(t, "four-step-two-pass") for t in ("c2c", "r2c", "c2r"))
     with pytest.raises(KeyError):
         family_allows("dct", "four-step-two-pass")
+
+
+def test_release_retired_destroys_each_handle_once(monkeypatch):
+    """Plans dropped by their owners wait in a list until release_retired
+    destroys them; two threads releasing at once must not both take (and
+    destroy) the same handles.  The list's copy is slowed down here so that,
+    without the lock, both threads would copy it before either removed it."""
+    import threading
+    import time
+
+    destroyed = []
+
+    class FakeLib:
+        def mfft_plan_destroy(self, h):
+            destroyed.append(h)
+
+    class SlowList(list):
+        def __getitem__(self, i):
+            got = list.__getitem__(self, i)
+            if isinstance(i, slice):
+                time.sleep(0.05)  # after the copy: others may copy the same items now
+            return got
+
+    retired = SlowList((("h%d" % i), 0) for i in range(100))
+    monkeypatch.setattr(native, "_lib", FakeLib())
+    monkeypatch.setattr(native, "_RETIRED", retired)
+    start = threading.Barrier(4)
+    counts = []
+
+    def release():
+        start.wait()
+        counts.append(native.release_retired())
+
+    threads = [threading.Thread(target=release) for _ in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert sorted(destroyed) == sorted("h%d" % i for i in range(100))
+    assert sum(counts) == 100 and len(retired) == 0
