@@ -56,12 +56,14 @@ def test_twiddle_transpose_rejects_bad_shapes(gpu):
         native.twiddle_transpose(x.data_ptr(), x.data_ptr(), 8, 8, 1, "forward", st)
 
 
-@pytest.mark.parametrize("n,b,tile", [(1024, 1, 32), (2048, 16, 64), (4096, 64, 16), (2048, 1, 128),
-                                      (1 << 16, 4, 256), (1 << 12, 3, 2)])
-@pytest.mark.parametrize("core", ["vendor", "local"])
+HYBRID_SHAPES = [(1024, 1, 32), (2048, 16, 64), (4096, 64, 16), (2048, 1, 128), (1 << 16, 4, 256), (1 << 12, 3, 2)]
+
+
+# the local core needs tile and N/tile in [16, 1024] (plan_hybrid rejects
+# other splits for it: tests/test_host_entry.py::test_hybrid_plan_contract)
+@pytest.mark.parametrize("n,b,tile,core", [(n, b, t, core) for core in ("vendor", "local") for n, b, t in HYBRID_SHAPES
+                                           if core == "vendor" or (16 <= t <= 1024 and 16 <= n // t <= 1024)])
 def test_run_hybrid_matches_oracle(gpu, n, b, tile, core):
-    if core == "local" and not (16 <= tile <= 1024 and 16 <= n // tile <= 1024):
-        pytest.skip("the local core needs tile and N/tile in [16, 1024] (plan_hybrid rejects it)")
     x = seeded(n, b, 61)
     y = run_hybrid(torch.from_numpy(x).to(gpu), plan_hybrid(n, b, tile=tile, core=core)).cpu().numpy()
     check(y, oracle.fft_dit(x), f"run_hybrid {core} N={n} B={b} tile={tile}")

@@ -81,11 +81,10 @@ FLOW_CASES += [("fft_lds_fused", n) for n in (1, 2, 4, 8, 16, 32, 64, 128, 256, 
 FLOW_CASES += [("fft_four_step", n) for n in (256, 1024, 4096, 1 << 14, 1 << 16, 1 << 18, 1 << 20)]
 
 
-@pytest.mark.parametrize("name,n", FLOW_CASES)
-@pytest.mark.parametrize("b", [1, 3])
+# batch 3 below 2^18 points (the large-N batches are the config tests' cases)
+@pytest.mark.parametrize("name,n,b", [(name, n, b) for b in (1, 3) for name, n in FLOW_CASES
+                                      if b == 1 or n < (1 << 18)])
 def test_c2c_forward_matches_oracle(gpu, name, n, b):
-    if n >= (1 << 18) and b > 1:
-        pytest.skip("large-N batch covered by the config tests")
     x = seeded_c64(n, b)
     bname = name + "_batch" if b > 1 else name
     y = execute_fft_plan(mkplan(bname, n, b), torch.from_numpy(x).to(gpu)).cpu().numpy()
@@ -369,8 +368,6 @@ def test_c2r_mirror_pairs(gpu, elems, n, b):
     transform) or through LDS (the other forms), bin 0
     pairs with bin n/2, and the DC/Nyquist imaginary parts are ignored.
     Ragged batches leave rows of a multi-transform block inactive."""
-    if elems < 16 and n > 8192:
-        pytest.skip("16+ elements from 8192-point cores")
     rng = np.random.default_rng(4000 + n + b + elems)
     m = n // 2 + 1
     h = (rng.standard_normal((b, m)) + 1j * rng.standard_normal((b, m))).astype(np.complex64)
