@@ -619,8 +619,10 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
     } else if (rc == MFFT_OK) {
         rc = put(&p->tw, roots(core_n, core_n, 1));
     }
-    if (rc == MFFT_OK && real) {
-        // exp(-2*pi*i*k/n), k in [0, n/2]  (runner.py:1650-1658 range)
+    if (rc == MFFT_OK && real && !p->real4_fused) {
+        // exp(-2*pi*i*k/n), k in [0, n/2]  (runner.py:1650-1658 range); the
+        // fused real four-step takes its bin roots from the two small tables
+        // below instead (this one would be 4 MiB at n = 2^20)
         rc = put(&p->tw_real, roots(n, n / 2 + 1, 1));
     }
     if (rc == MFFT_OK && p->real4_fused) {
