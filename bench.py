@@ -101,7 +101,7 @@ def main() -> int:
     import __graft_entry__
 
     pkg = __graft_entry__.load_package()
-    from kunlunxin_fft_amd import runner
+    from kunlunxin_fft_amd import native, runner
     from kunlunxin_fft_amd.entry import _resolve
 
     if not torch.cuda.is_available():
@@ -132,7 +132,29 @@ def main() -> int:
     copy_ms = statistics.median(s.elapsed_time(e) for s, e in evs)
     copy_gbps = 2 * src.numel() * 8 / (copy_ms * 1e-3) / 1e9
     log(f"d2d copy 256 MiB: {copy_ms:.4f} ms, {copy_gbps:.1f} GB/s (read + write)")
-    del src, dst
+
+    # ---- the library's streaming copy (non-temporal 16-byte lanes) of 256 MiB
+    # each way, each timed copy right after an untimed one of two other
+    # buffers so that the MALL holds none of its lines: what a transform that
+    # reads and writes every byte once could reach on this device
+    src2, dst2 = torch.empty_like(src), torch.empty_like(src)
+    nbytes = src.numel() * 8
+    sc = torch.cuda.current_stream(dev).cuda_stream
+    cevs = []
+    for i in range(23):
+        native.stream_copy(src2.data_ptr(), dst2.data_ptr(), nbytes, sc)
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        native.stream_copy(src.data_ptr(), dst.data_ptr(), nbytes, sc)
+        e.record()
+        if i >= 3:
+            cevs.append((s, e))
+    torch.cuda.synchronize()
+    ceil_ms = statistics.median(s.elapsed_time(e) for s, e in cevs)
+    ceil_gbps = 2 * nbytes / (ceil_ms * 1e-3) / 1e9
+    log(f"streaming copy 256 MiB (flushed): {ceil_ms:.4f} ms, {ceil_gbps:.1f} GB/s (read + write)")
+    del src, dst, src2, dst2
 
     # ---- inputs resident in HBM, plans resolved once (plan reuse)
     work = []
@@ -216,6 +238,16 @@ def main() -> int:
             launch_runs[i].append(nplan.execute_timed(x.data_ptr(), out.data_ptr(), stream.cuda_stream,
                                                       ws_ptr=ws.data_ptr() if ws is not None else 0,
                                                       ws_bytes=nplan.ws_bytes))
+    def round_trips(flow, launches):
+        """HBM round trips of the data in one execute: one for the single-pass
+        kernels, two for the four-step (its intermediate Z goes out and back),
+        one per launch for the stage flows."""
+        if flow in ("lds-fused", "dense-mfma"):
+            return 1
+        if flow == "four-step":
+            return 2
+        return launches
+
     flows = []  # per size: (launch names, per-launch ms) of one execute
     for i, (n, b, x, plan) in enumerate(work):
         nplan, out, _ = natives[i]
@@ -236,6 +268,7 @@ def main() -> int:
                 names.append(f"{flow} stage {j + 1}")
         flows.append((names, per_launch, rows))
         gbps = 16 * n * b / (ms * 1e-3) / 1e9
+        trips = round_trips(flow, len(per_launch))
         per_size.append({
             "n": n, "batch": b, "executed": plan.executed, "flow": flow,
             "fallback": plan.fallback, "launches": len(per_launch),
@@ -243,6 +276,7 @@ def main() -> int:
             "gflops": round(5 * n * math.log2(n) * b / (ms * 1e-3) / 1e9, 1),
             "launch_ms": [round(t, 5) for t in per_launch],
             "split": [int(nplan.info.n1), int(nplan.info.n2), rows] if nplan.info.n1 else None,
+            "round_trips": trips, "frac_of_copy_bound": round(gbps * trips / ceil_gbps, 4),
         })
         log(f"N={n:>8} B={b:>6} {flow:>10} {ms:8.4f} ms {gbps:8.1f} GB/s "
             f"({gbps / PEAK_GBPS:.1%}) launches={['%.4f' % t for t in per_launch]}")
@@ -274,7 +308,9 @@ def main() -> int:
                 "kernel": f"{' + '.join(kinds)} [{dflow}, N={dn}, B={db}, {drows} rows per launch, "
                           f"{len(dts)} launches per execute, counted together]",
                 "algorithmic_bytes_per_execute": d_bytes, "launch_ms": [round(t, 5) for t in dts],
-                "sum_launch_ms": round(d_ms, 5), "share_of_step": round(d_ms / ms_per_step, 3)}
+                "sum_launch_ms": round(d_ms, 5), "share_of_step": round(d_ms / ms_per_step, 3),
+                "copy_ceiling_gbps": round(ceil_gbps, 1), "round_trips": round_trips(dflow, len(dts)),
+                "frac_of_copy_bound": round(d_ach * round_trips(dflow, len(dts)) / ceil_gbps, 4)}
     log(f"dominant kernel: {roofline}")
 
     # ---- latency at N=2048 B=1 (reference protocol) and config 2
@@ -532,7 +568,9 @@ def main() -> int:
                    "frac_hbm_of_value": round(value / PEAK_GBPS, 4),
                    "runner_forced": args.runner or None,
                    "d2d_copy_gbps": round(copy_gbps, 1),
-                   "frac_of_d2d_copy": round(value / copy_gbps, 4)},
+                   "frac_of_d2d_copy": round(value / copy_gbps, 4),
+                   "stream_copy_gbps": round(ceil_gbps, 1),
+                   "frac_of_stream_copy": round(value / ceil_gbps, 4)},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "latency_n2048_b1": lat,

@@ -270,6 +270,13 @@ int mfft_bit_reverse_permute(const void* in, void* out, int64_t n, int64_t batch
 int mfft_twiddle_transpose(const void* in, void* out, int64_t rows, int64_t cols, int64_t batch, int direction,
                            void* stream);
 
+/* Measurement only; no counterpart in the reference, for benchmark callers:
+ * out = in over `bytes` (a multiple of 16; 16-byte aligned, non-overlapping
+ * buffers), a streaming copy with non-temporal loads and stores.  Its rate
+ * is the practical ceiling of a transform that reads and writes every byte
+ * once (bench.py divides its per-size rates by it). */
+int mfft_stream_copy(const void* in, void* out, int64_t bytes, void* stream);
+
 /* Device facts for the profile / environment fingerprint. */
 int mfft_device_props_get(int device, mfft_device_props* out);
 

@@ -912,6 +912,22 @@ int mfft_twiddle_transpose(const void* in, void* out, int64_t rows, int64_t cols
     return e == hipSuccess ? MFFT_OK : hip_fail(e, "kernel launch");
 }
 
+int mfft_stream_copy(const void* in, void* out, int64_t bytes, void* stream) {
+    g_err.clear();
+    if (!in || !out) return fail(MFFT_ERR_VALUE, "in and out must not be NULL");
+    if (bytes < 0 || bytes % 16) return fail(MFFT_ERR_VALUE, "bytes must be a non-negative multiple of 16, got %lld",
+                                             (long long)bytes);
+    if (bytes > ((int64_t)1 << 40)) return fail(MFFT_ERR_VALUE, "bytes over 2^40");
+    if (!mfft::launch_fits((bytes / 16 + 2047) / 2048, 256))  // 256 threads per 32 KiB
+        return fail(MFFT_ERR_UNSUPPORTED, "a copy of %lld bytes needs a launch of 2^32 work-items or more; split it",
+                    (long long)bytes);
+    if ((((uintptr_t)in) | ((uintptr_t)out)) & 15) return fail(MFFT_ERR_VALUE, "in and out must be 16-byte aligned");
+    if ((const char*)in < (const char*)out + bytes && (const char*)out < (const char*)in + bytes)
+        return fail(MFFT_ERR_VALUE, "in and out must not overlap");
+    const hipError_t e = mfft::launch_stream_copy(in, out, bytes, (hipStream_t)stream);
+    return e == hipSuccess ? MFFT_OK : hip_fail(e, "kernel launch");
+}
+
 int mfft_device_props_get(int device, mfft_device_props* out) {
     g_err.clear();
     if (!out) return fail(MFFT_ERR_VALUE, "out must not be NULL");

@@ -96,6 +96,8 @@ hipError_t launch_radix4(bool dif, int dir, const float2* src, float2* dst, floa
                          const float2* tw, int64_t n, int64_t rows, float scale, int block,
                          hipStream_t stream, int* launches);
 hipError_t launch_bitrev(const float2* src, float2* dst, int64_t n, int64_t rows, hipStream_t stream);
+// dst = src, `bytes` a multiple of 16 (16-byte aligned, non-overlapping)
+hipError_t launch_stream_copy(const void* src, void* dst, int64_t bytes, hipStream_t stream);
 // G[c][r] = S[r][c] * W_(rows*cols)^(dir * r * c) for `batch` rows x cols matrices
 hipError_t launch_twiddle_transpose(int dir, const float2* s, float2* g, int64_t rows, int64_t cols, int64_t batch,
                                     hipStream_t stream);

@@ -240,6 +240,35 @@ __global__ __launch_bounds__(256) void twiddle_transpose_kernel(const float2* __
     }
 }
 
+// Streaming copy of n16 16-byte words, the rate this device moves bytes
+// read once and written once: each thread moves 8 words 256 apart, with
+// non-temporal loads and stores.  Of the forms measured on MI355X (8- or
+// 16-byte lanes, 4 to 16 words per thread, temporal or non-temporal
+// stores; 256 MiB each way after an untimed 256 MiB write) this one was the
+// fastest, 6.1-6.2 TB/s read + write.  Not on any transform path: it is
+// the practical ceiling the bench measures its transforms against.
+typedef float nt_float4 __attribute__((ext_vector_type(4)));
+// Whole blocks take a branch-free path: a bounds check per word makes each
+// load its own branch, which the compiler closes with a wait for that load,
+// so the eight loads no longer overlap (measured 4.3 against 6.1 TB/s).
+__global__ __launch_bounds__(256) void stream_copy_kernel(const nt_float4* __restrict__ x,
+                                                          nt_float4* __restrict__ y, int64_t n16) {
+    const int64_t blk = (int64_t)blockIdx.x * 2048;
+    const int64_t base = blk + threadIdx.x;
+    nt_float4 v[8];
+    if (blk + 2048 <= n16) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = __builtin_nontemporal_load(x + base + q * 256);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) __builtin_nontemporal_store(v[q], y + base + q * 256);
+        return;
+    }
+    for (int q = 0; q < 8; ++q) {
+        const int64_t i = base + q * 256;
+        if (i < n16) __builtin_nontemporal_store(__builtin_nontemporal_load(x + i), y + i);
+    }
+}
+
 inline unsigned grid_for(int64_t total, int block) { return (unsigned)((total + block - 1) / block); }
 
 }  // namespace
@@ -347,6 +376,16 @@ hipError_t launch_bitrev(const float2* src, float2* dst, int64_t n, int64_t rows
     if (total == 0) return hipSuccess;
     if (!launch_fits((total + 255) / 256, 256)) return hipErrorInvalidConfiguration;
     bitrev_kernel<<<grid_for(total, 256), 256, 0, stream>>>(src, dst, total, logn);
+    mark(stream);
+    return hipGetLastError();
+}
+
+hipError_t launch_stream_copy(const void* src, void* dst, int64_t bytes, hipStream_t stream) {
+    const int64_t n16 = bytes / 16;
+    if (n16 == 0) return hipSuccess;
+    const int64_t blocks = (n16 + 2047) / 2048;
+    if (!launch_fits(blocks, 256)) return hipErrorInvalidConfiguration;
+    stream_copy_kernel<<<(unsigned)blocks, 256, 0, stream>>>((const nt_float4*)src, (nt_float4*)dst, n16);
     mark(stream);
     return hipGetLastError();
 }

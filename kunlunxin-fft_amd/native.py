@@ -39,7 +39,7 @@ EXPORTS = (
     "mfft_plan_create", "mfft_execute", "mfft_execute_timed", "mfft_plan_destroy", "mfft_plan_query",
     "mfft_bit_reverse_permute", "mfft_device_props_get", "mfft_last_error",
     "mfft_abi_version", "mfft_plan_sync_overruns", "mfft_plan_create_ex", "mfft_plan_workspace_size",
-    "mfft_execute_ws", "mfft_execute_noalloc", "mfft_twiddle_transpose",
+    "mfft_execute_ws", "mfft_execute_noalloc", "mfft_twiddle_transpose", "mfft_stream_copy",
 )
 PLAN_CALLER_WORKSPACE = 1
 
@@ -119,6 +119,8 @@ def load() -> ctypes.CDLL:
         lib.mfft_bit_reverse_permute.restype = i32
         lib.mfft_twiddle_transpose.argtypes = [vp, vp, i64, i64, i64, i32, vp]
         lib.mfft_twiddle_transpose.restype = i32
+        lib.mfft_stream_copy.argtypes = [vp, vp, i64, vp]
+        lib.mfft_stream_copy.restype = i32
         lib.mfft_device_props_get.argtypes = [i32, ctypes.POINTER(DeviceProps)]
         lib.mfft_device_props_get.restype = i32
         lib.mfft_last_error.argtypes = []
@@ -275,6 +277,12 @@ def twiddle_transpose(in_ptr: int, out_ptr: int, rows: int, cols: int, batch: in
     """out[c][r] = in[r][c] * W_(rows*cols)^(-+ r c) per rows x cols matrix."""
     check(load().mfft_twiddle_transpose(ctypes.c_void_p(in_ptr), ctypes.c_void_p(out_ptr), int(rows), int(cols),
                                         int(batch), DIR_IDS[direction], ctypes.c_void_p(stream_ptr)))
+
+
+def stream_copy(in_ptr: int, out_ptr: int, nbytes: int, stream_ptr: int) -> None:
+    """out = in over nbytes (measurement only: the streaming-copy ceiling)."""
+    check(load().mfft_stream_copy(ctypes.c_void_p(in_ptr), ctypes.c_void_p(out_ptr), int(nbytes),
+                                  ctypes.c_void_p(stream_ptr)))
 
 
 def device_props(device: int = 0) -> dict:

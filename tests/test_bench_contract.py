@@ -37,3 +37,9 @@ def test_bench_json_line(gpu):
     rf = line["roofline"]
     assert rf["bound"] == "hbm" and rf["unit"] == "GB/s" and rf["peak"] == 8000.0
     assert 0 < rf["frac"] < 1 and abs(rf["achieved"] / rf["peak"] - rf["frac"]) < 1e-3
+    # the measured streaming-copy ceiling, and the dominant flow against it
+    # (its round trips times the copy time of its bytes; above 1 where the
+    # MALL still holds part of the data, as in this two-size cycle)
+    assert 3000 < rf["copy_ceiling_gbps"] < 8000 and rf["round_trips"] >= 1
+    assert 0 < rf["frac_of_copy_bound"] < 3
+    assert line["config"]["stream_copy_gbps"] == rf["copy_ceiling_gbps"]

@@ -645,6 +645,20 @@ def test_bit_reverse_permute(gpu, golden):
     assert [y8.index(i) for i in range(8)] == list(golden["bitrev8"])
 
 
+@pytest.mark.parametrize("nbytes", [16, 4096, 32768, 32768 + 48, (64 << 20) + 16 * 777])
+def test_stream_copy_is_exact(gpu, nbytes):
+    """The bench's streaming copy moves every byte, including a tail shorter
+    than one 32 KiB block, and writes nothing past the end."""
+    from kunlunxin_fft_amd import native
+
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=gpu)
+    dst = torch.full((nbytes + 4096,), 7, dtype=torch.uint8, device=gpu)
+    native.stream_copy(src.data_ptr(), dst.data_ptr(), nbytes, torch.cuda.current_stream(gpu).cuda_stream)
+    torch.cuda.synchronize(gpu)
+    assert torch.equal(dst[:nbytes], src)
+    assert bool((dst[nbytes:] == 7).all())
+
+
 def test_reexecution_is_bitwise_stable_and_one_shot_matches(gpu):
     prof = DeviceProfile.load().hash()
     for n, b in ((128, 1), (2048, 16), (1 << 16, 2)):

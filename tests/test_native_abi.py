@@ -97,3 +97,22 @@ def test_standalone_kernels_refuse_oversized_batches():
     # 16 x 16 matrices fill a quarter of a 32 x 32 tile: 256 threads per 256 values
     assert lib.mfft_twiddle_transpose(a, b, 16, 16, 1 << 24, native.FORWARD, None) == native.ERR_UNSUPPORTED
     assert b"2^32" in lib.mfft_last_error()
+
+
+def test_stream_copy_validates_before_device_work():
+    """mfft_stream_copy (the bench's copy ceiling) refuses NULL, sizes that
+    are not a multiple of 16, misaligned or overlapping buffers, and copies
+    whose launch would reach 2^32 work-items, before touching the pointers."""
+    lib = native.load()
+    a, b = ctypes.c_void_p(1 << 20), ctypes.c_void_p(1 << 41)
+    assert lib.mfft_stream_copy(None, b, 16, None) == native.ERR_VALUE
+    assert lib.mfft_stream_copy(a, b, 24, None) == native.ERR_VALUE
+    assert b"multiple of 16" in lib.mfft_last_error()
+    assert lib.mfft_stream_copy(a, b, -16, None) == native.ERR_VALUE
+    assert lib.mfft_stream_copy(ctypes.c_void_p((1 << 20) + 8), b, 16, None) == native.ERR_VALUE
+    assert b"aligned" in lib.mfft_last_error()
+    assert lib.mfft_stream_copy(a, ctypes.c_void_p((1 << 20) + 16), 64, None) == native.ERR_VALUE
+    assert b"overlap" in lib.mfft_last_error()
+    assert lib.mfft_stream_copy(a, b, (1 << 40) + 16, None) == native.ERR_VALUE
+    assert lib.mfft_stream_copy(a, b, 1 << 39, None) == native.ERR_UNSUPPORTED
+    assert b"2^32" in lib.mfft_last_error()
