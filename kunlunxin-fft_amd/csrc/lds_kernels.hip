@@ -86,7 +86,7 @@ struct LdsCfg {
     // E - 1 - q, one lane swap away (j = 0 and j = T/2 pair with
     // themselves).
     static constexpr bool PAIR =
-        LE >= 4 && T >= 64 && (MODE == 2 || (MODE == 1 && sched_logr(LOGL, LE, P - 1, RF) == LE));
+        LE >= 3 && T >= 64 && (MODE == 2 || (MODE == 1 && sched_logr(LOGL, LE, P - 1, RF) == LE));
     static constexpr int logr(int p) { return sched_logr(LOGL, LE, p, RF); }
     static constexpr int lns(int p) { return sched_lns_rf(LOGL, LE, p, RF); }
 };
