@@ -75,9 +75,9 @@ struct LdsCfg {
     // when each wave stays within 64 VGPRs: the lane-paired r2c stitch took
     // 71-73 and lost a block per CU (N = 2^15 measured 13% slower).
     static constexpr int MIN_WAVES = SPLIT ? (LE == 4 ? 8 : 4) : 1;
-    // Lane pairing of the real modes with 16 or 32 elements per thread
+    // Lane pairing of the real modes with 8, 16 or 32 elements per thread
     // (the 32-element registers have no room for the mirror values, and it
-    // saves the 16-element kernels an LDS round trip): when whole waves make
+    // saves the 8- and 16-element kernels an LDS round trip): when whole waves make
     // up a transform and the pass next to HBM has the full radix (c2r: the
     // first pass, always; r2c: the last, as its remainder runs first), thread
     // t plays Stockham index pair_j(t), which puts the indices j and T - j

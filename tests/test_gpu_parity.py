@@ -116,11 +116,13 @@ def test_lds_elems_axis_neutral(gpu, elems, n):
 
 
 @pytest.mark.parametrize("elems", [4, 8])
-@pytest.mark.parametrize("n", [64, 2048])
+@pytest.mark.parametrize("n", [64, 1024, 2048])
 @pytest.mark.parametrize("b", [1, 5])
 def test_lds_small_elems_inverse_and_real(gpu, elems, n, b):
     """The latency kernels (4 and 8 elements per thread) in the inverse
-    direction (conjugated roots) and in the fused R2C/C2R modes."""
+    direction (conjugated roots) and in the fused R2C/C2R modes; at 8
+    elements, N = 1024 and 2048 pair the mirror bins across lanes (a
+    512- or 1024-point core, whole waves per transform)."""
     x = seeded_c64(n, b, session=3)
     sfx = "_batch" if b > 1 else ""
     p = {"elems": elems}
@@ -359,12 +361,12 @@ def test_r2c_c2r_match_oracle(gpu, name, n, norm):
     check(y, oracle.c2r_dedicated(Xh, n, norm), f"c2r {name} N={n} {norm}")
 
 
-@pytest.mark.parametrize("elems,n", [(e, n) for e in (4, 8, 16) for n in (16, 64, 512, 2048, 8192)]
+@pytest.mark.parametrize("elems,n", [(e, n) for e in (4, 8, 16) for n in (16, 64, 512, 2048, 8192)] + [(8, 1024)]
                          + [(16, 1 << 14), (16, 1 << 15), (32, 1 << 12), (32, 1 << 15), (32, 1 << 16)])
 @pytest.mark.parametrize("b", [1, 3, 37])
 def test_c2r_mirror_pairs(gpu, elems, n, b):
     """Fused C2R: each bin is loaded once and meets its mirror bin n/2 - k
-    from the partner lane (16 or 32 elements per thread and whole waves per
+    from the partner lane (8, 16 or 32 elements per thread and whole waves per
     transform) or through LDS (the other forms), bin 0
     pairs with bin n/2, and the DC/Nyquist imaginary parts are ignored.
     Ragged batches leave rows of a multi-transform block inactive."""
