@@ -10,7 +10,18 @@ Infinity Cache.  Inputs are synthetic
 HBM before the timed region.  ``value`` = algorithmic bytes of all K steps
 (16*N*B per transform) / timed wall time, in GB/s.
 
-Also reported (on the same JSON line):
+Output: the last stdout line is one compact JSON record (``compact_line``,
+a few KB: the contract keys, ``roofline``, ``cpu_baseline``, the latency
+p50s, per-size ``[N, GB/s, frac]`` rows, configs 2-4 rows, a config-5
+summary and the provenance hashes); progress and per-cell lines go to
+stderr before it, and the full record below (per-launch times, vendor
+columns, every config-5 cell) to ``--detail-out``
+(``gpurun_out/bench_detail.json`` by default).
+
+Also reported:
+* ``provenance``: device profile and live environment hashes, the sha256
+  of the selector/composition tables and their own bindings, of the kernel
+  sources and of the built library, and the commit when one is present;
 * ``roofline``: the dominant flow (the size whose launches take the largest
   share of a step): the transforms' algorithmic bytes (16 N per row) over the
   sum of the durations of all launches of one execute (both four-step passes
@@ -63,10 +74,130 @@ sys.path.insert(0, ROOT)
 
 PEAK_GBPS = 8000.0
 SIZES = [1 << k for k in range(10, 21)]
+METRIC = "C2C complex64 GB/s & % HBM peak, N=2^10-2^20; p50 latency N=2048 B=1"
+WORKLOAD = ("forward C2C complex64 via plan_fft/execute_fft_plan, N=2^10..2^20, B=max(64, 2^25/N) "
+            "per N (256 MiB in + 256 MiB out per N, 512 MiB each way at 2^20); one step = all 11 sizes")
+DEFAULT_DETAIL = os.path.join(ROOT, "gpurun_out", "bench_detail.json")
+# The stdout line is read from the tail of the process output; everything
+# else goes to stderr and to the detail file.
+LINE_LIMIT = 4096
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+def _sha16_files(paths) -> "str | None":
+    import hashlib
+
+    h = hashlib.sha256()
+    seen = False
+    for p in paths:
+        try:
+            with open(p, "rb") as f:
+                h.update(os.path.basename(p).encode() + b"\0" + f.read())
+            seen = True
+        except OSError:
+            continue
+    return h.hexdigest()[:16] if seen else None
+
+
+def provenance(pkg, profile_hash: str) -> dict:
+    """What a row is tied to: the device profile and live environment hashes,
+    the selector and composition tables the plans came from (file sha256 and
+    the table's own bindings), the kernel sources and the built library, and
+    the commit when a git checkout is present."""
+    import glob
+    import subprocess
+
+    from kunlunxin_fft_amd import envcheck
+    from kunlunxin_fft_amd.config import CONFIG_DIR
+
+    pdir = os.path.dirname(pkg.__file__)
+    sel = os.path.join(CONFIG_DIR, "selector_table.json")
+    try:
+        with open(sel) as f:
+            tab = json.load(f)
+    except (OSError, ValueError):
+        tab = {}
+    commit = None
+    try:
+        r = subprocess.run(["git", "rev-parse", "--short=12", "HEAD"], cwd=ROOT, capture_output=True,
+                           text=True, timeout=10)
+        commit = r.stdout.strip() or None if r.returncode == 0 else None
+    except (OSError, subprocess.SubprocessError):
+        commit = None
+    return {"profile_hash": profile_hash, "env_hash": envcheck.current_env_hash(),
+            "table_sha16": _sha16_files([sel]),
+            "table_profile_hash": tab.get("profile_hash"), "table_env_hash": tab.get("env_hash"),
+            "composition_sha16": _sha16_files([os.path.join(CONFIG_DIR, "composition_table.json")]),
+            "csrc_sha16": _sha16_files(sorted(glob.glob(os.path.join(pdir, "csrc", "*")))),
+            "lib_sha16": _sha16_files([os.path.join(pdir, "libmfft.so")]),
+            "commit": commit}
+
+
+def compact_line(full: dict, detail: "str | None" = None) -> dict:
+    """The driver's line, built from the full record: the contract keys,
+    ``roofline`` and ``cpu_baseline``, the N=2048 B=1 latencies, per-size
+    ``[N, GB/s, frac]`` triples (real: ``[N, r2c GB/s, r2c frac, c2r GB/s,
+    c2r frac]``), configs 2-4 as ``[N, B, api p50 ms, kernel ms]`` rows,
+    a summary of config 5, and the provenance hashes.  The per-launch lists,
+    vendor columns and config-5 cells stay in the detail record."""
+    line = {k: full.get(k) for k in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
+                                     "higher_is_better", "scaling", "vs_baseline", "dtype", "data")}
+    cfg = full.get("config") or {}
+    line["config"] = {k: cfg.get(k) for k in ("workload", "frac_hbm_of_value", "stream_copy_gbps",
+                                              "frac_of_stream_copy", "d2d_copy_gbps", "runner_forced")}
+    r = full.get("roofline")
+    if r:
+        line["roofline"] = {k: r.get(k) for k in (
+            "bound", "achieved", "peak", "unit", "frac", "traffic", "traffic_over_algorithmic", "kernel",
+            "launch_ms", "algorithmic_bytes_per_execute", "copy_ceiling_gbps", "round_trips",
+            "frac_of_copy_bound")}
+    else:
+        line["roofline"] = None
+    c = full.get("cpu_baseline")
+    if c:
+        mt = c.get("all_cores") or {}
+        line["cpu_baseline"] = {"value": c.get("value"), "unit": c.get("unit"), "cores": c.get("cores"),
+                                "kind": c.get("kind"), "sample": c.get("sample"),
+                                "gpu_over_cpu": c.get("gpu_over_cpu"), "cpu_model": c.get("cpu_model"),
+                                "all_cores": {"value": mt.get("value"), "cores": mt.get("cores")}}
+    else:
+        line["cpu_baseline"] = None
+    lat = full.get("latency_n2048_b1")
+    line["latency_n2048_b1"] = ({k: lat.get(k) for k in (
+        "executed", "api_wall_p50_ms", "kernel_event_p50_ms", "graph_replay_us_per_transform",
+        "reference_p800_api_p50_ms", "api_p50_speedup_vs_reference_p800")} if lat else None)
+    line["per_size"] = [[p["n"], p["gbps"], p["frac_hbm"]] for p in full.get("per_size") or []]
+    real = {}
+    for p in full.get("real_per_size") or []:
+        real.setdefault(p["n"], {})[p["transform"]] = p
+    line["real_per_size"] = [[n, d.get("r2c", {}).get("gbps"), d.get("r2c", {}).get("frac_hbm"),
+                              d.get("c2r", {}).get("gbps"), d.get("c2r", {}).get("frac_hbm")]
+                             for n, d in sorted(real.items())]
+    for key in ("config2", "config4"):
+        line[key] = [[c["n"], c["batch"], c["api_wall_p50_ms"], c["kernel_event_p50_ms"]]
+                     for c in full.get(key) or []]
+    line["config3"] = [[c["n"], c["batch"], c["transform"], c["api_wall_p50_ms"], c["kernel_event_p50_ms"]]
+                       for c in full.get("config3") or []]
+    cells = full.get("config5") or []
+    if cells:
+        sp = sorted(c["speedup_vs_m0"] for c in cells)
+        mf = sorted(c["mfma_over_selected"] for c in cells)
+        line["config5"] = {"cells": len(cells), "clears_guard": sum(bool(c["clears_guard"]) for c in cells),
+                           "speedup_vs_m0_min": sp[0], "speedup_vs_m0_median": sp[len(sp) // 2],
+                           "speedup_vs_m0_max": sp[-1], "mfma_over_selected_min": mf[0]}
+    else:
+        line["config5"] = None
+    line["provenance"] = full.get("provenance")
+    line["detail"] = detail
+    # never outgrow the tail the driver reads: shed the least important rows
+    for key in ("config3", "config2", "config4"):
+        if len(json.dumps(line)) < LINE_LIMIT:
+            break
+        line[key] = "in detail record"
+    return line
 
 
 def batch_for(n: int) -> int:
@@ -86,7 +217,9 @@ def main() -> int:
     ap.add_argument("--no-config5", action="store_true", help="skip the config-5 selector-vs-M0 sweep")
     ap.add_argument("--runner", default="", help="run every size through this runner name (e.g. "
                     "fft_dit_matrix_batch) instead of the selected plan: profiling runs of one flow")
-    ap.add_argument("--detail-out", default="", help="also write the JSON line, indented, to this file")
+    ap.add_argument("--detail-out", default=DEFAULT_DETAIL,
+                    help="write the full record (per-launch times, vendor columns, config 2-5 cells), "
+                         "indented, to this file ('' for none); stdout carries the compact line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every box here has one MI355X; "
@@ -556,21 +689,20 @@ def main() -> int:
                                        f"(host reports {os.cpu_count()} CPUs), {tot_mt:.2f} s per pass"}}
         log(f"cpu baseline: {cpu}")
 
-    line = {
-        "metric": "C2C complex64 GB/s & % HBM peak, N=2^10-2^20; p50 latency N=2048 B=1",
+    full = {
+        "metric": METRIC,
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "complex64 (fp32)",
         "data": "synthetic: iid N(0,1) real/imag parts, fixed device seed, resident in HBM",
-        "config": {"workload": "forward C2C complex64 via plan_fft/execute_fft_plan, "
-                               "N=2^10..2^20, B=max(64, 2^25/N) per N (256 MiB in + 256 MiB out "
-                               "per N, 512 MiB each way at 2^20); one step = all 11 sizes",
+        "config": {"workload": WORKLOAD,
                    "frac_hbm_of_value": round(value / PEAK_GBPS, 4),
                    "runner_forced": args.runner or None,
                    "d2d_copy_gbps": round(copy_gbps, 1),
                    "frac_of_d2d_copy": round(value / copy_gbps, 4),
                    "stream_copy_gbps": round(ceil_gbps, 1),
                    "frac_of_stream_copy": round(value / ceil_gbps, 4)},
+        "provenance": provenance(pkg, prof),
         "roofline": roofline,
         "cpu_baseline": cpu,
         "latency_n2048_b1": lat,
@@ -581,10 +713,17 @@ def main() -> int:
         "per_size": per_size,
         "real_per_size": real_rows,
     }
-    print(json.dumps(line), flush=True)
-    if args.detail_out:
-        with open(args.detail_out, "w") as f:
-            json.dump(line, f, indent=1)
+    detail = args.detail_out
+    if detail:
+        try:
+            os.makedirs(os.path.dirname(os.path.abspath(detail)), exist_ok=True)
+            with open(detail, "w") as f:
+                json.dump(full, f, indent=1)
+        except OSError as e:
+            log(f"detail record not written ({detail}): {e}")
+            detail = ""
+    # the one line the driver parses: last on stdout, a few KB at most
+    print(json.dumps(compact_line(full, os.path.relpath(detail, ROOT) if detail else None)), flush=True)
     return 0
 
 
