@@ -20,9 +20,14 @@ from .config import (  # noqa: F401
     ConfigError,
     DesignSpace,
     DeviceProfile,
+    Manifest,
     NORMALIZATIONS,
+    SizeMatrix,
     TRANSFORM_DIRECTIONS,
     TRANSFORM_TYPES,
+    build_manifest,
+    git_commit,
+    git_dirty,
 )
 from .entry import (  # noqa: F401
     SUPPORTED_NORMS,
@@ -36,7 +41,8 @@ from .entry import (  # noqa: F401
     run_fft,
 )
 from .composition import composition_select, load_composition_table  # noqa: F401
-from .selector import Selection, load_table, select  # noqa: F401
+from .error_metric import max_rel_error, rel_l2  # noqa: F401
+from .selector import Selection, assert_current_environment, load_table, select  # noqa: F401
 
 _TORCH_ATTRS = {
     "bit_reverse_permute": "runner",
@@ -59,6 +65,7 @@ _TORCH_ATTRS = {
     "fft_dif_matrix": "runner",
     "fft_dit_matrix_batch": "runner",
     "fft_dif_matrix_batch": "runner",
+    "fft_dit_matrix_packet_batch": "runner",
     "fft_dit_grouped": "runner",
     "fft_dif_grouped": "runner",
     "log2_exact": "validate",
@@ -66,14 +73,17 @@ _TORCH_ATTRS = {
     "time_call_detailed": "runner",
     "twiddle_tables": "runner",
     "device_context": "context",
+    "xpu_context": "context",
     "validate_input": "validate",
 }
 
 __all__ = [
     "ConfigError", "DesignSpace", "DeviceProfile", "ExecutionPlan",
-    "ExecutionReport", "Selection", "SUPPORTED_NORMS", "SUPPORTED_TRANSFORMS",
-    "SUPPORTED_TRANSFORM_DIRECTIONS", "composition_select", "execute_fft_plan",
-    "load_composition_table", "load_table", "norm_scale", "plan_fft", "run_fft", "select",
+    "ExecutionReport", "Manifest", "Selection", "SizeMatrix", "SUPPORTED_NORMS", "SUPPORTED_TRANSFORMS",
+    "SUPPORTED_TRANSFORM_DIRECTIONS", "assert_current_environment", "build_manifest",
+    "composition_select", "execute_fft_plan", "git_commit", "git_dirty",
+    "load_composition_table", "load_table", "max_rel_error", "norm_scale", "plan_fft", "rel_l2",
+    "run_fft", "select",
     *sorted(_TORCH_ATTRS),
 ]
 

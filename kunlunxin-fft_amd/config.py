@@ -7,6 +7,9 @@ parameters must come from -- with MI355X facts in place of the P800 ones.
 
 * ``DeviceProfile.hash()`` is sha256 of the sorted-key JSON of the profile,
   first 16 hex digits (config.py:94-95 of the reference).
+* ``SizeMatrix`` holds the correctness / bench length lists (reference
+  config.py:98-125); ``Manifest`` / ``build_manifest`` / ``git_commit`` /
+  ``git_dirty`` are the per-run provenance record (config.py:268-352).
 * The JSON files live in this package's ``config/`` directory.
 """
 from __future__ import annotations
@@ -14,9 +17,11 @@ from __future__ import annotations
 import hashlib
 import json
 import os
-from dataclasses import asdict, dataclass
+import subprocess
+from dataclasses import asdict, dataclass, field
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
+_ROOT = os.path.dirname(_PKG)
 CONFIG_DIR = os.path.join(_PKG, "config")
 
 
@@ -164,3 +169,100 @@ class DesignSpace:
             batch_candidates=tuple(b["candidates"]), batch_variants=tuple(variants),
             layout_in=lay["in"][0], layout_out=lay["out"][0],
         )
+
+
+@dataclass(frozen=True)
+class SizeMatrix:
+    """Validated length lists (config/sizes.json; reference config.py:98-125):
+    the correctness and benchmark lengths, the global-stage workgroup sizes
+    and the largest length the vendor comparison column runs at."""
+
+    correctness_sizes: tuple
+    bench_sizes: tuple
+    blocksizes: tuple
+    vendor_baseline_max_n: int
+
+    @staticmethod
+    def load() -> "SizeMatrix":
+        d = _read_json("sizes.json")
+        for key in ("correctness_sizes", "bench_sizes", "blocksizes"):
+            v = d.get(key)
+            _require(isinstance(v, list) and bool(v), f"sizes.json: {key} must be a non-empty list")
+            _require(all(isinstance(t, int) and not isinstance(t, bool) and t > 0 for t in v),
+                     f"sizes.json: {key} must be positive ints")
+            _require(all((t & (t - 1)) == 0 for t in v), f"sizes.json: {key} must be powers of two")
+        _require(isinstance(d.get("vendor_baseline_max_n"), int) and not isinstance(d["vendor_baseline_max_n"], bool),
+                 "sizes.json: vendor_baseline_max_n must be an int")
+        return SizeMatrix(correctness_sizes=tuple(d["correctness_sizes"]), bench_sizes=tuple(d["bench_sizes"]),
+                          blocksizes=tuple(d["blocksizes"]), vendor_baseline_max_n=d["vendor_baseline_max_n"])
+
+
+def git_commit() -> str:
+    """Best-effort commit hash of the checkout this package sits in;
+    ``"unknown"`` outside a git checkout."""
+    try:
+        out = subprocess.run(["git", "rev-parse", "HEAD"], cwd=_ROOT, capture_output=True, text=True, timeout=10)
+        return out.stdout.strip() or "unknown"
+    except (OSError, subprocess.SubprocessError):
+        return "unknown"
+
+
+def git_dirty() -> bool:
+    """True when tracked files differ from HEAD (untracked run output is
+    ignored: it cannot change the code a run executes); False outside a
+    checkout."""
+    try:
+        out = subprocess.run(["git", "status", "--porcelain", "--untracked-files=no"], cwd=_ROOT,
+                             capture_output=True, text=True, timeout=10)
+        return out.returncode == 0 and bool(out.stdout.strip())
+    except (OSError, subprocess.SubprocessError):
+        return False
+
+
+@dataclass
+class Manifest:
+    """Per-run provenance record (reference config.py:302-333), with the
+    MI355X profile's fields: ``gfx_arch`` where the reference records its
+    XPU architecture number, and ``env_hash`` for the live runtime/driver
+    fingerprint (``envcheck``), which the reference keeps as ``driver``."""
+
+    commit: str
+    dirty: bool
+    profile_hash: str
+    device: str
+    gfx_arch: str
+    torch_device_key: str
+    env_hash: str | None = None
+    dtype: str = "complex64"
+    direction: str = "forward"
+    precision: str = "fp32"
+    flow_id: str = "baseline-global-stage"
+    processing_unit: str = "radix2-scalar"
+    us: int = 1
+    ts: int = 1
+    ud: int = 1
+    td: int = 1
+    boundary_residence: str = "gm"
+    layout: str = "interleaved-complex64"
+    block: int = 256
+    fused_tile: int = 1
+    warmup: int = 10
+    trials: int = 50
+    correctness_threshold: float = 1e-4
+    command: str = ""
+    extra: dict = field(default_factory=dict)
+
+    def to_dict(self) -> dict:
+        return asdict(self)
+
+
+def build_manifest(profile: DeviceProfile, **overrides) -> Manifest:
+    """A manifest pinned to the current commit and ``profile``; keyword
+    overrides must name existing fields (``ConfigError`` otherwise)."""
+    m = Manifest(commit=git_commit(), dirty=git_dirty(), profile_hash=profile.hash(), device=profile.device,
+                 gfx_arch=profile.gfx_arch, torch_device_key=profile.torch_device_key)
+    for k, v in overrides.items():
+        if k not in Manifest.__dataclass_fields__:
+            raise ConfigError(f"unknown manifest field: {k}")
+        setattr(m, k, v)
+    return m

@@ -1,8 +1,10 @@
 """Device guard around every launch (reference src/xpu/context.py:43-66).
 
 ``device_context(device)`` makes the tensor's GPU current for the duration of
-a launch; the native plan is bound to the device that was current when it
-was created.  A missing GPU stack is a RuntimeError, never a silent no-op.
+a launch (``runner.launch`` enters it whenever the tensor's GPU is not the
+current one); the native plan is bound to the device that was current when
+it was created.  ``xpu_context`` is the reference's name for the same guard.
+A missing GPU stack is a RuntimeError, never a silent no-op.
 """
 from __future__ import annotations
 
@@ -28,6 +30,15 @@ def device_context(device):
     if index is None:
         index = torch.cuda.current_device()
     with torch.cuda.device(index):
+        yield index
+
+
+@contextlib.contextmanager
+def xpu_context(device: int = 0):
+    """The reference's name for the device guard (context.py:43-66): make
+    GPU ``device`` current for the body and restore the previous one after,
+    also when the body raises; ``RuntimeError`` without a GPU stack."""
+    with device_context(device) as index:
         yield index
 
 

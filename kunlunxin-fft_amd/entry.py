@@ -42,7 +42,6 @@ SUPPORTED_PRECISIONS = ("fp32",)
 SUPPORTED_TRANSFORMS = TRANSFORM_TYPES
 SUPPORTED_TRANSFORM_DIRECTIONS = TRANSFORM_DIRECTIONS
 SUPPORTED_NORMS = NORMALIZATIONS
-REAL_COMPAT_MARK = "packed-c2c-compat"
 REAL_FLOW_MARK = "dedicated-half-spectrum"
 REAL_FLOW_IDS = {"r2c": "dedicated-r2c-pack-v1", "c2r": "dedicated-c2r-hermitian-v1"}
 MAX_N = 1 << 20

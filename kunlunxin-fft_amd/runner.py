@@ -35,6 +35,7 @@ by shape/semantics/flow/device.
 from __future__ import annotations
 
 import math
+import random
 import threading
 import time
 import weakref
@@ -43,7 +44,7 @@ from collections import OrderedDict
 import torch
 
 from . import native
-from .context import device_name, device_ready  # noqa: F401  (re-exported)
+from .context import device_context, device_name, device_ready, xpu_context  # noqa: F401  (re-exported)
 from .validate import log2_exact, validate_batch_input, validate_input, validate_tensor, validate_twiddle
 
 DEFAULT_STAGE_BLOCK = 256
@@ -131,9 +132,10 @@ def flow_params(executed: str, n: int, transform_type: str, block, params: dict)
             return native.FLOW_AUTO, ()
         b = int(block or DEFAULT_STAGE_BLOCK)
         log2_exact(b)
-        if b < 64 or b > 1024:
-            raise ValueError(f"block must be a power of two in [64, 1024], got {b}")
-        return flow, (b,)
+        # the reference's block counts elements per Triton program (any power
+        # of two; its sweeps run up to 2048); here it is threads per
+        # workgroup, 64 (one wave) to 1024: other powers of two clamp
+        return flow, (min(max(b, 64), 1024),)
     if kind == "dense":
         # the dense-dot matrix-core flow runs cores of 2 .. 16384 points;
         # other lengths leave the flow to the library
@@ -156,7 +158,8 @@ _NATIVE: "OrderedDict[tuple, native.NativePlan]" = OrderedDict()
 _NATIVE_LOCK = threading.Lock()
 NATIVE_CACHE_SIZE = 256
 # Dropped native plans are destroyed in a batch once this many wait (never
-# inside a graph capture), after one synchronisation of their devices.
+# inside a graph capture, and automatically only in a single-threaded
+# process), after one synchronisation of their devices.
 RETIRED_FLUSH = 64
 
 
@@ -184,9 +187,14 @@ def get_native_plan(executed: str, n: int, batch: int, transform_type: str,
         if p is not None:
             _NATIVE.move_to_end(key)
             return p
-    if native.retired_count() >= RETIRED_FLUSH:
+    # Destroying retired plans synchronises their devices, which would break
+    # a graph capture in progress on any thread of the process.  This call
+    # can see only its own thread's capture, so it flushes only when it is
+    # the process's one Python thread; a multi-threaded caller flushes at
+    # points of its choosing (release_retired_plans / clear_native_cache).
+    if native.retired_count() >= RETIRED_FLUSH and threading.active_count() == 1:
         release_retired_plans()
-    with torch.cuda.device(device_index):
+    with device_context(device_index):
         p = native.NativePlan(n, batch, transform_type, transform_direction, norm, flow, prm,
                               caller_workspace=True)
     with _NATIVE_LOCK:
@@ -251,13 +259,13 @@ def launch(nplan: native.NativePlan, x: torch.Tensor, out: torch.Tensor) -> torc
         if current_device() == dev:
             nplan.execute_ws(x.data_ptr(), out.data_ptr(), ws.data_ptr(), nplan.ws_bytes, stream)
         else:
-            with torch.cuda.device(dev):
+            with device_context(dev):
                 nplan.execute_ws(x.data_ptr(), out.data_ptr(), ws.data_ptr(), nplan.ws_bytes, stream)
         return out
     if current_device() == dev:
         nplan.execute(x.data_ptr(), out.data_ptr(), stream)
     else:
-        with torch.cuda.device(dev):
+        with device_context(dev):
             nplan.execute(x.data_ptr(), out.data_ptr(), stream)
     return out
 
@@ -323,128 +331,188 @@ def _single(name, x, block, params=None, twiddle=None):
     return run(name, x, 1, x.numel(), block=block, params=params, norm="backward")
 
 
-def _batched(name, x, block, params=None):
+def _batched(name, x, block, params=None, twiddle=None, variant=None):
+    if variant is not None:
+        _check_variant(variant)
     validate_batch_input(x, "x", block=block)
+    check_twiddle(twiddle, x)
     b, n = int(x.shape[0]), int(x.shape[1])
     y = run(name, x, b, n, block=block, params=params, norm="backward")
     return y.reshape(b, n)
 
 
-def fft_dit(x, block: int = DEFAULT_STAGE_BLOCK, twiddle=None):
-    """M0 radix-2 DIT: log2(N) stage launches, bit reversal folded into stage 0."""
+# Every runner keeps the reference's signature (src/xpu/runner.py:118-1472):
+# the same positional order, keywords and defaults, block=1024 included.
+# ``block`` sizes the global-stage flows' workgroups; the single-pass,
+# four-step and matrix-core flows size their own launches and only check
+# that it is a power of two.  ``tile``/``rows``/``glog``/``maxp``/``cells``/
+# ``packets`` shape the reference's Triton programs and have no counterpart
+# in the HIP kernels; they are accepted and ignored.  ``variant`` is
+# 'spread' or 'folded' (the batch always folds into one 1-D grid here; both
+# compute the same values).  ``twiddle`` must hold the forward roots
+# (check_twiddle).  Batches need not be powers of two (the reference's
+# stage runners require it; every flow here runs any B >= 1).
+
+def fft_dit(x, block: int = 1024, twiddle=None):
+    """M0 radix-2 DIT: log2(N) stage launches, bit reversal folded into stage 0
+    (reference runner.py:118)."""
     return _single("fft_dit", x, block, twiddle=twiddle)
 
 
-def fft_dif(x, block: int = DEFAULT_STAGE_BLOCK, twiddle=None):
-    """M0 radix-2 DIF: log2(N) stage launches, bit reversal folded into the last."""
+def fft_dif(x, block: int = 1024, twiddle=None):
+    """M0 radix-2 DIF: log2(N) stage launches, bit reversal folded into the
+    last (reference runner.py:166)."""
     return _single("fft_dif", x, block, twiddle=twiddle)
 
 
-def fft_dit_batch(x, block: int = DEFAULT_STAGE_BLOCK, variant: str = "folded"):
-    """M4: M0 over a (B, N) batch folded into one 1-D grid per stage."""
-    _check_variant(variant)
-    return _batched("fft_dit_batch", x, block)
+def fft_dit_batch(x, block: int = 1024, variant: str = "spread", twiddle=None):
+    """M4: M0 over a (B, N) batch, one launch per stage (reference runner.py:781)."""
+    return _batched("fft_dit_batch", x, block, twiddle=twiddle, variant=variant)
 
 
-def fft_dif_batch(x, block: int = DEFAULT_STAGE_BLOCK, variant: str = "folded"):
-    _check_variant(variant)
-    return _batched("fft_dif_batch", x, block)
+def fft_dif_batch(x, block: int = 1024, variant: str = "spread", twiddle=None):
+    """M4 DIF mirror (reference runner.py:844)."""
+    return _batched("fft_dif_batch", x, block, twiddle=twiddle, variant=variant)
 
 
-def fft_dit_radix4(x, block: int = DEFAULT_STAGE_BLOCK, twiddle=None):
-    """M5 radix-4 DIT (radix-2 tail for odd log2 N), digit reversal folded in."""
-    if x.numel() < 4:
+def fft_dit_radix4(x, block: int = 1024, twiddle=None):
+    """M5 radix-4 DIT (radix-2 tail for odd log2 N), digit reversal folded in
+    (reference runner.py:1399)."""
+    if isinstance(x, torch.Tensor) and x.numel() < 4:
         raise ValueError(f"radix-4 requires N >= 4, got N={x.numel()}")
     return _single("fft_dit_radix4", x, block, twiddle=twiddle)
 
 
-def fft_dif_radix4(x, block: int = DEFAULT_STAGE_BLOCK, twiddle=None):
-    if x.numel() < 4:
+def fft_dif_radix4(x, block: int = 1024, twiddle=None):
+    """M5 radix-4 DIF (reference runner.py:1472)."""
+    if isinstance(x, torch.Tensor) and x.numel() < 4:
         raise ValueError(f"radix-4 requires N >= 4, got N={x.numel()}")
     return _single("fft_dif_radix4", x, block, twiddle=twiddle)
 
 
-def fft_dit_radix4_batch(x, block: int = DEFAULT_STAGE_BLOCK, variant: str = "folded"):
-    _check_variant(variant)
-    return _batched("fft_dit_radix4_batch", x, block)
+def fft_dit_radix4_batch(x, block: int = 1024, variant: str = "spread", twiddle=None):
+    """M5 batch (reference runner.py:1112)."""
+    return _batched("fft_dit_radix4_batch", x, block, twiddle=twiddle, variant=variant)
 
 
-def fft_dif_radix4_batch(x, block: int = DEFAULT_STAGE_BLOCK, variant: str = "folded"):
-    _check_variant(variant)
-    return _batched("fft_dif_radix4_batch", x, block)
+def fft_dif_radix4_batch(x, block: int = 1024, variant: str = "spread", twiddle=None):
+    """M5 batch DIF (reference runner.py:1193)."""
+    return _batched("fft_dif_radix4_batch", x, block, twiddle=twiddle, variant=variant)
 
 
-def fft_lds_fused(x, elems: int = 0):
+def fft_lds_fused(x, elems: int = 0, twiddle=None):
     """Single-pass LDS-resident Stockham FFT (core length <= 32768)."""
-    return _single("fft_lds_fused", x, None, {"elems": elems})
+    return _single("fft_lds_fused", x, None, {"elems": elems}, twiddle=twiddle)
 
 
-def fft_lds_fused_batch(x, elems: int = 0):
-    return _batched("fft_lds_fused_batch", x, None, {"elems": elems})
+def fft_lds_fused_batch(x, elems: int = 0, twiddle=None):
+    return _batched("fft_lds_fused_batch", x, None, {"elems": elems}, twiddle=twiddle)
 
 
-def fft_four_step(x, n1: int = 0, chunk_rows: int = 0, schedule: int = 0):
-    """Two-pass four-step FFT (column pass + twiddle, in-place row pass)."""
-    return _single("fft_four_step", x, None, {"n1": n1, "chunk_rows": chunk_rows, "schedule": schedule})
+def _four_step_params(n1, chunk_rows, schedule, allow_fused_schedule) -> dict:
+    if schedule == 2 and not allow_fused_schedule:
+        raise ValueError("schedule=2 (both passes in one launch) needs allow_fused_schedule=True: when one of "
+                         "its bounded waits gives up, the launch writes NaN and the execute still returns "
+                         "success; the caller must check NativePlan.sync_overruns() (mfft_plan_sync_overruns) "
+                         "after synchronising")
+    return {"n1": n1, "chunk_rows": chunk_rows, "schedule": schedule}
 
 
-def fft_four_step_batch(x, n1: int = 0, chunk_rows: int = 0, schedule: int = 0):
+def fft_four_step(x, n1: int = 0, chunk_rows: int = 0, schedule: int = 0, twiddle=None, *,
+                  allow_fused_schedule: bool = False):
+    """Two-pass four-step FFT (column pass + twiddle, in-place row pass).
+    ``schedule=2`` (one fused launch) only with ``allow_fused_schedule=True``."""
+    return _single("fft_four_step", x, None, _four_step_params(n1, chunk_rows, schedule, allow_fused_schedule),
+                   twiddle=twiddle)
+
+
+def fft_four_step_batch(x, n1: int = 0, chunk_rows: int = 0, schedule: int = 0, twiddle=None, *,
+                        allow_fused_schedule: bool = False):
     return _batched("fft_four_step_batch", x, None,
-                    {"n1": n1, "chunk_rows": chunk_rows, "schedule": schedule})
+                    _four_step_params(n1, chunk_rows, schedule, allow_fused_schedule), twiddle=twiddle)
 
 
-def fft_dit_fused(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64):
-    """Reference M1 name: all stages fused on chip (LDS kernel)."""
-    return _single("fft_dit_fused", x, None)
+def fft_dit_fused(x, block: int = 1024, tile: int = 64, twiddle=None):
+    """Reference M1 name (runner.py:209): all stages fused on chip (LDS
+    kernel, four-step above 32768 points)."""
+    _check_pow2_block(block)
+    return _single("fft_dit_fused", x, None, twiddle=twiddle)
 
 
-def fft_dit_matrix(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64, rows: int = 8):
-    """Reference M2 name: the dense-dot core on the fp32 matrix cores
-    (cores of 2..16384 points; the library's choice above)."""
-    return _single("fft_dit_matrix", x, None)
+def fft_dit_matrix(x, block: int = 1024, tile: int = 64, rows: int = 8, twiddle=None):
+    """Reference M2 name (runner.py:379): the dense-dot core on the fp32
+    matrix cores (cores of 2..16384 points; the library's choice above)."""
+    _check_pow2_block(block)
+    return _single("fft_dit_matrix", x, None, twiddle=twiddle)
 
 
-def fft_dif_matrix(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64, rows: int = 8):
-    return _single("fft_dif_matrix", x, None)
+def fft_dif_matrix(x, block: int = 1024, tile: int = 64, rows: int = 8, twiddle=None):
+    """Reference M2 DIF name (runner.py:445)."""
+    _check_pow2_block(block)
+    return _single("fft_dif_matrix", x, None, twiddle=twiddle)
 
 
-def fft_dit_matrix_batch(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64, rows: int = 8,
-                         variant: str = "spread"):
-    return _batched("fft_dit_matrix_batch", x, None)
+def fft_dit_matrix_batch(x, block: int = 1024, tile: int = 64, rows: int = 8, variant: str = "spread",
+                         twiddle=None):
+    """Reference M2 batch name (runner.py:956)."""
+    _check_pow2_block(block)
+    return _batched("fft_dit_matrix_batch", x, None, twiddle=twiddle, variant=variant)
 
 
-def fft_dif_matrix_batch(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64, rows: int = 8,
-                         variant: str = "spread"):
-    return _batched("fft_dif_matrix_batch", x, None)
+def fft_dif_matrix_batch(x, block: int = 1024, tile: int = 64, rows: int = 8, variant: str = "spread",
+                         twiddle=None):
+    """Reference M2 batch DIF name (runner.py:1038)."""
+    _check_pow2_block(block)
+    return _batched("fft_dif_matrix_batch", x, None, twiddle=twiddle, variant=variant)
 
 
-def fft_dit_grouped(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64, rows: int = 8,
-                    glog: int = 2, maxp: int = 4096, cells: int = 1):
-    """Reference M3 name: runs the LDS / four-step kernels on MI355X."""
-    return _single("fft_dit_grouped", x, None)
+def fft_dit_matrix_packet_batch(x, block: int = 1024, tile: int = 64, rows: int = 8, packets: int = 2,
+                                twiddle=None):
+    """Reference M2 packet-loop name (runner.py:1271, experimental there):
+    the same dense-dot matrix-core flow as fft_dit_matrix_batch."""
+    _check_pow2_block(block)
+    return _batched("fft_dit_matrix_batch", x, None, twiddle=twiddle)
 
 
-def fft_dif_grouped(x, block: int = DEFAULT_STAGE_BLOCK, tile: int = 64, rows: int = 8,
-                    glog: int = 2, maxp: int = 4096, cells: int = 1):
-    return _single("fft_dif_grouped", x, None)
+def fft_dit_grouped(x, block: int = 1024, tile: int = 64, rows: int = 8,
+                    glog: int = 2, maxp: int = 4096, cells: int = 1, twiddle=None):
+    """Reference M3 name (runner.py:603): runs the LDS / four-step kernels."""
+    _check_pow2_block(block)
+    return _single("fft_dit_grouped", x, None, twiddle=twiddle)
+
+
+def fft_dif_grouped(x, block: int = 1024, tile: int = 64, rows: int = 8,
+                    glog: int = 2, maxp: int = 4096, cells: int = 1, twiddle=None):
+    """Reference M3 DIF name (runner.py:685)."""
+    _check_pow2_block(block)
+    return _single("fft_dif_grouped", x, None, twiddle=twiddle)
 
 
 def _check_variant(variant: str) -> None:
-    if variant not in ("folded", "spread"):
-        raise ValueError(f"variant must be 'folded' or 'spread', got {variant!r}")
+    if variant not in ("spread", "folded"):
+        raise ValueError(f"variant must be 'spread' or 'folded', got {variant!r}")
 
 
-def bit_reverse_permute(x):
-    """Y[r][bit_reverse(i)] = X[r][i] (reference runner.py:1542-1552)."""
-    validate_tensor(x, "x", dtype=torch.complex64)
+def _check_pow2_block(block) -> None:
+    if block is not None:
+        log2_exact(block)
+
+
+def bit_reverse_permute(x, block: int = 1024):
+    """Y[r][bit_reverse(i)] = X[r][i] (reference runner.py:1542-1552), on a
+    rank-1 (N,) or rank-2 (B, N) complex64 tensor; ``block`` must be a power
+    of two (the kernel sizes its own launch)."""
+    if isinstance(x, torch.Tensor) and x.dim() == 1:
+        validate_input(x, "x", block=block, require_complex=True)
+    else:
+        validate_tensor(x, "x", dtype=torch.complex64, block=block)
     n = int(x.shape[-1])
     log2_exact(n)
     b = 1 if x.dim() == 1 else int(x.shape[0])
     out = torch.empty_like(x)
     dev = x.device.index if x.device.index is not None else torch.cuda.current_device()
-    with torch.cuda.device(dev):
-        native.bit_reverse_permute(x.data_ptr(), out.data_ptr(), n, b,
-                                   torch.cuda.current_stream(dev).cuda_stream)
+    with device_context(dev):
+        native.bit_reverse_permute(x.data_ptr(), out.data_ptr(), n, b, stream_handle(dev))
     return out
 
 
@@ -458,41 +526,73 @@ def twiddle_tables(n: int, device):
     return (torch.cos(ang).to(torch.float32).to(device), torch.sin(ang).to(torch.float32).to(device))
 
 
-def time_call(fn, *args, warmup: int = 5, trials: int = 50, **kwargs) -> float:
-    """Median wall time (ms) of fn(*args) with a device sync per trial."""
-    for _ in range(warmup):
-        fn(*args, **kwargs)
-    torch.cuda.synchronize()
-    ts = []
-    for _ in range(trials):
-        t0 = time.perf_counter()
-        fn(*args, **kwargs)
+def _sync() -> None:
+    if device_ready():
         torch.cuda.synchronize()
-        ts.append((time.perf_counter() - t0) * 1e3)
-    ts.sort()
-    return ts[len(ts) // 2]
 
 
-def time_call_detailed(fn, *args, warmup: int = 5, trials: int = 50, **kwargs) -> dict:
-    """Wall-time and HIP-event medians (ms) of fn(*args) on the current stream."""
+def time_call(fn, warmup: int = 5, iters: int = 20) -> float:
+    """Median API wall time in ms of ``fn()`` (reference runner.py:1560-1573):
+    ``warmup`` untimed calls, then ``iters`` calls each followed by a device
+    synchronisation; includes the host path, allocation and the sync."""
     for _ in range(warmup):
-        fn(*args, **kwargs)
-    torch.cuda.synchronize()
-    wall, ev = [], []
-    for _ in range(trials):
-        s = torch.cuda.Event(enable_timing=True)
-        e = torch.cuda.Event(enable_timing=True)
+        fn()
+    _sync()
+    samples = []
+    for _ in range(iters):
         t0 = time.perf_counter()
-        s.record()
-        fn(*args, **kwargs)
-        e.record()
-        torch.cuda.synchronize()
-        wall.append((time.perf_counter() - t0) * 1e3)
-        ev.append(s.elapsed_time(e))
-    wall.sort()
-    ev.sort()
-    return {"wall_ms_p50": wall[len(wall) // 2], "event_ms_p50": ev[len(ev) // 2],
-            "wall_ms_min": wall[0], "trials": trials}
+        fn()
+        _sync()
+        samples.append((time.perf_counter() - t0) * 1e3)
+    samples.sort()
+    return samples[len(samples) // 2]
+
+
+def _stats(xs):
+    if not xs:
+        return None
+    xs = sorted(xs)
+    return {"median": xs[len(xs) // 2], "min": xs[0], "p10": xs[max(0, int(0.10 * len(xs)))],
+            "p90": xs[min(len(xs) - 1, int(0.90 * len(xs)))], "trials": len(xs)}
+
+
+def time_call_detailed(fn, warmup: int = 10, trials: int = 50, seed: int = 0) -> dict:
+    """The reference's trial protocol (runner.py:1576-1635): ``warmup``
+    untimed calls, then ``trials`` calls in an order shuffled by
+    ``random.Random(seed)``, each bracketed by HIP events on the current
+    stream and a device synchronisation.  Returns ``{"api_ms": stats,
+    "kernel_ms": stats, "metric_note": str}`` with stats = ``{median, min,
+    p10, p90, trials}``; ``kernel_ms`` keeps only positive event times and
+    is None when there are none (or no GPU)."""
+    for _ in range(warmup):
+        fn()
+    _sync()
+    use_events = device_ready()
+    order = list(range(trials))
+    random.Random(seed).shuffle(order)
+    api, kern = [], []
+    for _ in order:
+        if use_events:
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            s.record()
+            fn()
+            e.record()
+            torch.cuda.synchronize()
+            api.append((time.perf_counter() - t0) * 1e3)
+            kt = s.elapsed_time(e)
+            if kt > 0:
+                kern.append(kt)
+        else:
+            t0 = time.perf_counter()
+            fn()
+            _sync()
+            api.append((time.perf_counter() - t0) * 1e3)
+    return {"api_ms": _stats(api), "kernel_ms": _stats(kern),
+            "metric_note": ("api_ms = synchronized wall time (host path + allocation + launch + sync); "
+                            "kernel_ms = HIP event elapsed time on the current stream (device time) when "
+                            "events report > 0, else null")}
 
 
 def time_native_graph(nplan: native.NativePlan, x: torch.Tensor, out: torch.Tensor, ws, reps: int = 20,

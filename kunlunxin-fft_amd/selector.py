@@ -275,6 +275,28 @@ def load_table(path: str = TABLE_PATH) -> dict:
     return table
 
 
+def assert_current_environment(table: dict) -> str:
+    """Freshness gate for measurement runs (reference selector.py:482-510):
+    raise ``RuntimeError`` unless the live environment fingerprint equals the
+    table's ``env_hash``, before any kernel launch; a table without one, or
+    an environment that cannot be fingerprinted, fails closed too.  Returns
+    the live hash so a run can record it."""
+    bound = table.get("env_hash") or ""
+    if not bound:
+        raise RuntimeError("selector table carries no env_hash; refusing to measure against it "
+                           "-- rebuild the table under the current environment")
+    from .envcheck import current_env_hash
+
+    cur = current_env_hash()
+    if cur is None:
+        raise RuntimeError("live environment fingerprint unknown (no GPU, or the library is not built); "
+                           "cannot verify the table -- failing closed")
+    if cur != bound:
+        raise RuntimeError(f"environment hash {cur} != table {bound} (device, runtime or library changed "
+                           "since the table was built); re-measure before producing new results")
+    return cur
+
+
 def _abstain(n, direction, batch, precision, reason, tt, td, norm) -> Selection:
     return Selection(n=n, direction=direction, batch=batch, precision=precision, source="abstain",
                      reason=reason, transform_type=tt, transform_direction=td,

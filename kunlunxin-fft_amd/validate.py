@@ -37,11 +37,13 @@ def validate_tensor(x, name: str = "x", *, dtype=None, ranks=(1, 2), last=None,
         log2_exact(block)
 
 
-def validate_input(x, name: str = "x", *, allow_n: int | None = None, block: int | None = None) -> None:
-    """Rank-1 complex64 contiguous GPU tensor with a power-of-two length."""
+def validate_input(x, name: str = "x", *, allow_n: int | None = None, block: int | None = None,
+                   require_complex: bool = True) -> None:
+    """Rank-1 contiguous GPU tensor with a power-of-two length, complex64
+    unless ``require_complex=False`` (reference validate.py:19-66)."""
     import torch
 
-    validate_tensor(x, name, dtype=torch.complex64, ranks=(1,), block=block)
+    validate_tensor(x, name, dtype=torch.complex64 if require_complex else None, ranks=(1,), block=block)
     log2_exact(x.numel())
     if allow_n is not None and x.numel() != allow_n:
         raise ValueError(f"{name} length {x.numel()} != expected {allow_n}")

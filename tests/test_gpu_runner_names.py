@@ -116,3 +116,88 @@ def test_twiddle_contract(gpu, fn, n):
         f(x, twiddle=(ref_tables[0].cpu(), ref_tables[1].cpu()))
     with pytest.raises(TypeError, match="tuple"):
         f(x, twiddle=[ref_tables[0], ref_tables[1]])
+
+
+# ---- the reference's full keyword sets (src/xpu/runner.py:118-1472) on the GPU
+
+BATCH_STAGE = ["fft_dit_batch", "fft_dif_batch", "fft_dit_radix4_batch", "fft_dif_radix4_batch"]
+
+
+@pytest.mark.parametrize("fn", BATCH_STAGE)
+@pytest.mark.parametrize("variant", ["spread", "folded"])
+@pytest.mark.parametrize("block", [64, 1024, 2048])
+def test_batch_stage_runners_reference_keywords(gpu, fn, variant, block):
+    """Both variants, the reference's default block (1024), a block above
+    a workgroup's 1024 threads (clamped) and a forward-roots twiddle table
+    give the oracle's transform; the twiddle table changes nothing."""
+    n, b = 1024, 4
+    x = torch.from_numpy(seeded(n, b, 37)).to(gpu)
+    f = getattr(runner, fn)
+    y = f(x, block=block, variant=variant).cpu().numpy()
+    check(y, ref_fft(x.cpu().numpy()), f"{fn} block={block} variant={variant}")
+    np.testing.assert_array_equal(f(x, block, variant, runner.twiddle_tables(n, gpu)).cpu().numpy(), y)
+
+
+@pytest.mark.parametrize("fn", ["fft_dit", "fft_dif", "fft_dit_radix4", "fft_dif_radix4"])
+@pytest.mark.parametrize("n", [4, 8, 2048])
+def test_stage_runners_default_block(gpu, fn, n):
+    """block=1024 (the reference's default) over fewer butterflies than
+    threads: the stage kernels' bounds checks hold."""
+    x = torch.from_numpy(seeded(n, 1, 38)).to(gpu)
+    check(getattr(runner, fn)(x).cpu().numpy(), ref_fft(x.cpu().numpy()), f"{fn} N={n}")
+
+
+@pytest.mark.parametrize("fn,args", [
+    ("fft_dit_fused", dict(block=256, tile=32)),
+    ("fft_dit_matrix", dict(block=512, tile=64, rows=16)),
+    ("fft_dif_matrix", dict(block=512, tile=128, rows=4)),
+    ("fft_dit_grouped", dict(block=1024, tile=64, rows=8, glog=3, maxp=2048, cells=2)),
+    ("fft_dif_grouped", dict(block=1024, tile=64, rows=8, glog=2, maxp=4096, cells=1)),
+])
+def test_alias_runners_reference_keywords(gpu, fn, args):
+    n = 4096
+    x = torch.from_numpy(seeded(n, 1, 39)).to(gpu)
+    y = getattr(runner, fn)(x, twiddle=runner.twiddle_tables(n, gpu), **args).cpu().numpy()
+    check(y, ref_fft(x.cpu().numpy()), f"runner.{fn} {args}")
+
+
+@pytest.mark.parametrize("fn", ["fft_dit_matrix_batch", "fft_dif_matrix_batch", "fft_dit_matrix_packet_batch"])
+def test_matrix_batch_runners_reference_keywords(gpu, fn):
+    n, b = 512, 3
+    x = torch.from_numpy(seeded(n, b, 40)).to(gpu)
+    kw = dict(block=1024, tile=64, rows=8, twiddle=runner.twiddle_tables(n, gpu))
+    kw.update({"packets": 2} if "packet" in fn else {"variant": "folded"})
+    y = getattr(runner, fn)(x, **kw).cpu().numpy()
+    check(y, ref_fft(x.cpu().numpy()), f"runner.{fn}")
+
+
+def test_bit_reverse_permute_block_keyword(gpu):
+    n = 256
+    x = torch.arange(n, dtype=torch.float32).to(torch.complex64).to(gpu)
+    y = runner.bit_reverse_permute(x, block=1024).cpu().real.to(torch.int64).numpy()
+    assert [int(y[oracle.bit_reverse(i, 8)]) for i in range(n)] == list(range(n))
+    with pytest.raises(ValueError, match="power of two"):
+        runner.bit_reverse_permute(x, block=1000)
+
+
+def test_time_call_detailed_on_a_plan(gpu):
+    """The reference's trial protocol on an execute: shuffled trials, api
+    wall time and device (event) time, both positive, device time the
+    smaller."""
+    from kunlunxin_fft_amd import plan_fft
+
+    plan = plan_fft("dit", 2048, batch=16)
+    x = torch.from_numpy(seeded(2048, 16, 41)).to(gpu)
+    d = runner.time_call_detailed(lambda: execute_fft_plan(plan, x), warmup=3, trials=20, seed=0)
+    assert d["api_ms"]["trials"] == 20 and d["kernel_ms"] is not None
+    assert 0 < d["kernel_ms"]["median"] <= d["api_ms"]["median"]
+    assert "api_ms" in d["metric_note"] and "kernel_ms" in d["metric_note"]
+    ms = runner.time_call(lambda: execute_fft_plan(plan, x), warmup=2, iters=10)
+    assert 0 < ms < 1000
+
+
+def test_xpu_context_guard(gpu):
+    prev = torch.cuda.current_device()
+    with runner.xpu_context(0) as idx:
+        assert idx == 0 and torch.cuda.current_device() == 0
+    assert torch.cuda.current_device() == prev

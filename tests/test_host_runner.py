@@ -47,8 +47,9 @@ def test_four_step_params_map_to_split_chunk_schedule_order():
 
 def test_stage_flows_validate_the_block():
     assert flow_params("fft_dit_batch", 1024, "c2c", 512, {}) == (native.FLOW_RADIX2_DIT, (512,))
-    with pytest.raises(ValueError):
-        flow_params("fft_dit", 1024, "c2c", 32, {})
+    # any power of two, as in the reference; the workgroup clamps to 64..1024 threads
+    assert flow_params("fft_dit", 1024, "c2c", 32, {}) == (native.FLOW_RADIX2_DIT, (64,))
+    assert flow_params("fft_dit", 1024, "c2c", 2048, {}) == (native.FLOW_RADIX2_DIT, (1024,))
     with pytest.raises(ValueError):
         flow_params("fft_dit", 1024, "c2c", 96, {})
     with pytest.raises(ValueError):
