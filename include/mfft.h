@@ -169,12 +169,18 @@ typedef struct {
  * and that `flow` can run the shape: at most 2^40 bytes of complex64 rows,
  * and no launch of 2^32 work-items or more (one dispatch's count is 32-bit;
  * MFFT_ERR_UNSUPPORTED, split the batch).  Uploads the twiddle tables and
- * allocates the workspace (the only allocations the library makes). */
+ * allocates the workspace: the only allocations the library makes per plan.
+ * Apart from them, the library holds one static device buffer of
+ * MFFT_NOALLOC_SCRATCH_BYTES per device for mfft_execute_noalloc. */
 int mfft_plan_create(mfft_plan** out, int64_t n, int64_t batch, int transform_type,
                      int transform_direction, int norm, int flow,
                      const int32_t* params, int nparams);
 
-/* Enqueue one transform of all `batch` rows.  No allocation, no host sync. */
+/* Enqueue one transform of all `batch` rows.  No allocation, no host sync.
+ * FOUR_STEP schedule 2 (params[2] = 2) only: a launch whose bounded wait
+ * gives up writes NaN from then on and this call still returns MFFT_OK (the
+ * failure is not known when the work is enqueued); synchronise, then check
+ * mfft_plan_sync_overruns == 0 before using the output. */
 int mfft_execute(const mfft_plan* plan, const void* in, void* out, void* stream);
 
 /* Caller-owned workspace.  The reference exposes neither a stream nor a
@@ -222,8 +228,9 @@ int mfft_execute_timed(const mfft_plan* plan, const void* in, void* out, void* w
  * callers that cannot allocate device memory at execute time (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * Same work and results as mfft_execute / mfft_execute_ws, but the scratch
- * of a plan that needs one (mfft_plan_workspace_size > 0: the stage flows
- * and the real flows around a non-fused core) comes from a static device
+ * of a plan that needs one (mfft_plan_workspace_size > 0: the stage flows,
+ * the real flows around a non-fused core, and the fused FOUR_STEP schedule's
+ * launch counters and Z ring) comes from a static device
  * buffer of MFFT_NOALLOC_SCRATCH_BYTES that the library holds on every
  * device it runs on until the process ends; the call itself allocates
  * nothing (no hipMalloc, no allocating library routine).  A plan needing
@@ -231,8 +238,10 @@ int mfft_execute_timed(const mfft_plan* plan, const void* in, void* out, void* w
  * Every call on one device shares that device's buffer: calls that overlap
  * in time on one device (two streams, two host threads) race, so serialise
  * them.  The buffer keeps whatever the last call left in it; no kernel
- * reads scratch it has not written in the same call, so nothing needs
- * clearing.  The first call on a device looks the buffer's address up once
+ * reads scratch it has not written in the same call (the fused schedule's
+ * counters are zeroed by a fill kernel at the start of every call, never by
+ * a memset, so a captured call replays correctly).  The first call on a
+ * device looks the buffer's address up once
  * (with that device current, as every execute requires). */
 #define MFFT_NOALLOC_SCRATCH_BYTES ((int64_t)32 << 20)
 int mfft_execute_noalloc(const mfft_plan* plan, const void* in, void* out, void* stream);

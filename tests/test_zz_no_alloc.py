@@ -2,8 +2,12 @@
 static scratch, through the C ABI (ctypes), against mfft_execute_ws with a
 torch-allocated workspace -- the same kernels, so the results must be
 bit-identical.  Two calls in a row share the static buffer, the second with
-a smaller input; a plan needing more scratch than the buffer is refused
-before any launch."""
+a smaller input; among them the fused four-step schedule, whose scratch
+carries state (launch counters, cleared by a fill kernel at the start of
+every call, and its ring of Z slots).  The same executes recorded into a HIP
+graph and replayed, with new inputs and eager work between replays, match
+eager executes every time.  A plan needing more scratch than the buffer is
+refused before any launch."""
 import numpy as np
 import pytest
 import torch
@@ -13,6 +17,10 @@ from kunlunxin_fft_amd import native
 pytestmark = pytest.mark.gpu
 
 LIMIT = 32 << 20  # MFFT_NOALLOC_SCRATCH_BYTES
+# fused-schedule queue settings (params[3]): lag 2, 2 items per dequeue, 6 Z
+# slots per XCD, 2 blocks per CU -- a ring of 8 XCDs x 6 x N complex64 that
+# fits the static buffer at N = 2^16 (24 MiB)
+FUSED_WORD = 2 | (2 << 8) | (6 << 16) | (2 << 24)
 
 # (n, batch, transform, direction, flow, params): the second of each pair is smaller
 PAIRS = [
@@ -26,6 +34,9 @@ PAIRS = [
      (1 << 12, 4, "c2c", "inverse", native.FLOW_RADIX4_DIF, ())),
     ((2048, 16, "c2c", "forward", native.FLOW_LDS_FUSED, ()),
      (256, 3, "c2c", "forward", native.FLOW_LDS_FUSED, ())),
+    # the fused schedule (params[2] = 2): counters + Z ring in the static buffer
+    ((1 << 16, 8, "c2c", "forward", native.FLOW_FOUR_STEP, (256, 0, 2, FUSED_WORD)),
+     (1 << 15, 3, "c2c", "inverse", native.FLOW_FOUR_STEP, (128, 0, 2, FUSED_WORD))),
 ]
 
 
@@ -57,6 +68,50 @@ def test_noalloc_matches_execute_ws(gpu, pair):
         torch.cuda.synchronize()
         assert torch.equal(y, y_ref), f"call {k}: N={n} B={b} {tt}"
         assert torch.isfinite(torch.view_as_real(y) if y.is_complex() else y).all()
+        assert p.sync_overruns() == 0
+
+
+GRAPH_CASES = [
+    (4096, 16, "c2c", "forward", native.FLOW_RADIX2_DIT, (256,)),
+    (1 << 17, 2, "r2c", "forward", native.FLOW_FOUR_STEP, (256,)),
+    (1 << 16, 4, "c2c", "forward", native.FLOW_FOUR_STEP, (256, 0, 2, FUSED_WORD)),
+]
+
+
+@pytest.mark.parametrize("case", GRAPH_CASES, ids=lambda c: f"{c[2]}-flow{c[4]}-N{c[0]}-p{len(c[5])}")
+def test_noalloc_under_graph_capture(gpu, case):
+    """The entry point's purpose: an execute recorded into a HIP graph with
+    no allocation.  Three replays, each on a new input copied into the
+    captured buffer, with an eager execute_ws of the same input between
+    them: every replay's output equals the eager one bit for bit."""
+    n, b, tt, td, flow, prm = case
+    print(f"noalloc graph case {tt} {td} flow={flow} N={n} B={b} params={prm}", flush=True)
+    p = native.NativePlan(n, b, tt, td, "backward", flow, prm, caller_workspace=True)
+    assert p.ws_bytes <= LIMIT
+    assert p.ws_bytes > 0 or tt == "r2c"  # the stage flow and the fused schedule use scratch
+    x, y_ref, y = _io(n, b, tt, gpu, seed=500 + n)
+    ws = torch.empty(max(p.ws_bytes, 1), dtype=torch.uint8, device=gpu)
+    side = torch.cuda.Stream(gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        p.execute_noalloc(x.data_ptr(), y.data_ptr(), side.cuda_stream)  # first call outside the capture
+        side.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            p.execute_noalloc(x.data_ptr(), y.data_ptr(), side.cuda_stream)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream(gpu).cuda_stream
+    for r in range(3):
+        x2, _, _ = _io(n, b, tt, gpu, seed=600 + 13 * r + n)
+        x.copy_(x2)
+        y.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        p.execute_ws(x.data_ptr(), y_ref.data_ptr(), ws.data_ptr() if p.ws_bytes else 0, p.ws_bytes, st)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ref), f"replay {r}: N={n} B={b} {tt} params={prm}"
+    assert p.sync_overruns() == 0
+    del graph
 
 
 def test_noalloc_refuses_plans_beyond_the_static_buffer(gpu):
