@@ -20,6 +20,15 @@ for R2C forward and C2R inverse with the default norm, against the M0 real
 flow, and stored as exact-semantic entries: the real modes of the LDS kernel
 and the four-step around a half-length core have their own best settings.
 
+A rebuild never silently regresses a cell the deployed table won: every
+cell whose decision changed is re-timed against the previous decision,
+alternately, under the current environment, and where the previous one is
+faster by more than the guard it is kept as a ``previous_fallbacks`` cell,
+bound to this table's environment, profile, precision and device and to the
+sha256 of the previous table and of the paired samples
+(``carry_previous_fallbacks``); the previous table's own fallback cells are
+reconfirmed the same way or dropped with a reason.
+
 Timing: forward C2C complex64 (and the real cells), inputs resident on the GPU.  Cells under
 64 MiB: ``reps`` back-to-back executes recorded into one HIP graph, the graph
 replayed between HIP events, median of ``rounds`` replays (ms per execute of
@@ -56,6 +65,128 @@ REAL_NORM = "backward"
 # again against it, alternately, this many times each, before a cell is decided
 CONFIRM_PCT = 20.0
 CONFIRM_ROUNDS = 5
+
+
+def _sha256_file(path: str) -> str:
+    import hashlib
+
+    with open(path, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
+
+
+def _sha256_json(obj) -> str:
+    import hashlib
+
+    return hashlib.sha256(json.dumps(obj, sort_keys=True, separators=(",", ":")).encode()).hexdigest()
+
+
+def cell_key(entry: dict) -> tuple:
+    """(N, batch, direction, transform_type, transform_direction,
+    normalization) of an entry; a legacy entry (no semantic triple) is the
+    forward C2C cell it was measured on."""
+    from kunlunxin_fft_amd.selector import semantic_key_of
+
+    sk = semantic_key_of(entry) or ("c2c", "forward", "backward")
+    return (entry["N"], entry["batch"], entry["direction"]) + tuple(sk)
+
+
+def _geometry(entry: dict) -> tuple:
+    """What an entry runs: runner name, block and parameters."""
+    return (entry.get("executed"), entry.get("block"), json.dumps(entry.get("params") or {}, sort_keys=True))
+
+
+def carry_previous_fallbacks(prev: "dict | None", prev_sha: "str | None", table: dict, paired, guard: float,
+                             rounds: int = CONFIRM_ROUNDS) -> tuple:
+    """Per-cell regression guard of a rebuild (the reference's
+    previous-fallback carry and reconfirm, scripts/build_selector_table.py:
+    884-1106, under the binding contract of src/xpu/selector.py:260-340).
+
+    ``prev`` is the previously deployed table (its file sha256 ``prev_sha``),
+    ``table`` the rebuilt one (its ``entries``, env/profile/precision
+    binding and ``env`` device identity already set).  For every rebuilt
+    cell whose previous decision (its previous fallback cell, else its exact
+    semantic entry, else its legacy entry) runs something else,
+    ``paired(rebuilt_entry, previous_entry)`` times the two alternately,
+    ``rounds`` times each, under the current environment, and returns
+    ``(rebuilt_samples_ms, previous_samples_ms)``.  When the rebuilt choice
+    is slower by more than ``guard`` percent (median against median), the
+    previous decision is kept as a ``previous_fallbacks`` cell with the exact
+    semantic triple and a ``fallback-env-binding-v1`` provenance bound to the
+    rebuilt table's environment, profile, precision and device, the previous
+    table's sha256 and the sha256 of the paired samples.  The previous
+    table's own fallback cells are reconfirmed the same way: kept while they
+    still clear the guard, dropped with a reason otherwise.
+
+    Nothing is carried across environments: a previous table bound to
+    another env, profile or precision contributes no cell (one reason says
+    why), and a previous fallback cell that fails its own binding, or whose
+    parameters left the published design space, is dropped with a reason.
+    Returns ``(fallbacks, drop_reasons, paired_records)``."""
+    from kunlunxin_fft_amd.selector import (DEVICE_IDENTITY_KEYS, FALLBACK_CARRY_CONTRACT,
+                                            entry_contract_violations, fallback_binding_violations,
+                                            find_entry)
+
+    if not prev:
+        return [], [], []
+    for key in ("env_hash", "profile_hash", "precision"):
+        if not prev.get(key) or prev.get(key) != table.get(key):
+            return [], [f"previous table {key} {prev.get(key)!r} != rebuilt table {table.get(key)!r}: "
+                        "nothing carried across environments (re-measure instead)"], []
+    drops: list[str] = []
+    prev_fbs = list(prev.get("previous_fallbacks") or [])
+    if prev_fbs and fallback_binding_violations(prev):
+        drops += [f"previous fallback cells dropped (binding contract): {m}"
+                  for m in fallback_binding_violations(prev)]
+        prev = dict(prev, previous_fallbacks=[])
+        prev_fbs = []
+    ident = {k: (table.get("env") or {}).get(k) for k in DEVICE_IDENTITY_KEYS}
+    rebuilt = {cell_key(e): e for e in table.get("entries", [])}
+    for fb in prev_fbs:
+        if cell_key(fb) not in rebuilt:
+            drops.append(f"{cell_key(fb)}: previous fallback cell not in the rebuilt sweep -- dropped")
+    fallbacks, records = [], []
+    for key, new in rebuilt.items():
+        old = find_entry(prev, key[0], key[1], key[2], *key[3:])
+        if old is None or _geometry(old) == _geometry(new):
+            continue
+        was_fallback = any(old is f for f in prev_fbs)
+        bad = entry_contract_violations(old)
+        if bad:
+            if was_fallback:
+                drops.append(f"{key}: previous fallback outside the published design space ({bad[0]}) -- dropped")
+            continue
+        new_s, old_s = paired(new, old)
+        new_ms, old_ms = statistics.median(new_s), statistics.median(old_s)
+        delta = new_ms / old_ms - 1.0
+        rec = {"cell": list(key), "rebuilt": list(_geometry(new)), "previous": list(_geometry(old)),
+               "rebuilt_ms": [round(v, 6) for v in new_s], "previous_ms": [round(v, 6) for v in old_s],
+               "selector_vs_previous": round(delta, 5)}
+        records.append(rec)
+        if delta <= guard / 100.0:
+            if was_fallback:
+                drops.append(f"{key}: rebuilt choice within {delta:+.2%} of the previous fallback "
+                             f"(guard {guard}%) -- fallback dropped")
+            continue
+        fb = json.loads(json.dumps(old))
+        fb["transform_type"], fb["transform_direction"], fb["normalization"] = key[3:]
+        prov = dict(fb.get("previous_fallback_provenance") or {})
+        prov.update({
+            "carry_contract": FALLBACK_CARRY_CONTRACT,
+            "source_env_hash": table["env_hash"], "source_profile_hash": table["profile_hash"],
+            "source_precision": table["precision"], "source_device": ident,
+            "source_table_sha256": prev_sha, "source_result_sha256": _sha256_json(rec),
+            "paired_confirm": f"table_builder paired re-timing: {rounds} alternating timings each of the rebuilt "
+                              "and the previous choice under the rebuilt table's environment",
+            "selector_vs_previous": round(delta, 5), "selector_ms": round(new_ms, 6),
+            "previous_ms": round(old_ms, 6),
+            "regression_reason": f"rebuilt choice {new.get('executed')} slower than the previous deployed "
+                                 f"{old.get('executed')} by {delta:+.2%} (> {guard}%)",
+        })
+        fb["previous_fallback_provenance"] = prov
+        fb["reason"] = (f"previous deployed {old.get('executed')} {json.dumps(old.get('params') or {}, sort_keys=True)} "
+                        f"kept: the rebuilt choice is {delta:+.1%} slower in paired re-timing")
+        fallbacks.append(fb)
+    return fallbacks, drops, records
 
 
 def cells(quick: bool = False):
@@ -188,6 +319,10 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--rounds", type=int, default=3)
+    ap.add_argument("--previous", default=None,
+                    help="previously deployed table to guard against (default: the package's "
+                         "config/selector_table.json when present)")
+    ap.add_argument("--no-carry", action="store_true", help="write no previous_fallbacks cells")
     args = ap.parse_args()
 
     import torch
@@ -200,7 +335,7 @@ def main() -> int:
     from kunlunxin_fft_amd.config import DesignSpace, DeviceProfile
     from kunlunxin_fft_amd.entry import ExecutionPlan
     from kunlunxin_fft_amd.runner import get_native_plan, output_spec, time_native_graph, workspace_for
-    from kunlunxin_fft_amd.selector import GUARD_PCT
+    from kunlunxin_fft_amd.selector import GUARD_PCT, TABLE_PATH
 
     space = DesignSpace.load()
     env = envcheck.collect()
@@ -364,6 +499,43 @@ def main() -> int:
         "sources": ["kunlunxin-fft_amd/table_builder.py live sweep"],
         "entries": entries, "previous_fallbacks": [],
     }
+
+    # ---- per-cell regression guard against the previously deployed table
+    prev_path = args.previous or TABLE_PATH
+    prev = prev_sha = None
+    if not args.no_carry and os.path.exists(prev_path):
+        try:
+            prev = pkg.load_table(prev_path)
+            prev_sha = _sha256_file(prev_path)
+        except pkg.ConfigError as e:
+            print(f"previous table {prev_path} refused by the loader ({e}); nothing carried", file=sys.stderr)
+            prev = None
+    if prev is not None:
+        def paired(new_e, old_e):
+            n, b, d = new_e["N"], new_e["batch"], new_e["direction"]
+            tt, td, _ = cell_key(new_e)[3:]
+            if tt == "r2c":
+                x = torch.randn((b, n), dtype=torch.float32, device=dev, generator=gen)
+            else:
+                m = n // 2 + 1 if tt == "c2r" else n
+                x = torch.randn((m,) if b == 1 else (b, m), dtype=torch.complex64, device=dev, generator=gen)
+            got = ([], [])
+            for _ in range(CONFIRM_ROUNDS):
+                for i, e in enumerate((new_e, old_e)):
+                    got[i].append(time_runner(e["executed"], n, b, e["block"], e.get("params") or {}, x, tt, td))
+            return got
+
+        fbs, drops, records = carry_previous_fallbacks(prev, prev_sha, table, paired, GUARD_PCT)
+        table["previous_table_sha256"] = prev_sha
+        table["previous_fallbacks"] = fbs
+        if drops:
+            table["previous_fallbacks_dropped"] = drops
+        sweep.append({"paired_with_previous": records})
+        for fb in fbs:
+            print(f"previous fallback kept: {cell_key(fb)} -> {fb['executed']} "
+                  f"({fb['previous_fallback_provenance']['selector_vs_previous']:+.2%})", flush=True)
+        for m in drops:
+            print(f"previous_fallbacks: {m}", file=sys.stderr, flush=True)
     with open(args.out, "w") as f:
         json.dump(table, f, indent=1)
     with open(os.path.splitext(args.out)[0] + "_sweep.json", "w") as f:
