@@ -41,9 +41,10 @@ Also reported:
   {16, 64}); ``config3``: the same for inverse C2C, R2C and C2R at N in {256, 4096}, B in {1, 64}
   (real transforms count 4N + 8(N/2+1) bytes per row); ``config4``: the same for N=2^20 B=1 and
   N=2^16 B=256;
-* ``real_per_size``: R2C forward and C2R inverse at the same N and B (the
-  selected plans), GB/s and fraction of peak from HIP events in cyclic order,
-  counting 4N + 8(N/2+1) bytes per row;
+* ``real_per_size``: R2C forward and C2R inverse at the same N and twice the
+  batch, i.e. the same bytes per launch as the C2C row (the selected plans),
+  GB/s and fraction of peak from HIP events in cyclic order, counting
+  4N + 8(N/2+1) bytes per row;
 * ``per_size[].vendor_*``: torch.fft.fft (rocFFT) on the same inputs, a
   comparison column only;
 * ``config5``: the selector sweep (N = 16 .. 2^14, B in {1, 16, 64, 256}):
@@ -202,6 +203,13 @@ def compact_line(full: dict, detail: "str | None" = None) -> dict:
 
 def batch_for(n: int) -> int:
     return max(64, (1 << 25) // n)
+
+
+def real_batch_for(n: int) -> int:
+    """R2C/C2R rows: twice the C2C batch, the same bytes per launch (a
+    real row moves 4N + 8(N/2+1) bytes, about half of a complex row's 16N),
+    so that both transforms are compared at one launch size and working set."""
+    return 2 * batch_for(n)
 
 
 def main() -> int:
@@ -536,14 +544,15 @@ def main() -> int:
         for c in cfg4:
             log(f"config4: {c}")
 
-    # ---- R2C and C2R throughput at the same sizes and batches (selected plans),
-    # timed in cyclic order like per_size; algorithmic bytes per row are
-    # 4N (real side) + 8(N/2+1) (half spectrum)
+    # ---- R2C and C2R throughput at the same sizes (selected plans), twice
+    # the C2C batch so that a launch moves the same bytes as the C2C row
+    # (algorithmic bytes per row are 4N (real side) + 8(N/2+1) (half
+    # spectrum), about half of C2C's 16N), timed in cyclic order like per_size
     real_rows = []
     if not args.no_real:
         rwork = []
         for n in sizes:
-            b = batch_for(n)
+            b = real_batch_for(n)
             xr = torch.randn((b, n), dtype=torch.float32, device=dev, generator=gen)
             xc = torch.randn((b, n // 2 + 1), dtype=torch.complex64, device=dev, generator=gen)
             for tt, td, x in (("r2c", "forward", xr), ("c2r", "inverse", xc)):
@@ -567,7 +576,7 @@ def main() -> int:
             ms = statistics.median(s.elapsed_time(e) for s, e in revs[i])
             gbps = b * (4 * n + 8 * (n // 2 + 1)) / (ms * 1e-3) / 1e9
             real_rows.append({"n": n, "batch": b, "transform": tt, "executed": plan.executed,
-                              "flow": nplan.flow_name, "launches": int(nplan.info.launches), "ms": round(ms, 5),
+                              "fallback": plan.fallback, "flow": nplan.flow_name, "launches": int(nplan.info.launches), "ms": round(ms, 5),
                               "gbps": round(gbps, 1), "frac_hbm": round(gbps / PEAK_GBPS, 4),
                               "split": ([int(nplan.info.n1), int(nplan.info.n2), int(nplan.info.chunk_rows) or b]
                                         if nplan.info.n1 else None)})

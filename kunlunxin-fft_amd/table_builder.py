@@ -15,10 +15,11 @@ otherwise the cell keeps M0.  The table is bound to the device profile hash
 and the live environment fingerprint, so it selects only on the stack it was
 measured on.
 
-The roofline rows (N = 2^10..2^20, B = max(64, 2^25/N)) are also measured
-for R2C forward and C2R inverse with the default norm, against the M0 real
-flow, and stored as exact-semantic entries: the real modes of the LDS kernel
-and the four-step around a half-length core have their own best settings.
+The roofline rows (N = 2^10..2^20, B = max(64, 2^25/N), and twice that
+batch, where a real launch moves the C2C row's bytes) are also measured for
+R2C forward and C2R inverse with the default norm, against the M0 real flow,
+and stored as exact-semantic entries: the real modes of the LDS kernel and
+the four-step around a half-length core have their own best settings.
 
 A rebuild never silently regresses a cell the deployed table won: every
 cell whose decision changed is re-timed against the previous decision,
@@ -187,6 +188,13 @@ def carry_previous_fallbacks(prev: "dict | None", prev_sha: "str | None", table:
                         f"kept: the rebuilt choice is {delta:+.1%} slower in paired re-timing")
         fallbacks.append(fb)
     return fallbacks, drops, records
+
+
+def real_cells():
+    """(N, batch) of the exact-semantic real entries: the roofline rows'
+    batch, and twice it (the same bytes per launch as the C2C row, which
+    bench.py's real rows use)."""
+    return [(n, b) for n in ROOF_SIZES for b in (max(64, (1 << 25) // n), 2 * max(64, (1 << 25) // n))]
 
 
 def cells(quick: bool = False):
@@ -452,8 +460,7 @@ def main() -> int:
                   f"[{time.time() - t_start:.0f}s]", flush=True)
         del x
     # ---- real transforms at the roofline rows: exact-semantic entries
-    for n in ([] if args.quick else ROOF_SIZES):
-        b = max(64, (1 << 25) // n)
+    for n, b in ([] if args.quick else real_cells()):
         for tt, td in REAL_SEMANTICS:
             if tt == "r2c":
                 x = torch.randn((b, n), dtype=torch.float32, device=dev, generator=gen)
