@@ -331,12 +331,20 @@ def _single(name, x, block, params=None, twiddle=None):
     return run(name, x, 1, x.numel(), block=block, params=params, norm="backward")
 
 
-def _batched(name, x, block, params=None, twiddle=None, variant=None):
+def _batched(name, x, block, params=None, twiddle=None, variant=None, spread_only=False):
+    """A runner over a (B, N) batch: the reference's batch contract
+    (runner.py:757-778: rank-2 contiguous complex64 on the GPU, N and B
+    powers of two, variant 'spread' or 'folded'), then the native flow.
+    ``spread_only``: the reference lowers only 'spread' for this runner
+    (radix-4 and matrix batches) and refuses 'folded' with ValueError."""
     if variant is not None:
         _check_variant(variant)
+    if spread_only and variant != "spread":
+        raise ValueError(f"{name} lowers variant='spread' only (as the reference); got variant={variant!r}")
     validate_batch_input(x, "x", block=block)
-    check_twiddle(twiddle, x)
     b, n = int(x.shape[0]), int(x.shape[1])
+    log2_exact(b)
+    check_twiddle(twiddle, x)
     y = run(name, x, b, n, block=block, params=params, norm="backward")
     return y.reshape(b, n)
 
@@ -349,9 +357,11 @@ def _batched(name, x, block, params=None, twiddle=None, variant=None):
 # ``packets`` shape the reference's Triton programs and have no counterpart
 # in the HIP kernels; they are accepted and ignored.  ``variant`` is
 # 'spread' or 'folded' (the batch always folds into one 1-D grid here; both
-# compute the same values).  ``twiddle`` must hold the forward roots
-# (check_twiddle).  Batches need not be powers of two (the reference's
-# stage runners require it; every flow here runs any B >= 1).
+# compute the same values), except for the radix-4 and matrix batches,
+# which take 'spread' only, as in the reference.  ``twiddle`` must hold the
+# forward roots (check_twiddle).  The runner functions take power-of-two
+# batches, as the reference's do; plans (``execute_fft_plan``) run any
+# B >= 1.
 
 def fft_dit(x, block: int = 1024, twiddle=None):
     """M0 radix-2 DIT: log2(N) stage launches, bit reversal folded into stage 0
@@ -392,12 +402,12 @@ def fft_dif_radix4(x, block: int = 1024, twiddle=None):
 
 def fft_dit_radix4_batch(x, block: int = 1024, variant: str = "spread", twiddle=None):
     """M5 batch (reference runner.py:1112)."""
-    return _batched("fft_dit_radix4_batch", x, block, twiddle=twiddle, variant=variant)
+    return _batched("fft_dit_radix4_batch", x, block, twiddle=twiddle, variant=variant, spread_only=True)
 
 
 def fft_dif_radix4_batch(x, block: int = 1024, variant: str = "spread", twiddle=None):
     """M5 batch DIF (reference runner.py:1193)."""
-    return _batched("fft_dif_radix4_batch", x, block, twiddle=twiddle, variant=variant)
+    return _batched("fft_dif_radix4_batch", x, block, twiddle=twiddle, variant=variant, spread_only=True)
 
 
 def fft_lds_fused(x, elems: int = 0, twiddle=None):
@@ -456,21 +466,31 @@ def fft_dit_matrix_batch(x, block: int = 1024, tile: int = 64, rows: int = 8, va
                          twiddle=None):
     """Reference M2 batch name (runner.py:956)."""
     _check_pow2_block(block)
-    return _batched("fft_dit_matrix_batch", x, None, twiddle=twiddle, variant=variant)
+    return _batched("fft_dit_matrix_batch", x, None, twiddle=twiddle, variant=variant, spread_only=True)
 
 
 def fft_dif_matrix_batch(x, block: int = 1024, tile: int = 64, rows: int = 8, variant: str = "spread",
                          twiddle=None):
     """Reference M2 batch DIF name (runner.py:1038)."""
     _check_pow2_block(block)
-    return _batched("fft_dif_matrix_batch", x, None, twiddle=twiddle, variant=variant)
+    return _batched("fft_dif_matrix_batch", x, None, twiddle=twiddle, variant=variant, spread_only=True)
 
 
 def fft_dit_matrix_packet_batch(x, block: int = 1024, tile: int = 64, rows: int = 8, packets: int = 2,
                                 twiddle=None):
     """Reference M2 packet-loop name (runner.py:1271, experimental there):
-    the same dense-dot matrix-core flow as fft_dit_matrix_batch."""
+    the same dense-dot matrix-core flow as fft_dit_matrix_batch, with the
+    reference's checks of ``packets`` (a power of two, at most 2, dividing
+    B), which only concern its Triton program."""
     _check_pow2_block(block)
+    if isinstance(x, torch.Tensor) and x.dim() == 2:
+        b = int(x.shape[0])
+        if packets < 1 or (packets & (packets - 1)) != 0:
+            raise ValueError(f"packets must be a power of two, got {packets}")
+        if packets > 2:
+            raise ValueError(f"packets={packets} exceeds the reference program's ceiling of 2")
+        if b % packets != 0:
+            raise ValueError(f"packets={packets} must divide batch B={b}")
     return _batched("fft_dit_matrix_batch", x, None, twiddle=twiddle)
 
 

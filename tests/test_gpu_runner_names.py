@@ -133,6 +133,10 @@ def test_batch_stage_runners_reference_keywords(gpu, fn, variant, block):
     n, b = 1024, 4
     x = torch.from_numpy(seeded(n, b, 37)).to(gpu)
     f = getattr(runner, fn)
+    if "radix4" in fn and variant == "folded":  # the reference lowers 'spread' only for radix-4 batches
+        with pytest.raises(ValueError, match="spread"):
+            f(x, block=block, variant=variant)
+        return
     y = f(x, block=block, variant=variant).cpu().numpy()
     check(y, ref_fft(x.cpu().numpy()), f"{fn} block={block} variant={variant}")
     np.testing.assert_array_equal(f(x, block, variant, runner.twiddle_tables(n, gpu)).cpu().numpy(), y)
@@ -163,12 +167,39 @@ def test_alias_runners_reference_keywords(gpu, fn, args):
 
 @pytest.mark.parametrize("fn", ["fft_dit_matrix_batch", "fft_dif_matrix_batch", "fft_dit_matrix_packet_batch"])
 def test_matrix_batch_runners_reference_keywords(gpu, fn):
-    n, b = 512, 3
+    n, b = 512, 4
     x = torch.from_numpy(seeded(n, b, 40)).to(gpu)
     kw = dict(block=1024, tile=64, rows=8, twiddle=runner.twiddle_tables(n, gpu))
-    kw.update({"packets": 2} if "packet" in fn else {"variant": "folded"})
+    kw.update({"packets": 2} if "packet" in fn else {"variant": "spread"})
     y = getattr(runner, fn)(x, **kw).cpu().numpy()
     check(y, ref_fft(x.cpu().numpy()), f"runner.{fn}")
+
+
+def test_batch_runner_contract_errors(gpu):
+    """The reference's batch-runner errors (test_fft.py:405-419, 456-465,
+    483-497) on the GPU, before any launch: 'folded' for the matrix and
+    radix-4 batches, a rank-1 input, a block that is not a power of two,
+    a batch that is not a power of two, and the packet runner's limits."""
+    good = torch.complex(torch.ones(4, 64, device=gpu), torch.zeros(4, 64, device=gpu))
+    for fn in ("fft_dit_matrix_batch", "fft_dif_matrix_batch", "fft_dit_radix4_batch", "fft_dif_radix4_batch"):
+        with pytest.raises(ValueError, match="spread"):
+            getattr(runner, fn)(good, variant="folded")
+    with pytest.raises(ValueError):
+        runner.fft_dit_matrix_batch(good.view(-1))
+    with pytest.raises(ValueError):
+        runner.fft_dit_matrix_batch(good, block=1000)
+    with pytest.raises(ValueError, match="power of two"):
+        runner.fft_dit_batch(torch.ones((3, 64), dtype=torch.complex64, device=gpu))
+    x16 = torch.ones((16, 1024), dtype=torch.complex64, device=gpu)
+    with pytest.raises(ValueError, match="ceiling"):
+        runner.fft_dit_matrix_packet_batch(x16, packets=4)
+    with pytest.raises(ValueError, match="power of two"):
+        runner.fft_dit_matrix_packet_batch(x16, packets=3)
+    with pytest.raises(ValueError, match="divide"):
+        runner.fft_dit_matrix_packet_batch(x16[:1], packets=2)
+    for packets in (1, 2):
+        y = runner.fft_dit_matrix_packet_batch(x16, packets=packets).cpu().numpy()
+        check(y, np.fft.fft(x16.cpu().numpy().astype(np.complex128), axis=-1), f"packet batch packets={packets}")
 
 
 def test_bit_reverse_permute_block_keyword(gpu):

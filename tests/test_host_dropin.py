@@ -96,6 +96,29 @@ def test_batch_runners_reject_an_unknown_variant():
             getattr(runner, name)(x, variant="tiled")
 
 
+def test_radix4_and_matrix_batches_take_spread_only():
+    """reference test_fft.py:405-419, 456-465: 'folded' is refused, naming 'spread'."""
+    x = torch.zeros((4, 64), dtype=torch.complex64)
+    for name in ("fft_dit_radix4_batch", "fft_dif_radix4_batch", "fft_dit_matrix_batch", "fft_dif_matrix_batch"):
+        with pytest.raises(ValueError, match="spread"):
+            getattr(runner, name)(x, variant="folded")
+    # the M4 batch runners lower both variants
+    for name in ("fft_dit_batch", "fft_dif_batch"):
+        with pytest.raises(RuntimeError, match="GPU"):
+            getattr(runner, name)(x, variant="folded")
+
+
+def test_packet_batch_checks_packets():
+    """reference test_fft.py:483-497: packets a power of two, at most 2, dividing B."""
+    x = torch.zeros((16, 1024), dtype=torch.complex64)
+    with pytest.raises(ValueError, match="ceiling"):
+        runner.fft_dit_matrix_packet_batch(x, packets=4)
+    with pytest.raises(ValueError, match="power of two"):
+        runner.fft_dit_matrix_packet_batch(x, packets=3)
+    with pytest.raises(ValueError, match="divide"):
+        runner.fft_dit_matrix_packet_batch(torch.zeros((1, 1024), dtype=torch.complex64), packets=2)
+
+
 def test_fused_schedule_needs_the_opt_in():
     x = torch.zeros((2, 1 << 16), dtype=torch.complex64)
     with pytest.raises(ValueError, match="allow_fused_schedule"):
