@@ -269,6 +269,29 @@ int mfft_plan_sync_overruns(const mfft_plan* plan, int64_t* count);
  * (runner.bit_reverse_permute, runner.py:1542-1552); n a power of two. */
 int mfft_bit_reverse_permute(const void* in, void* out, int64_t n, int64_t batch, void* stream);
 
+/* The dedicated real-transform epilogues as standalone launches, for a
+ * caller that runs the half-length (n/2-point) complex core itself
+ * (runner.r2c_stitch / c2r_pre / c2r_unpack, runner.py:1687-1767).  The
+ * plans fuse the same arithmetic into their kernels; these take no plan and
+ * allocate nothing (the roots exp(-2 pi i k / n) are computed in the
+ * kernel).  n a power of two in [4, 2^20], `batch` rows, device pointers
+ * that do not overlap, enqueued on `stream`.
+ *   mfft_r2c_stitch: z [batch][n/2] complex64 (the unnormalised forward
+ *     FFT of the packed pairs x[2m] + i x[2m+1]) -> x [batch][n/2+1]
+ *     complex64, the real input's spectrum times `scale` (imaginary parts
+ *     of bins 0 and n/2 exactly 0).
+ *   mfft_c2r_pre: x [batch][n/2+1] complex64 half spectrum (imaginary parts
+ *     of bins 0 and n/2 ignored) -> z [batch][n/2] complex64, the input of
+ *     the half-length core.
+ *   mfft_c2r_unpack: u [batch][n/2] complex64, the unnormalised FORWARD
+ *     n/2-point FFT of mfft_c2r_pre's output -> out [batch][n] float32 real
+ *     samples times `scale` (2 * the norm's inverse scale: 2/n for
+ *     "backward"); read in mirror order, which turns the forward core into
+ *     the inverse one. */
+int mfft_r2c_stitch(const void* z, void* x, int64_t n, int64_t batch, float scale, void* stream);
+int mfft_c2r_pre(const void* x, void* z, int64_t n, int64_t batch, void* stream);
+int mfft_c2r_unpack(const void* u, void* out, int64_t n, int64_t batch, float scale, void* stream);
+
 /* The twiddle + transpose boundary of a composed four-step whose sub-FFTs
  * run elsewhere (the reference's run_hybrid, adapter_hybrid.py:294-301, a
  * fused "transpose + twiddle" pass between two vendor sub-FFT stages): for

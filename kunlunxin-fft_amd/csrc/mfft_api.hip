@@ -912,6 +912,47 @@ int mfft_twiddle_transpose(const void* in, void* out, int64_t rows, int64_t cols
     return e == hipSuccess ? MFFT_OK : hip_fail(e, "kernel launch");
 }
 
+namespace {
+// The shared contract of the standalone real epilogues (the reference's
+// _validate_real_half, runner.py:1661-1678): n a power of two in [4, 2^20],
+// batch >= 1, device pointers that do not overlap, 8-byte aligned.
+int real_epilogue(int kind, const void* in, void* out, int64_t n, int64_t batch, float scale, void* stream) {
+    g_err.clear();
+    if (!in || !out) return fail(MFFT_ERR_VALUE, "in and out must not be NULL");
+    const int logn = log2_exact(n);
+    if (logn < 2 || logn > mfft::kMaxLog2N)
+        return fail(MFFT_ERR_VALUE, "the real epilogues need N a power of two in [4, 2^%d], got %lld",
+                    mfft::kMaxLog2N, (long long)n);
+    if (batch < 1) return fail(MFFT_ERR_VALUE, "batch must be >= 1");
+    if (batch > ((int64_t)1 << 37) / n) return fail(MFFT_ERR_VALUE, "batch too large (over 2^40 bytes)");
+    const int64_t np = n >> 1;
+    const int64_t per_row = kind == 0 ? np + 1 : np;  // output values (threads) per row
+    if (!mfft::launch_fits((batch * per_row + 255) / 256, 256))
+        return fail(MFFT_ERR_UNSUPPORTED, "batch=%lld of n=%lld needs a launch of 2^32 work-items or more; "
+                    "split the batch", (long long)batch, (long long)n);
+    if (!std::isfinite(scale)) return fail(MFFT_ERR_VALUE, "scale must be finite");
+    const size_t in_bytes = (size_t)batch * (size_t)(kind == 1 ? np + 1 : np) * 8;
+    const size_t out_bytes = (size_t)batch * (size_t)(kind == 0 ? np + 1 : np) * 8;
+    if ((const char*)in < (const char*)out + out_bytes && (const char*)out < (const char*)in + in_bytes)
+        return fail(MFFT_ERR_VALUE, "in and out must not overlap");
+    if ((((uintptr_t)in) | ((uintptr_t)out)) & 7) return fail(MFFT_ERR_VALUE, "in and out must be 8-byte aligned");
+    const hipError_t e = mfft::launch_real_epilogue(kind, in, out, n, batch, scale, (hipStream_t)stream);
+    return e == hipSuccess ? MFFT_OK : hip_fail(e, "kernel launch");
+}
+}  // namespace
+
+int mfft_r2c_stitch(const void* z, void* x, int64_t n, int64_t batch, float scale, void* stream) {
+    return real_epilogue(0, z, x, n, batch, scale, stream);
+}
+
+int mfft_c2r_pre(const void* x, void* z, int64_t n, int64_t batch, void* stream) {
+    return real_epilogue(1, x, z, n, batch, 1.0f, stream);
+}
+
+int mfft_c2r_unpack(const void* u, void* out, int64_t n, int64_t batch, float scale, void* stream) {
+    return real_epilogue(2, u, out, n, batch, scale, stream);
+}
+
 int mfft_stream_copy(const void* in, void* out, int64_t bytes, void* stream) {
     g_err.clear();
     if (!in || !out) return fail(MFFT_ERR_VALUE, "in and out must not be NULL");

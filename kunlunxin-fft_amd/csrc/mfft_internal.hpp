@@ -107,6 +107,12 @@ hipError_t launch_r2c_stitch(const float2* z, float2* x, const float2* tw_real, 
 // C2R pre-twiddle: x [rows][n/2+1] -> z [rows][n/2], the inverse core's input
 hipError_t launch_c2r_pre(const float2* x, float2* z, const float2* tw_real, int64_t n,
                           int64_t rows, hipStream_t stream);
+// The standalone epilogues, roots computed in the kernel: kind 0 stitch
+// (z [rows][n/2] -> x [rows][n/2+1], times scale), 1 pre-twiddle
+// (x [rows][n/2+1] -> z [rows][n/2]), 2 unpack (u [rows][n/2] -> real
+// [rows][n], mirror order, times scale)
+hipError_t launch_real_epilogue(int kind, const void* in, void* out, int64_t n, int64_t rows, float scale,
+                                hipStream_t stream);
 
 // ---- lds_kernels.hip: single-pass LDS-resident Stockham kernel ------------
 // mode 0: c2c core; 1: r2c (core forward + fused stitch); 2: c2r (fused

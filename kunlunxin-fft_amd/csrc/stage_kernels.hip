@@ -201,6 +201,59 @@ __global__ __launch_bounds__(256) void c2r_pre_kernel(const float2* __restrict__
     if (k != 0 && k != half) zr[np - k] = c2r_pre_bin(xj, xk, tw_real[np - k]);
 }
 
+// The standalone real-flow epilogues of the reference's runner
+// (r2c_stitch, c2r_pre, c2r_unpack; src/xpu/runner.py:1687-1767), for a
+// caller that runs the half-length core itself.  One thread per output
+// value over the flattened batch; the root exp(-2 pi i k / n) comes from
+// sinpi/cospi of k / (n/2), exact in float for a power-of-two n, instead of
+// a per-plan table, so these need no plan and no allocation.
+__device__ __forceinline__ float2 real_root(int64_t k, float inv_np) {
+    float sn, cs;
+    sincospif((float)k * inv_np, &sn, &cs);  // angle pi k / np = 2 pi k / n
+    return make_float2(cs, -sn);
+}
+
+// x[row][k], k in [0, np]: the stitch of z[row][k mod np] and z[row][(np-k) mod np]
+__global__ __launch_bounds__(256) void r2c_stitch_free_kernel(const float2* __restrict__ z, float2* __restrict__ x,
+                                                              int64_t np, int64_t total, float inv_np, float scale) {
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (g >= total) return;
+    const int64_t row = g / (np + 1);
+    const int64_t k = g - row * (np + 1);
+    const float2* zr = z + row * np;
+    x[g] = r2c_bin(zr[k & (np - 1)], zr[(np - k) & (np - 1)], real_root(k, inv_np), scale, k == 0 || k == np);
+}
+
+// z[row][k], k in [0, np): the pre-twiddle of x[row][k] and x[row][np-k]
+// (imaginary parts of bins 0 and np ignored)
+__global__ __launch_bounds__(256) void c2r_pre_free_kernel(const float2* __restrict__ x, float2* __restrict__ z,
+                                                           int64_t np, int64_t total, float inv_np) {
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (g >= total) return;
+    const int64_t row = g / np;
+    const int64_t k = g - row * np;
+    const float2* xr = x + row * (np + 1);
+    float2 xk = xr[k];
+    float2 xj = xr[np - k];
+    if (k == 0) {
+        xk.y = 0.0f;
+        xj.y = 0.0f;
+    }
+    z[g] = c2r_pre_bin(xk, xj, real_root(k, inv_np));
+}
+
+// out[row][2k], out[row][2k+1] = scale * u[row][(np-k) mod np]: the forward
+// core's output read in mirror order is the unnormalised inverse transform
+// (conj(fft(conj Z))[k] = fft(Z)[(np-k) mod np]), stored as real pairs
+__global__ __launch_bounds__(256) void c2r_unpack_kernel(const float2* __restrict__ u, float2* __restrict__ out,
+                                                         int64_t np, int64_t total, float scale) {
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (g >= total) return;
+    const int64_t row = g / np;
+    const int64_t k = g - row * np;
+    out[g] = cscale(u[row * np + ((np - k) & (np - 1))], scale);
+}
+
 // Fused twiddle + transpose between the two sub-FFT stages of a composed
 // four-step (the reference's one-pass "transpose + twiddle" boundary of
 // run_hybrid, adapter_hybrid.py:294-301): for each of `batch` matrices
@@ -386,6 +439,24 @@ hipError_t launch_stream_copy(const void* src, void* dst, int64_t bytes, hipStre
     const int64_t blocks = (n16 + 2047) / 2048;
     if (!launch_fits(blocks, 256)) return hipErrorInvalidConfiguration;
     stream_copy_kernel<<<(unsigned)blocks, 256, 0, stream>>>((const nt_float4*)src, (nt_float4*)dst, n16);
+    mark(stream);
+    return hipGetLastError();
+}
+
+hipError_t launch_real_epilogue(int kind, const void* in, void* out, int64_t n, int64_t rows, float scale,
+                                hipStream_t stream) {
+    const int64_t np = n >> 1;
+    const int64_t total = rows * (kind == 0 ? np + 1 : np);
+    if (total == 0) return hipSuccess;
+    if (!launch_fits((total + 255) / 256, 256)) return hipErrorInvalidConfiguration;
+    const unsigned grid = grid_for(total, 256);
+    const float inv_np = 1.0f / (float)np;
+    if (kind == 0)
+        r2c_stitch_free_kernel<<<grid, 256, 0, stream>>>((const float2*)in, (float2*)out, np, total, inv_np, scale);
+    else if (kind == 1)
+        c2r_pre_free_kernel<<<grid, 256, 0, stream>>>((const float2*)in, (float2*)out, np, total, inv_np);
+    else
+        c2r_unpack_kernel<<<grid, 256, 0, stream>>>((const float2*)in, (float2*)out, np, total, scale);
     mark(stream);
     return hipGetLastError();
 }

@@ -40,6 +40,7 @@ EXPORTS = (
     "mfft_bit_reverse_permute", "mfft_device_props_get", "mfft_last_error",
     "mfft_abi_version", "mfft_plan_sync_overruns", "mfft_plan_create_ex", "mfft_plan_workspace_size",
     "mfft_execute_ws", "mfft_execute_noalloc", "mfft_twiddle_transpose", "mfft_stream_copy",
+    "mfft_r2c_stitch", "mfft_c2r_pre", "mfft_c2r_unpack",
 )
 PLAN_CALLER_WORKSPACE = 1
 
@@ -117,6 +118,11 @@ def load() -> ctypes.CDLL:
         lib.mfft_plan_sync_overruns.restype = i32
         lib.mfft_bit_reverse_permute.argtypes = [vp, vp, i64, i64, vp]
         lib.mfft_bit_reverse_permute.restype = i32
+        for nm in ("mfft_r2c_stitch", "mfft_c2r_unpack"):
+            getattr(lib, nm).argtypes = [vp, vp, i64, i64, ctypes.c_float, vp]
+            getattr(lib, nm).restype = i32
+        lib.mfft_c2r_pre.argtypes = [vp, vp, i64, i64, vp]
+        lib.mfft_c2r_pre.restype = i32
         lib.mfft_twiddle_transpose.argtypes = [vp, vp, i64, i64, i64, i32, vp]
         lib.mfft_twiddle_transpose.restype = i32
         lib.mfft_stream_copy.argtypes = [vp, vp, i64, vp]
@@ -265,6 +271,21 @@ def release_retired(sync=None) -> int:
     for h, _ in items:
         _lib.mfft_plan_destroy(h)
     return len(items)
+
+
+def r2c_stitch(z_ptr: int, x_ptr: int, n: int, batch: int, scale: float, stream_ptr: int) -> None:
+    check(load().mfft_r2c_stitch(ctypes.c_void_p(z_ptr), ctypes.c_void_p(x_ptr), int(n), int(batch),
+                                 float(scale), ctypes.c_void_p(stream_ptr)))
+
+
+def c2r_pre(x_ptr: int, z_ptr: int, n: int, batch: int, stream_ptr: int) -> None:
+    check(load().mfft_c2r_pre(ctypes.c_void_p(x_ptr), ctypes.c_void_p(z_ptr), int(n), int(batch),
+                              ctypes.c_void_p(stream_ptr)))
+
+
+def c2r_unpack(u_ptr: int, out_ptr: int, n: int, batch: int, scale: float, stream_ptr: int) -> None:
+    check(load().mfft_c2r_unpack(ctypes.c_void_p(u_ptr), ctypes.c_void_p(out_ptr), int(n), int(batch),
+                                 float(scale), ctypes.c_void_p(stream_ptr)))
 
 
 def bit_reverse_permute(in_ptr: int, out_ptr: int, n: int, batch: int, stream_ptr: int) -> None:

@@ -536,6 +536,131 @@ def bit_reverse_permute(x, block: int = 1024):
     return out
 
 
+# ---------------- dedicated real-flow epilogues (runner.py:1640-1834) ----------------
+# The plans fuse the R2C stitch and the C2R pre-twiddle into their kernels;
+# these runners expose the same steps on their own, for a caller that runs
+# the half-length core itself (mfft_r2c_stitch / mfft_c2r_pre /
+# mfft_c2r_unpack: one launch each, no plan, no allocation but the output).
+
+
+def _validate_real_half(x, n: int, bins: int, name: str) -> None:
+    """The epilogues' shared contract (reference runner.py:1661-1678)."""
+    if not isinstance(x, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(x).__name__}")
+    if x.dtype != torch.complex64:
+        raise TypeError(f"{name} must be complex64, got {x.dtype}")
+    if x.device.type != "cuda":
+        raise ValueError(f"{name} must be on the GPU (device='cuda'), got {x.device}")
+    if x.dim() not in (1, 2):
+        raise ValueError(f"{name} must be rank-1 or rank-2, got dim={x.dim()}")
+    if not x.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    log2_exact(n)
+    if n < 4:
+        raise ValueError(f"dedicated real flow needs N >= 4, got {n}")
+    if x.shape[-1] != bins:
+        raise ValueError(f"{name} last dim {x.shape[-1]} != expected {bins}")
+
+
+def _epilogue_block(block) -> int:
+    if not isinstance(block, int) or block <= 0 or (block & (block - 1)):
+        raise ValueError(f"block must be a positive power of two, got {block!r}")
+    return block
+
+
+def _epilogue(fn, x, out, n):
+    dev = x.device.index if x.device.index is not None else torch.cuda.current_device()
+    rows = 1 if x.dim() == 1 else int(x.shape[0])
+    with device_context(dev):
+        fn(x.data_ptr(), out.data_ptr(), n, rows, stream_handle(dev))
+    return out
+
+
+def r2c_stitch(z, n: int, scale: float = 1.0, block: int = 1024):
+    """R2C epilogue: ``z``, the unnormalised N/2-point FFT of the packed
+    pairs x[2k] + i x[2k+1] (``(N/2,)`` or ``(B, N/2)``), to the real input's
+    ``(N/2+1,)`` / ``(B, N/2+1)`` spectrum times ``scale``, with the
+    imaginary parts of bins 0 and N/2 exactly 0 (reference runner.py:1687)."""
+    _validate_real_half(z, n, n >> 1, "z")
+    scale = float(scale)
+    _epilogue_block(block)
+    out = torch.empty((*z.shape[:-1], (n >> 1) + 1), dtype=torch.complex64, device=z.device)
+    return _epilogue(lambda i, o, nn, r, st: native.r2c_stitch(i, o, nn, r, scale, st), z, out, n)
+
+
+def c2r_pre(xh, n: int, block: int = 1024):
+    """C2R prologue: the half spectrum ``(N/2+1,)`` / ``(B, N/2+1)``
+    (imaginary parts of bins 0 and N/2 ignored) to the ``(N/2,)`` /
+    ``(B, N/2)`` input of the half-length core (reference runner.py:1718)."""
+    _validate_real_half(xh, n, (n >> 1) + 1, "xh")
+    _epilogue_block(block)
+    out = torch.empty((*xh.shape[:-1], n >> 1), dtype=torch.complex64, device=xh.device)
+    return _epilogue(native.c2r_pre, xh, out, n)
+
+
+def c2r_unpack(u, n: int, scale: float = 1.0, block: int = 1024):
+    """C2R epilogue: ``u``, the unnormalised forward N/2-point FFT of
+    :func:`c2r_pre`'s output, to the real samples ``(N,)`` / ``(B, N)``
+    float32 times ``scale`` (2 x the norm's inverse scale, e.g. 2/N for
+    ``backward``); ``u`` is read in mirror order, which turns the forward
+    core into the inverse (reference runner.py:1744)."""
+    _validate_real_half(u, n, n >> 1, "u")
+    scale = float(scale)
+    _epilogue_block(block)
+    out = torch.empty((*u.shape[:-1], n), dtype=torch.float32, device=u.device)
+    return _epilogue(lambda i, o, nn, r, st: native.c2r_unpack(i, o, nn, r, scale, st), u, out, n)
+
+
+# Host references of the three epilogues (the reference's *_ref functions,
+# runner.py:1776-1834): the same formulas in torch complex arithmetic, on
+# any device, with the roots in float64.  They are what the reference's
+# host tests check the epilogues against; no execute path calls them.
+
+def _roots(n: int, count: int, sign: float, device):
+    k = torch.arange(count, dtype=torch.float64, device=device)
+    return torch.polar(torch.ones_like(k), sign * 2.0 * math.pi * k / n).to(torch.complex64)
+
+
+def r2c_stitch_ref(z, n: int, scale: float = 1.0):
+    """X[k] = A - i w^k C for k in [0, N/2], A = (Z[k] + conj Z[-k]) / 2,
+    C = (Z[k] - conj Z[-k]) / 2 (indices mod N/2), w = exp(-2 pi i / N);
+    imaginary parts of bins 0 and N/2 set to 0; times ``scale``."""
+    h = n >> 1
+    if z.shape[-1] != h:
+        raise ValueError(f"z last dim {z.shape[-1]} != N/2 ({h})")
+    k = torch.arange(h + 1, device=z.device)
+    zk, zj = z[..., k % h], z[..., (h - k) % h].conj()
+    x = 0.5 * (zk + zj) - 1j * _roots(n, h + 1, -1.0, z.device) * (0.5 * (zk - zj))
+    edge = (k == 0) | (k == h)
+    x = torch.complex(x.real, torch.where(edge, torch.zeros_like(x.imag), x.imag))
+    return x * scale
+
+
+def c2r_pre_ref(xh, n: int):
+    """Z[k] = A + i w^-k C for k in [0, N/2), A = (X[k] + conj X[N/2-k]) / 2,
+    C = (X[k] - conj X[N/2-k]) / 2, w = exp(-2 pi i / N), with the
+    imaginary parts of X[0] and X[N/2] taken as 0."""
+    h = n >> 1
+    if xh.shape[-1] != h + 1:
+        raise ValueError(f"xh last dim {xh.shape[-1]} != N/2+1 ({h + 1})")
+    x = xh.clone()
+    x[..., 0] = x[..., 0].real.to(x.dtype)
+    x[..., h] = x[..., h].real.to(x.dtype)
+    k = torch.arange(h, device=xh.device)
+    xk, xj = x[..., k], x[..., h - k].conj()
+    return 0.5 * (xk + xj) + 1j * _roots(n, h, 1.0, xh.device) * (0.5 * (xk - xj))
+
+
+def c2r_unpack_ref(u, n: int, scale: float = 1.0):
+    """out[2k] + i out[2k+1] = scale * U[(N/2 - k) mod N/2]."""
+    h = n >> 1
+    if u.shape[-1] != h:
+        raise ValueError(f"u last dim {u.shape[-1]} != N/2 ({h})")
+    k = torch.arange(h, device=u.device)
+    v = (u[..., (h - k) % h] * scale).contiguous()
+    return torch.view_as_real(v).reshape(*u.shape[:-1], n)
+
+
 def twiddle_tables(n: int, device):
     """Planar (cos, sin) float32 of exp(-2*pi*i*idx/n), idx in [0, n/2)
     (reference runner.py:93-97); computed in float64 and rounded once.

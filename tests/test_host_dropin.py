@@ -223,3 +223,53 @@ def test_device_guards_need_a_gpu():
     with pytest.raises(RuntimeError, match="GPU"):
         with device_context(torch.device("cuda:0")):
             pass
+
+
+# ---- the real-flow epilogues' host references (runner.py:1776-1834)
+
+@pytest.mark.parametrize("n", [4, 8, 64, 1024])
+@pytest.mark.parametrize("b", [1, 3])
+def test_real_epilogue_refs_against_numpy(n, b):
+    """r2c_stitch_ref of the packed pairs' FFT is numpy's rfft; c2r_pre_ref,
+    a forward FFT and c2r_unpack_ref with scale 2/N are numpy's irfft, the
+    DC and Nyquist imaginary parts ignored."""
+    rng = np.random.default_rng(3 * n + b)
+    x = rng.standard_normal((b, n))
+    z = np.fft.fft(x[:, 0::2] + 1j * x[:, 1::2], axis=-1).astype(np.complex64)
+    X = runner.r2c_stitch_ref(torch.from_numpy(z), n).numpy()
+    ref = np.fft.rfft(x, axis=-1)
+    assert np.abs(X - ref).max() <= 1e-6 * np.abs(ref).max()
+    assert np.all(X[:, 0].imag == 0) and np.all(X[:, n // 2].imag == 0)
+    h = (rng.standard_normal((b, n // 2 + 1)) + 1j * rng.standard_normal((b, n // 2 + 1))).astype(np.complex64)
+    Z = runner.c2r_pre_ref(torch.from_numpy(h), n).numpy()
+    u = np.fft.fft(Z.astype(np.complex128), axis=-1).astype(np.complex64)
+    y = runner.c2r_unpack_ref(torch.from_numpy(u), n, 2.0 / n).numpy()
+    h64 = h.astype(np.complex128)
+    h64[:, 0] = h64[:, 0].real
+    h64[:, n // 2] = h64[:, n // 2].real
+    want = np.fft.irfft(h64, n=n, axis=-1)
+    assert y.shape == (b, n) and y.dtype == np.float32
+    assert np.abs(y - want).max() <= 1e-6 * np.abs(want).max()
+
+
+def test_real_epilogue_ref_contracts():
+    """reference test_semantic_real_flow_host.py:321-330."""
+    with pytest.raises(ValueError, match="N/2"):
+        runner.r2c_stitch_ref(torch.zeros(32, dtype=torch.complex64), 128)
+    with pytest.raises(ValueError, match="N/2\\+1"):
+        runner.c2r_pre_ref(torch.zeros(64, dtype=torch.complex64), 128)
+    with pytest.raises(ValueError, match="N/2"):
+        runner.c2r_unpack_ref(torch.zeros(63, dtype=torch.complex64), 128)
+
+
+def test_real_epilogues_check_before_the_gpu():
+    """The runners' contract (reference runner.py:1661-1684) raises before
+    anything needs a GPU: a CPU tensor is a ValueError, a wrong dtype a
+    TypeError."""
+    z = torch.zeros(32, dtype=torch.complex64)
+    with pytest.raises(ValueError, match="GPU"):
+        runner.r2c_stitch(z, 64)
+    with pytest.raises(TypeError, match="complex64"):
+        runner.c2r_pre(torch.zeros(33), 64)
+    with pytest.raises(TypeError, match="torch.Tensor"):
+        runner.c2r_unpack([0j] * 32, 64)
