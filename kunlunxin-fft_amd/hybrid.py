@@ -17,7 +17,8 @@ registry, config/external_cores.json):
   materialized external sub-transform.  Steps 1 and 5 are torch copies, as in
   the reference; step 3 is this library's ``mfft_twiddle_transpose`` kernel.
 * ``"local"``: this library's own four-step (one native plan, both passes
-  fused with the twiddle and the transposes), n1 = t2.
+  fused with the twiddle and the transposes), n1 = t2.  The reference's
+  name for its in-library core, ``"triton"``, selects it too.
 
 A composition only ever runs when a composition table promotes it for an
 exact shape (``composition.composition_select``), or when a caller builds a
@@ -44,14 +45,18 @@ class HybridPlan:
     stage2_len: int = field(init=False)
 
     def __post_init__(self):
+        # the reference's order of checks and key phrases (adapter_hybrid.py:82-90)
         if self.direction != "dit":
-            raise ValueError("the composition covers the DIT decomposition only")
-        if self.n <= 0 or (self.n & (self.n - 1)) or self.tile <= 0 or (self.tile & (self.tile - 1)):
-            raise ValueError("N and tile must be powers of two")
-        if self.n % self.tile:
+            raise ValueError("the composition covers DIT only (the DIT decomposition)")
+        if self.tile <= 0 or self.n % self.tile:
             raise ValueError(f"tile {self.tile} must divide N={self.n}")
+        if self.n <= 0 or (self.n & (self.n - 1)) or (self.tile & (self.tile - 1)):
+            raise ValueError("N and tile must be powers of two")
+        # the reference's in-library core is its Triton one; here it is this library's own
+        if self.core == "triton":
+            self.core = "local"
         if self.core not in CORES:
-            raise ValueError(f"unknown core {self.core!r}; known: {CORES}")
+            raise ValueError(f"unknown core {self.core!r}; known: {CORES} (and 'triton', an alias of 'local')")
         if self.transform_direction not in ("forward", "inverse"):
             raise ValueError(f"bad transform_direction {self.transform_direction!r}")
         self.stage2_len = self.n // self.tile

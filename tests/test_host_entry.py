@@ -362,15 +362,22 @@ def test_external_core_registry_and_composition_contract():
 
 
 def test_hybrid_plan_contract():
-    from kunlunxin_fft_amd.hybrid import plan_hybrid
+    from kunlunxin_fft_amd.hybrid import HybridPlan, plan_hybrid
 
     p = plan_hybrid(2048, 16, tile=64)
     assert p.stage2_len == 32 and p.core == "vendor"
-    with pytest.raises(ValueError):
+    # the reference's checks and key phrases (test_adapter_hybrid.py:19-30)
+    with pytest.raises(ValueError, match="must divide"):
         plan_hybrid(2048, 1, tile=48)
-    with pytest.raises(ValueError):
+    with pytest.raises(ValueError, match="powers of two"):
+        plan_hybrid(960, 16, tile=64)  # divides, but N is not a power of two
+    with pytest.raises(ValueError, match="must divide"):
         plan_hybrid(2048, 1, tile=4096)
-    with pytest.raises(ValueError):
-        plan_hybrid(2048, 1, tile=64, core="triton")
+    with pytest.raises(ValueError, match="DIT only"):
+        HybridPlan(n=1024, batch=16, tile=64, direction="dif")
+    with pytest.raises(ValueError, match="unknown core"):
+        plan_hybrid(1024, 16, tile=64, core="external")
+    # the reference's in-library core name selects this library's own core
+    assert plan_hybrid(2048, 1, tile=64, core="triton").core == "local"
     with pytest.raises(ValueError):
         plan_hybrid(1 << 12, 1, tile=8, core="local")  # the local core needs tile >= 16
