@@ -169,7 +169,7 @@ def fallback_binding_violations(table: dict) -> list[str]:
             continue
         missing = [k for k in FALLBACK_BINDING_KEYS if prov.get(k) in (None, "")]
         if missing:
-            out.append(f"previous_fallbacks[{i}] {key}: provenance missing {', '.join(missing)}")
+            out.append(f"previous_fallbacks[{i}] {key}: provenance missing binding key(s) {', '.join(missing)}")
             continue
         if prov["carry_contract"] != FALLBACK_CARRY_CONTRACT:
             out.append(f"previous_fallbacks[{i}] {key}: carry_contract {prov['carry_contract']!r}")

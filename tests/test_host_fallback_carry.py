@@ -157,3 +157,30 @@ def test_fallback_cells_missing_from_the_rebuild_are_dropped():
 @pytest.mark.parametrize("prev", [None, {}])
 def test_no_previous_table(prev):
     assert carry_previous_fallbacks(prev, None, table([]), Timer({}), guard=2.0) == ([], [], [])
+
+
+@pytest.mark.parametrize("mutate,phrase", [
+    (lambda p: p.update(source_env_hash="f" * 16), "source env"),
+    (lambda p: p.update(source_profile_hash="f" * 16), "source profile"),
+    (lambda p: p.update(source_precision="bf16"), "source precision"),
+    (lambda p: p.update(source_device={"device_model": "gfx942", "multiprocessor_count": 304,
+                                       "max_shared_mem": 65536}), "source device"),
+    (lambda p: p.pop("source_result_sha256"), "missing binding key"),
+    (lambda p: p.update(carry_contract="fallback-env-binding-v0"), "carry_contract"),
+    (None, "provenance"),
+])
+def test_load_table_refuses_unbound_fallback_cells(tmp_path, mutate, phrase):
+    """The loader's binding contract, with the reference's key phrases
+    (test_selector.py:645-701)."""
+    prev = table([lds_entry(1024, 64, 16)])
+    new = table([lds_entry(1024, 64, 32)])
+    fbs, _, _ = carry_previous_fallbacks(prev, "ab" * 32, new, Timer({16: 0.1, 32: 0.2}), guard=2.0)
+    if mutate is None:
+        fbs[0].pop("previous_fallback_provenance")
+    else:
+        mutate(fbs[0]["previous_fallback_provenance"])
+    new["previous_fallbacks"] = fbs
+    path = tmp_path / "t.json"
+    path.write_text(json.dumps(new))
+    with pytest.raises(pkg.ConfigError, match=phrase):
+        pkg.load_table(str(path))
