@@ -34,7 +34,7 @@ Also reported:
   cyclic order, after the timed steps as warm-up), and each launch's median
   duration over 20 timed executes;
 * ``latency_n2048_b1``: the reference protocol (warmup 5, 5 x 32 trials,
-  device sync per trial, pooled p50, scripts/issue10_wp3_holdout.py:176-190)
+  device sync per trial, pooled p50 and MAD, scripts/issue10_wp3_holdout.py:176-190)
   for execute_fft_plan, plus the kernel-only event p50 and the per-transform
   time of 64 executes recorded into one HIP graph and replayed;
 * ``config2``: latency and GB/s of the reference's small-batch configuration (N in {1024, 2048}, B in
@@ -148,7 +148,9 @@ def compact_line(full: dict, detail: "str | None" = None) -> dict:
                                      "higher_is_better", "scaling", "vs_baseline", "dtype", "data")}
     cfg = full.get("config") or {}
     line["config"] = {k: cfg.get(k) for k in ("workload", "frac_hbm_of_value", "stream_copy_gbps",
-                                              "frac_of_stream_copy", "d2d_copy_gbps", "runner_forced")}
+                                              "frac_of_stream_copy", "d2d_copy_gbps")}
+    if cfg.get("runner_forced"):
+        line["config"]["runner_forced"] = cfg["runner_forced"]
     r = full.get("roofline")
     if r:
         line["roofline"] = {k: r.get(k) for k in (
@@ -168,8 +170,8 @@ def compact_line(full: dict, detail: "str | None" = None) -> dict:
         line["cpu_baseline"] = None
     lat = full.get("latency_n2048_b1")
     line["latency_n2048_b1"] = ({k: lat.get(k) for k in (
-        "executed", "api_wall_p50_ms", "kernel_event_p50_ms", "graph_replay_us_per_transform",
-        "reference_p800_api_p50_ms", "api_p50_speedup_vs_reference_p800")} if lat else None)
+        "executed", "api_wall_p50_ms", "api_wall_mad_ms", "trials", "kernel_event_p50_ms",
+        "graph_replay_us_per_transform", "api_p50_speedup_vs_reference_p800")} if lat else None)
     line["per_size"] = [[p["n"], p["gbps"], p["frac_hbm"]] for p in full.get("per_size") or []]
     real = {}
     for p in full.get("real_per_size") or []:
@@ -199,6 +201,16 @@ def compact_line(full: dict, detail: "str | None" = None) -> dict:
             break
         line[key] = "in detail record"
     return line
+
+
+def p50_mad(xs):
+    """Pooled p50 and median absolute deviation of trial times, both as the
+    upper median (the element at len // 2 of the sorted list), the
+    reference holdout's convention (scripts/issue10_wp3_holdout.py:510-520)."""
+    ys = sorted(xs)
+    p50 = ys[len(ys) // 2]
+    dev = sorted(abs(v - p50) for v in ys)
+    return p50, dev[len(dev) // 2]
 
 
 def batch_for(n: int) -> int:
@@ -490,10 +502,10 @@ def main() -> int:
             evs.append((s, e))
         torch.cuda.synchronize()
         ev = statistics.median(s.elapsed_time(e) for s, e in evs)
-        p50 = statistics.median(wall)
+        p50, mad = p50_mad(wall)
         return {"n": n, "batch": b, "transform": f"{ttype} {plan.transform_direction}",
-                "executed": plan.executed, "api_wall_p50_ms": round(p50, 5),
-                "kernel_event_p50_ms": round(ev, 5),
+                "executed": plan.executed, "api_wall_p50_ms": round(p50, 5), "api_wall_mad_ms": round(mad, 5),
+                "trials": len(wall), "kernel_event_p50_ms": round(ev, 5),
                 "api_gbps": round(nbytes / (p50 * 1e-3) / 1e9, 3),
                 "kernel_gbps": round(nbytes / (ev * 1e-3) / 1e9, 1)}
 

@@ -43,7 +43,8 @@ def _full_record(bench):
                          "flow": "four-step", "launches": 2, "ms": 0.11378, "gbps": 2359.2, "frac_hbm": 0.2949,
                          "split": [512, 128, 256]})
     lat = {"n": 2048, "batch": 1, "transform": "c2c forward", "executed": "fft_lds_fused",
-           "api_wall_p50_ms": 0.04123, "kernel_event_p50_ms": 0.00612, "api_gbps": 0.795, "kernel_gbps": 5.4,
+           "api_wall_p50_ms": 0.04123, "api_wall_mad_ms": 0.00071, "trials": 160, "kernel_event_p50_ms": 0.00612,
+           "api_gbps": 0.795, "kernel_gbps": 5.4,
            "graph_replay_us_per_transform": 2.123, "reference_p800_api_p50_ms": 0.4036,
            "api_p50_speedup_vs_reference_p800": 9.8}
     cfg = lambda n, b, t="c2c forward": dict(lat, n=n, batch=b, transform=t)  # noqa: E731
@@ -135,6 +136,12 @@ def test_compact_line_of_a_partial_run():
     assert line["cpu_baseline"] is None and line["config5"] is None and line["real_per_size"] == []
 
 
+def test_p50_mad_upper_median_convention():
+    bench = _bench_module()
+    assert bench.p50_mad([1.0, 2.0, 3.0, 10.0]) == (3.0, 2.0)  # p50 = ys[2]; |dev| sorted 0,1,2,7 -> 2
+    assert bench.p50_mad([5.0]) == (5.0, 0.0)
+
+
 def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, BENCH, "--gpus", "2"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 2
@@ -171,7 +178,8 @@ def test_bench_json_line(gpu, tmp_path):
     assert line["config"]["stream_copy_gbps"] == rf["copy_ceiling_gbps"]
     cpu = line["cpu_baseline"]
     assert cpu["value"] > 0 and cpu["cores"] == 1 and cpu["kind"] in ("reference", "port")
-    assert line["latency_n2048_b1"]["api_wall_p50_ms"] > 0
+    assert line["latency_n2048_b1"]["api_wall_p50_ms"] > 0 and line["latency_n2048_b1"]["trials"] == 160
+    assert line["latency_n2048_b1"]["api_wall_mad_ms"] >= 0
     assert len(line["per_size"]) == 11 and len(line["real_per_size"]) == 11
     assert line["config5"]["cells"] == 44
     assert line["provenance"]["profile_hash"] and line["provenance"]["csrc_sha16"]
