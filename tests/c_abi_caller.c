@@ -7,7 +7,10 @@
  * 2. c2c inverse, ortho norm, the radix-2 stage flow, with a plan created
  *    with MFFT_PLAN_CALLER_WORKSPACE and executed through mfft_execute_ws
  *    on a stream of its own (mfft_execute must refuse that plan);
- * 3. r2c forward then c2r inverse (automatic flows), a round trip.
+ * 3. r2c forward then c2r inverse (automatic flows), a round trip;
+ * 4. the same two transforms by hand around an N/2-point c2c plan: the
+ *    packed reals through the core and mfft_r2c_stitch, then mfft_c2r_pre,
+ *    the core again and mfft_c2r_unpack with scale 2/N.
  * Each result is compared with a direct O(n^2) DFT in double precision
  * (relative L2 error, the library's 1e-5 gate).  Exit status 0 = all pass.
  */
@@ -171,6 +174,54 @@ int main(void) {
     fails += !(e <= TOL);
     mfft_ok(mfft_plan_destroy(pr), "destroy");
     mfft_ok(mfft_plan_destroy(pc), "destroy");
+
+    /* 4. the standalone real epilogues around an N/2-point c2c core (d_ref
+     * still holds the DFT of the real rows) */
+    void *dz = NULL, *dbins = NULL, *du = NULL;
+    hip_ok(hipMalloc(&dz, (size_t)B * (N / 2) * 8), "hipMalloc z");
+    hip_ok(hipMalloc(&dbins, (size_t)B * (N / 2 + 1) * 8), "hipMalloc bins");
+    hip_ok(hipMalloc(&du, (size_t)B * (N / 2) * 8), "hipMalloc u");
+    mfft_plan* ph = NULL;
+    mfft_ok(mfft_plan_create(&ph, N / 2, B, MFFT_C2C, MFFT_FORWARD, MFFT_NORM_NONE, MFFT_FLOW_AUTO, NULL, 0),
+            "plan half core");
+    mfft_ok(mfft_execute(ph, dreal, dz, NULL), "core of the packed reals");
+    mfft_ok(mfft_r2c_stitch(dz, dbins, N, B, 1.0f, NULL), "r2c stitch");
+    hip_ok(hipDeviceSynchronize(), "sync");
+    hip_ok(hipMemcpy(h_out, dbins, (size_t)B * (N / 2 + 1) * 8, hipMemcpyDeviceToHost), "copy stitched bins");
+    num = den = 0.0;
+    for (int r = 0; r < B; ++r)
+        for (int k = 0; k <= N / 2; ++k)
+            for (int c = 0; c < 2; ++c) {
+                const double ref = d_ref[2 * ((size_t)r * N + k) + c];
+                const double d = h_out[2 * ((size_t)r * (N / 2 + 1) + k) + c] - ref;
+                num += d * d;
+                den += ref * ref;
+            }
+    e = sqrt(num / den);
+    printf("core + mfft_r2c_stitch: rel L2 %.3e\n", e);
+    fails += !(e <= TOL);
+    mfft_ok(mfft_c2r_pre(dbins, dz, N, B, NULL), "c2r pre");
+    mfft_ok(mfft_execute(ph, dz, du, NULL), "core of the pre-twiddled bins");
+    mfft_ok(mfft_c2r_unpack(du, din, N, B, 2.0f / N, NULL), "c2r unpack");  /* din: B x N reals */
+    hip_ok(hipDeviceSynchronize(), "sync");
+    hip_ok(hipMemcpy(h_back, din, (size_t)N * B * 4, hipMemcpyDeviceToHost), "copy unpacked");
+    num = den = 0.0;
+    for (size_t i = 0; i < (size_t)N * B; ++i) {
+        const double d = (double)h_back[i] - h_real[i];
+        num += d * d;
+        den += (double)h_real[i] * h_real[i];
+    }
+    e = sqrt(num / den);
+    printf("mfft_c2r_pre + core + mfft_c2r_unpack round trip: rel L2 %.3e\n", e);
+    fails += !(e <= TOL);
+    if (mfft_r2c_stitch(dz, dz, N, B, 1.0f, NULL) != MFFT_ERR_VALUE) {
+        printf("mfft_r2c_stitch accepted overlapping buffers\n");
+        fails++;
+    }
+    mfft_ok(mfft_plan_destroy(ph), "destroy");
+    hipFree(dz);
+    hipFree(dbins);
+    hipFree(du);
 
     hipFree(din);
     hipFree(dout);

@@ -20,5 +20,5 @@ def test_plain_c_caller(gpu):
     print(res.stdout)
     assert res.returncode == 0, f"rc={res.returncode}\n{res.stdout}\n{res.stderr}"
     assert res.stdout.strip().endswith("OK")
-    assert res.stdout.count("rel L2") == 4
+    assert res.stdout.count("rel L2") == 6
 
