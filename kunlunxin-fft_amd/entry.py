@@ -327,7 +327,7 @@ def execute_fft_plan(plan: ExecutionPlan, x):
     raise the reference's errors.
     """
     hit = _FAST.get(id(plan))
-    if hit is not None and _ledger._active is None and hit[0]() is plan and type(x) is _fast_mods[0].Tensor:
+    if hit is not None and _ledger.ACTIVE.get() is None and hit[0]() is plan and type(x) is _fast_mods[0].Tensor:
         if x.get_device() == hit[1] and x.dtype is hit[2] and x.shape == hit[3] and x.is_contiguous():
             torch, launch = _fast_mods
             return launch(hit[4], x, torch.empty(hit[5], dtype=hit[6], device=x.device))
