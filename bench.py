@@ -107,7 +107,8 @@ def provenance(pkg, profile_hash: str) -> dict:
     """What a row is tied to: the device profile and live environment hashes,
     the selector and composition tables the plans came from (file sha256 and
     the table's own bindings), the kernel sources and the built library, and
-    the commit when a git checkout is present."""
+    the commit when a git checkout is present, else the one the library's
+    build recorded."""
     import glob
     import subprocess
 
@@ -128,13 +129,23 @@ def provenance(pkg, profile_hash: str) -> dict:
         commit = r.stdout.strip() or None if r.returncode == 0 else None
     except (OSError, subprocess.SubprocessError):
         commit = None
+    try:
+        with open(os.path.join(pdir, "libmfft.build.json")) as f:
+            built = json.load(f)
+    except (OSError, ValueError):
+        built = {}
+    csrc = _sha16_files(sorted(glob.glob(os.path.join(pdir, "csrc", "*"))))
     return {"profile_hash": profile_hash, "env_hash": envcheck.current_env_hash(),
             "table_sha16": _sha16_files([sel]),
             "table_profile_hash": tab.get("profile_hash"), "table_env_hash": tab.get("env_hash"),
             "composition_sha16": _sha16_files([os.path.join(CONFIG_DIR, "composition_table.json")]),
-            "csrc_sha16": _sha16_files(sorted(glob.glob(os.path.join(pdir, "csrc", "*")))),
+            "csrc_sha16": csrc,
             "lib_sha16": _sha16_files([os.path.join(pdir, "libmfft.so")]),
-            "commit": commit}
+            "commit": commit,
+            # the library's own build record: the commit it was built at (this
+            # run may have no git metadata) and whether its sources are these
+            "build_commit": built.get("commit"), "build_dirty": built.get("dirty"),
+            "build_matches_csrc": (built.get("csrc_sha16") == csrc) if built else None}
 
 
 def compact_line(full: dict, detail: "str | None" = None) -> dict:

@@ -63,7 +63,8 @@ def _full_record(bench):
         "provenance": {"profile_hash": "0123456789abcdef", "env_hash": "fedcba9876543210",
                        "table_sha16": "0" * 16, "table_profile_hash": "0123456789abcdef",
                        "table_env_hash": "fedcba9876543210", "composition_sha16": "1" * 16,
-                       "csrc_sha16": "2" * 16, "lib_sha16": "3" * 16, "commit": "abcdef012345"},
+                       "csrc_sha16": "2" * 16, "lib_sha16": "3" * 16, "commit": "abcdef012345",
+                       "build_commit": "abcdef012345", "build_dirty": False, "build_matches_csrc": True},
         "roofline": {"bound": "hbm", "achieved": 2810.4, "peak": 8000.0, "unit": "GB/s", "frac": 0.3513,
                      "traffic": 2149580800, "traffic_over_algorithmic": 2.001,
                      "kernel": "fourstep_pass_kernel pass 1 (n1=1024) + fourstep_pass_kernel pass 2 (n2=1024) "
@@ -110,6 +111,7 @@ def test_compact_line_fits_the_driver_tail():
     assert len(line["config3"]) == 12 and len(line["config4"]) == 2
     assert line["config5"]["cells"] == 44 and line["config5"]["clears_guard"] == 44
     assert line["provenance"]["env_hash"] == "fedcba9876543210"
+    assert line["provenance"]["build_matches_csrc"] is True and line["config3"] != "in detail record"
     assert line["detail"] == "gpurun_out/bench_detail.json"
 
 
@@ -183,5 +185,7 @@ def test_bench_json_line(gpu, tmp_path):
     assert len(line["per_size"]) == 11 and len(line["real_per_size"]) == 11
     assert line["config5"]["cells"] == 44
     assert line["provenance"]["profile_hash"] and line["provenance"]["csrc_sha16"]
+    # the library was built from the sources in this tree
+    assert line["provenance"]["build_matches_csrc"] is True and line["provenance"]["build_commit"]
     full = json.loads(detail.read_text())
     assert len(full["config5"]) == 44 and all("launch_ms" in p for p in full["per_size"])
