@@ -90,3 +90,35 @@ def test_composition_plan_executes_its_core(gpu, core):
     x = seeded(n, b, 63)
     y = execute_fft_plan(plan, torch.from_numpy(x).to(gpu)).cpu().numpy()
     check(y, oracle.fft_dit(x), f"composition plan {core}")
+
+
+@pytest.mark.parametrize("core,n,b,tile", [("vendor", 1024, 16, 64), ("vendor", 1 << 16, 2, 256),
+                                           ("local", 1024, 16, 64), ("local", 1 << 16, 2, 256)])
+def test_profile_hybrid_matches_run_hybrid(gpu, core, n, b, tile):
+    """profile_hybrid gives run_hybrid's bits and times every phase
+    (reference tests/test_adapter_hybrid.py:141-164)."""
+    from kunlunxin_fft_amd.hybrid import profile_hybrid
+
+    x = torch.from_numpy(seeded(n, b, 7)).to(gpu)
+    plan = plan_hybrid(n, b, tile, core)
+    y1 = run_hybrid(x, plan)
+    y2, phases = profile_hybrid(x, plan)
+    assert torch.equal(y1, y2)
+    check(y2.cpu().numpy(), oracle.fft_dit(x.cpu().numpy()) if n <= 4096 else
+          np.fft.fft(x.cpu().numpy().astype(np.complex128)), f"profile_hybrid {core} N={n}")
+    assert phases["core"] == core and phases["hidden_copies"] == []
+    if core == "vendor":
+        for key in ("gather_ms", "stage1_core_ms", "twiddle_transpose_ms", "stage2_core_ms", "scatter_ms"):
+            assert phases[key] >= 0.0, key
+        assert phases["stage2_in_contiguous"] is True and phases["stage1_out_contiguous"] is True
+    else:
+        assert phases["fused_four_step_ms"] > 0.0
+
+
+def test_time_cell_summarises_every_trial(gpu):
+    from kunlunxin_fft_amd.hybrid import time_cell
+
+    x = torch.from_numpy(seeded(4096, 8, 3)).to(gpu)
+    plan = plan_hybrid(4096, 8, 64, "local")
+    first_ms, stats = time_cell(lambda t: run_hybrid(t, plan), x, warmup=3, trials=11)
+    assert first_ms > 0 and stats["n"] == 11 and 0 < stats["p50"] <= stats["max"]
