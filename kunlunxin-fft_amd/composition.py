@@ -23,12 +23,53 @@ TABLE_PATH = os.path.join(CONFIG_DIR, "composition_table.json")
 KIND = "composition-promotion"
 TABLE_REQUIRED_KEYS = ("kind", "profile_hash", "env_hash", "precision", "guard_pct", "entries")
 ENTRY_REQUIRED_KEYS = ("N", "batch", "direction", "flow_id", "flow_realization",
-                       "processing_unit", "candidate_ms", "incumbent_ms", "guard_pct", "reason", "tile", "core")
+                       "processing_unit", "candidate_ms", "incumbent_ms", "guard_pct", "reason", "tile", "core",
+                       "evidence")
+# what the builder measured for the entry: the plan it beat, every candidate's
+# time, and the winner's relative L2 distance from the plan's output
+EVIDENCE_REQUIRED_KEYS = ("incumbent", "candidates", "err_rel_l2")
+MAX_ERR_REL_L2 = 1e-5
 
 
 def guard_pct_of(candidate_ms: float, incumbent_ms: float) -> float:
     """Percent by which the candidate beats the incumbent (positive = faster)."""
     return (incumbent_ms - candidate_ms) / incumbent_ms * 100.0
+
+
+def composition_entry_violations(entry: dict, table: dict) -> list[str]:
+    """Contract violations of one composition entry (reference
+    composition.py:64-114, on this library's entry fields): every required
+    key; the DIT decomposition; a positive integer N and batch; a known
+    core; a power-of-two tile of at least 16 dividing N; the stamped guard
+    equal to the one its two medians give, and at least the table's; and
+    the evidence, whose error is within the parity bound."""
+    bad = [f"missing {k!r}" for k in ENTRY_REQUIRED_KEYS if entry.get(k) in (None, "")]
+    if bad:
+        return bad
+    n, b, tile = entry["N"], entry["batch"], entry["tile"]
+    if entry["direction"] != "dit":
+        bad.append(f"direction {entry['direction']!r} (the composition is DIT only)")
+    if not isinstance(n, int) or n <= 0:
+        bad.append(f"N {n!r} not a positive int (exact keys only)")
+    if not isinstance(b, int) or b <= 0:
+        bad.append(f"batch {b!r} not a positive int")
+    if entry["core"] not in ("vendor", "local", "triton"):
+        bad.append(f"unknown core {entry['core']!r}")
+    if not isinstance(tile, int) or tile < 16 or tile & (tile - 1) or (isinstance(n, int) and n % tile):
+        bad.append(f"tile {tile!r} invalid (a power of two >= 16 dividing N)")
+    g = guard_pct_of(float(entry["candidate_ms"]), float(entry["incumbent_ms"]))
+    if abs(g - float(entry["guard_pct"])) > 1e-6:
+        bad.append(f"guard_pct {entry['guard_pct']!r} != {g:.6f} recomputed from its medians")
+    if g < float(table.get("guard_pct", 2.0)):
+        bad.append(f"guard {g:.3f}% below {table.get('guard_pct')}%")
+    ev = entry["evidence"]
+    if not isinstance(ev, dict):
+        return bad + ["evidence not an object"]
+    bad += [f"evidence missing {k!r}" for k in EVIDENCE_REQUIRED_KEYS if ev.get(k) in (None, "")]
+    err = ev.get("err_rel_l2")
+    if isinstance(err, (int, float)) and not err <= MAX_ERR_REL_L2:
+        bad.append(f"evidence err_rel_l2 {err} > {MAX_ERR_REL_L2} (parity gate)")
+    return bad
 
 
 def table_violations(table: dict) -> list[str]:
@@ -41,21 +82,14 @@ def table_violations(table: dict) -> list[str]:
         return bad + ["entries not a list"]
     seen = set()
     for i, e in enumerate(table["entries"]):
-        miss = [k for k in ENTRY_REQUIRED_KEYS if e.get(k) in (None, "")]
-        if miss:
-            bad.append(f"entry {i}: missing {miss}")
+        if not isinstance(e, dict):
+            bad.append(f"entry {i} not an object")
             continue
-        key = (e["N"], e["batch"], e["direction"])
+        key = (e.get("N"), e.get("batch"), e.get("direction"))
         if key in seen:
             bad.append(f"duplicate exact-shape key {key}")
         seen.add(key)
-        if e["core"] not in ("vendor", "local"):
-            bad.append(f"entry {key}: unknown core {e['core']!r}")
-        g = guard_pct_of(float(e["candidate_ms"]), float(e["incumbent_ms"]))
-        if abs(g - float(e["guard_pct"])) > 1e-6:
-            bad.append(f"entry {key}: guard_pct does not match its medians")
-        if g < float(table["guard_pct"]):
-            bad.append(f"entry {key}: guard {g:.3f}% below {table['guard_pct']}%")
+        bad.extend(f"entry {key}: {msg}" for msg in composition_entry_violations(e, table))
     return bad
 
 
@@ -77,6 +111,7 @@ def load_composition_table(path: str = TABLE_PATH):
 
 
 CORES_PATH = os.path.join(CONFIG_DIR, "external_cores.json")
+EXTERNAL_CORES_PATH = CORES_PATH  # the reference's name
 CLASSIFICATIONS = ("local-core", "materialized-external-subtransform", "full-transform-only", "boundary",
                    "reference-only", "unavailable")
 CORE_REQUIRED_KEYS = ("id", "source", "api", "classification", "device_resident", "selector_status")

@@ -131,20 +131,22 @@ def main() -> int:
             ms = timed(lambda: run_hybrid(x, hp), 8 * n * b)
             row["candidates"][f"{core}@{tile}"] = round(ms, 5)
             if best is None or ms < best[0]:
-                best = (ms, core, tile)
+                best = (ms, core, tile, err)
         measurements.append(row)
         gain = composition.guard_pct_of(best[0], inc_ms) if best else -100.0
         print(f"N={n:>6} B={b:>4} incumbent {plan.executed} {inc_ms * 1e3:8.2f} us, best composition "
               f"{best[1]}@{best[2]} {best[0] * 1e3:8.2f} us ({gain:+.1f}%)", flush=True)
         if best is not None and gain >= GUARD_PCT:
-            ms, core, tile = best
+            ms, core, tile, err = best
             entries.append({
                 "N": n, "batch": b, "direction": "dit", "tile": tile, "core": core,
                 "flow_id": f"composition-{cores[core]['id']}", "flow_realization": "four-step-composition",
                 "processing_unit": cores[core]["id"], "candidate_ms": ms, "incumbent_ms": inc_ms,
                 "guard_pct": composition.guard_pct_of(ms, inc_ms),
                 "reason": f"{core}-core four-step at tile {tile} beats {plan.executed} by {gain:.1f}% "
-                          f"(>= {GUARD_PCT}%)"})
+                          f"(>= {GUARD_PCT}%)",
+                "evidence": {"incumbent": plan.executed, "candidates": dict(row["candidates"]),
+                             "err_rel_l2": err}})
         del x, ref
     table = {"kind": composition.KIND, "profile_hash": prof, "env_hash": env_hash, "precision": "fp32",
              "guard_pct": GUARD_PCT, "entries": entries,

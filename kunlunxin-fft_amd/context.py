@@ -42,7 +42,22 @@ def xpu_context(device: int = 0):
         yield index
 
 
-def device_name(index: int = 0) -> str:
+def current_device_index() -> int:
+    """Index of the current torch GPU (reference context.py:38-40)."""
     import torch
 
-    return torch.cuda.get_device_name(index)
+    return torch.cuda.current_device()
+
+
+def device_name(index: int = 0) -> str:
+    """Human-readable device string (reference runner.py:70-91): the
+    device name with its architecture, CU count and LDS per CU; ``"cpu"``
+    without a GPU."""
+    if not device_ready():
+        return "cpu"
+    import torch
+
+    p = torch.cuda.get_device_properties(index)
+    arch = getattr(p, "gcnArchName", "").split(":")[0] or "unknown"
+    lds = getattr(p, "shared_memory_per_multiprocessor", 0) or getattr(p, "max_shared_memory_per_multiprocessor", 0)
+    return f"{p.name} ({arch}, {p.multi_processor_count} CUs, {lds // 1024} KiB LDS per CU)"

@@ -44,7 +44,9 @@ from collections import OrderedDict
 import torch
 
 from . import native
-from .context import device_context, device_name, device_ready, xpu_context  # noqa: F401  (re-exported)
+from .context import (  # noqa: F401  (re-exported)
+    current_device_index, device_context, device_name, device_ready, xpu_context,
+)
 from .validate import log2_exact, validate_batch_input, validate_input, validate_tensor, validate_twiddle
 
 from .flows import DEFAULT_STAGE_BLOCK, RUNNER_FLOWS, flow_params  # noqa: F401  (re-exported)

@@ -232,3 +232,9 @@ def test_xpu_context_guard(gpu):
     with runner.xpu_context(0) as idx:
         assert idx == 0 and torch.cuda.current_device() == 0
     assert torch.cuda.current_device() == prev
+
+
+def test_device_name_and_index(gpu):
+    name = runner.device_name()
+    assert "gfx950" in name and "CUs" in name, name
+    assert runner.current_device_index() == torch.cuda.current_device()

@@ -343,10 +343,23 @@ def test_external_core_registry_and_composition_contract():
         composition.load_external_cores(f.name)
     entry = {"N": 2048, "batch": 16, "direction": "dit", "tile": 64, "core": "vendor", "flow_id": "c",
              "flow_realization": "four-step-composition", "processing_unit": "rocfft_torch_fft",
-             "candidate_ms": 0.01, "incumbent_ms": 0.02, "guard_pct": 50.0, "reason": "test"}
+             "candidate_ms": 0.01, "incumbent_ms": 0.02, "guard_pct": 50.0, "reason": "test",
+             "evidence": {"incumbent": "fft_lds_fused_batch", "candidates": {"vendor@64": 0.01},
+                          "err_rel_l2": 3e-7}}
     table = {"kind": composition.KIND, "profile_hash": PROF, "env_hash": ENV, "precision": "fp32",
              "guard_pct": 2.0, "entries": [entry]}
     assert composition.table_violations(table) == []
+    # one entry's contract, rule by rule (the reference's composition_entry_violations)
+    viol = lambda **kw: composition.composition_entry_violations(dict(entry, **kw), table)  # noqa: E731
+    assert viol() == []
+    assert any("DIT only" in v for v in viol(direction="dif"))
+    assert any("positive int" in v for v in viol(N=2048.0)) and any("positive int" in v for v in viol(batch=0))
+    assert any("unknown core" in v for v in viol(core="cufft"))
+    assert any("tile" in v for v in viol(tile=48)) and any("tile" in v for v in viol(tile=8))
+    assert any("recomputed" in v for v in viol(guard_pct=49.0))
+    assert any("err_rel_l2" in v for v in viol(evidence=dict(entry["evidence"], err_rel_l2=2e-5)))
+    assert any("evidence missing" in v for v in viol(evidence={"incumbent": "x"}))
+    assert viol(core="triton") == []  # the reference's name for the library's own core
     assert any("missing" in v for v in composition.table_violations(
         dict(table, entries=[{k: v for k, v in entry.items() if k != "core"}])))
     assert any("guard" in v for v in composition.table_violations(
@@ -381,3 +394,30 @@ def test_hybrid_plan_contract():
     assert plan_hybrid(2048, 1, tile=64, core="triton").core == "local"
     with pytest.raises(ValueError):
         plan_hybrid(1 << 12, 1, tile=8, core="local")  # the local core needs tile >= 16
+
+
+def test_semantic_specs_and_families():
+    """The reference's semantic helpers (semantic.py:36-125): labels map to
+    the selector's exact keys, families are the shared cores plus a real
+    type's own flow, and the taxonomy self-check is clean."""
+    from kunlunxin_fft_amd import semantic
+
+    assert semantic.spec("c2r").key == ("c2r", "inverse", "backward")
+    assert semantic.spec("c2c-inverse").transform_direction == "inverse"
+    with pytest.raises(KeyError, match="unknown semantic label"):
+        semantic.spec("c2c-sideways")
+    assert semantic.family("c2c") == semantic.CORE_FLOWS
+    assert semantic.family("r2c") - semantic.CORE_FLOWS == {"dedicated-r2c-pack-v1"}
+    assert semantic.family_allows("c2r", "dedicated-c2r-hermitian-v1")
+    assert not semantic.family_allows("r2c", "dedicated-c2r-hermitian-v1")
+    assert semantic.family_size("r2c") == len(semantic.CORE_FLOWS) + 1
+    with pytest.raises(KeyError):
+        semantic.family("dct")
+    assert semantic.validate_taxonomy() == []
+
+
+def test_device_helpers_without_a_gpu():
+    from kunlunxin_fft_amd import runner
+
+    if not runner.device_ready():
+        assert runner.device_name() == "cpu"
