@@ -273,3 +273,45 @@ def test_real_epilogues_check_before_the_gpu():
         runner.c2r_pre(torch.zeros(33), 64)
     with pytest.raises(TypeError, match="torch.Tensor"):
         runner.c2r_unpack([0j] * 32, 64)
+
+
+# (module, name, leading parameters in the reference's order, their defaults):
+# the module-level helpers beside the runners (ledger.py, adapter_hybrid.py,
+# semantic.py, composition.py, context.py); trailing parameters this build
+# adds after them are allowed
+REFERENCE_HELPERS = [
+    ("ledger", "phase", ["name"], {}),
+    ("ledger", "current_ledger", [], {}),
+    ("ledger", "launch_ledger", ["plan"], {}),
+    ("ledger", "measure_phases", ["plan", "x", "trials", "warmup"], {"trials": 30, "warmup": 5}),
+    ("ledger", "batch_fill_analysis", ["cases", "n_values"], {"n_values": None}),
+    ("ledger", "PhaseLedger", ["sync"], {"sync": True}),
+    ("hybrid", "plan_hybrid", ["n", "batch", "tile", "core"], {"tile": 64, "core": "vendor"}),
+    ("hybrid", "run_hybrid", ["x", "plan"], {}),
+    ("hybrid", "plan_ledger", ["plan"], {}),
+    ("hybrid", "summarize_samples", ["samples"], {}),
+    ("hybrid", "time_cell", ["fn", "x", "warmup", "trials"], {}),
+    ("hybrid", "profile_hybrid", ["x", "plan"], {}),
+    ("semantic", "spec", ["label"], {}),
+    ("semantic", "family", ["transform_type"], {}),
+    ("semantic", "family_allows", ["transform_type", "flow_id"], {}),
+    ("semantic", "family_size", ["transform_type"], {}),
+    ("semantic", "validate_taxonomy", [], {}),
+    ("composition", "composition_entry_violations", ["entry", "table"], {}),
+    ("composition", "table_violations", ["table"], {}),
+    ("context", "current_device_index", [], {}),
+    ("context", "xpu_context", ["device"], {"device": 0}),
+]
+
+
+@pytest.mark.parametrize("mod,name,params,defaults", REFERENCE_HELPERS,
+                         ids=[f"{m}.{n}" for m, n, _, _ in REFERENCE_HELPERS])
+def test_helper_signature_matches_the_reference(mod, name, params, defaults):
+    import importlib
+
+    obj = getattr(importlib.import_module(f"kunlunxin_fft_amd.{mod}"), name)
+    sig = inspect.signature(obj)
+    got = [p.name for p in sig.parameters.values() if p.kind in (p.POSITIONAL_OR_KEYWORD, p.POSITIONAL_ONLY)]
+    assert got[:len(params)] == params, got
+    for k, v in defaults.items():
+        assert sig.parameters[k].default == v, (k, sig.parameters[k].default)
