@@ -34,7 +34,7 @@ from dataclasses import dataclass, field
 from . import ledger as _ledger
 from .composition import composition_select
 from .config import NORMALIZATIONS, TRANSFORM_DIRECTIONS, TRANSFORM_TYPES
-from .selector import Selection, find_entry, load_table, select
+from .selector import Selection, default_table, find_entry, load_table, select  # noqa: F401
 
 DEFAULT_BLOCK = 256
 SUPPORTED_DIRECTIONS = ("dit", "dif")
@@ -235,7 +235,7 @@ def plan_fft(direction: str, n: int, batch: int = 1, precision: str = "fp32",
                                   transform_direction=transform_direction, normalization=norm)
         if comp is not None:
             return _composition_plan(comp, n, batch, direction, precision, transform_direction, norm)
-    table = table if table is not None else load_table()
+    table = table if table is not None else default_table()
     sel = select(direction, n, batch=batch, precision=precision, profile_hash=profile_hash,
                  table=table, env_hash=env_hash, transform_type=transform_type,
                  transform_direction=transform_direction, normalization=norm)

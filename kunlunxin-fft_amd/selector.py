@@ -73,14 +73,17 @@ def _is_pow2(v) -> bool:
     return isinstance(v, int) and v > 0 and (v & (v - 1)) == 0
 
 
-def entry_contract_violations(entry: dict) -> list[str]:
-    """Design-space and runner-family violations of one table entry."""
+def entry_contract_violations(entry: dict, space=None) -> list[str]:
+    """Design-space and runner-family violations of one table entry
+    (``space``: the loaded DesignSpace, read from disk when None)."""
     from .config import DesignSpace
 
-    try:
-        sp = DesignSpace.load()
-    except ConfigError as e:
-        return [f"design space unreadable: {e}"]
+    sp = space
+    if sp is None:
+        try:
+            sp = DesignSpace.load()
+        except ConfigError as e:
+            return [f"design space unreadable: {e}"]
     bad: list[str] = []
     n, batch = entry.get("N"), entry.get("batch")
     if not _is_pow2(n):
@@ -252,10 +255,16 @@ def load_table(path: str = TABLE_PATH) -> dict:
     for key in ("profile_hash", "precision", "guard_pct", "entries"):
         if key not in table:
             raise ConfigError(f"selector table missing required key {key!r}")
+    from .config import DesignSpace
+
+    try:
+        space = DesignSpace.load()
+    except ConfigError as e:
+        raise ConfigError(f"selector table cannot be checked: design space unreadable: {e}") from None
     problems: list[str] = []
     for e in table["entries"]:
         key = (e.get("N"), e.get("batch"), e.get("direction"))
-        problems += [f"entry {key}: {m}" for m in entry_contract_violations(e)]
+        problems += [f"entry {key}: {m}" for m in entry_contract_violations(e, space)]
     seen: set = set()
     for i, e in enumerate(table.get("previous_fallbacks") or []):
         key = (e.get("N"), e.get("batch"), e.get("direction"))
@@ -266,12 +275,33 @@ def load_table(path: str = TABLE_PATH) -> dict:
             problems.append(f"previous_fallbacks[{i}] {key} {sk}: duplicate cell")
         else:
             seen.add(key + sk)
-        problems += [f"previous_fallbacks[{i}] {key}: {m}" for m in entry_contract_violations(e)]
+        problems += [f"previous_fallbacks[{i}] {key}: {m}" for m in entry_contract_violations(e, space)]
     problems += fallback_binding_violations(table)
     if problems:
         raise ConfigError(f"selector table violates the design space / runner contract "
                           f"({len(problems)}): " + "; ".join(problems[:8])
                           + (" ..." if len(problems) > 8 else ""))
+    return table
+
+
+_DEFAULT: dict = {}  # path -> ((mtime_ns, size), validated table) for plan-time lookups
+
+
+def default_table(path: str = TABLE_PATH) -> dict:
+    """The package's table for plan-time lookups: ``load_table(path)``,
+    re-read and re-checked only when the file's modification time or size
+    changes.  The returned dict is shared and must not be modified (the
+    planner copies what it keeps); ``load_table`` gives a private copy."""
+    try:
+        st = os.stat(path)
+    except OSError:
+        return load_table(path)  # raises the loader's error
+    stamp = (st.st_mtime_ns, st.st_size)
+    hit = _DEFAULT.get(path)
+    if hit is not None and hit[0] == stamp:
+        return hit[1]
+    table = load_table(path)
+    _DEFAULT[path] = (stamp, table)
     return table
 
 
@@ -308,7 +338,7 @@ def select(direction: str, n: int, batch: int = 1, precision: str = "fp32",
            env_hash: str | None = "auto", transform_type: str = "c2c",
            transform_direction: str = "forward", normalization: str = "backward") -> Selection:
     """Measured winner for one shape, or an abstain verdict with its reason."""
-    table = table if table is not None else load_table()
+    table = table if table is not None else default_table()
     sem = (transform_type, transform_direction, normalization)
 
     def no(reason: str) -> Selection:

@@ -421,3 +421,29 @@ def test_device_helpers_without_a_gpu():
 
     if not runner.device_ready():
         assert runner.device_name() == "cpu"
+
+
+def test_default_table_is_read_once_per_file_version(tmp_path):
+    """plan_fft's table lookups reuse the validated table until the file
+    changes; load_table still returns a private copy each call."""
+    import json
+    import os
+
+    from kunlunxin_fft_amd import selector
+
+    src = selector.TABLE_PATH
+    path = tmp_path / "t.json"
+    path.write_text(open(src).read())
+    a = selector.default_table(str(path))
+    assert selector.default_table(str(path)) is a
+    assert selector.load_table(str(path)) is not a and selector.load_table(str(path)) == a
+    t = json.loads(path.read_text())
+    t["entries"] = t["entries"][:3]
+    path.write_text(json.dumps(t))
+    os.utime(path, ns=(1, 1))  # a new version even within one mtime tick
+    b = selector.default_table(str(path))
+    assert b is not a and len(b["entries"]) == 3
+    # an invalid new version raises, as load_table does
+    path.write_text("{}")
+    with pytest.raises(ConfigError):
+        selector.default_table(str(path))
