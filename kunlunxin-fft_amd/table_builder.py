@@ -57,6 +57,12 @@ C5_SIZES = [1 << k for k in range(4, 15)]        # the reference's size sweep: N
 C5_BATCHES = [1, 16, 64, 256]
 ROOF_SIZES = [1 << k for k in range(10, 21)]      # roofline rows: B = max(64, 2^25/N)
 EXTRA_CELLS = [(1 << k, 1) for k in range(15, 21)] + [(1 << 16, 256), (256, 1), (4096, 64)]
+# Every power-of-two batch of every power-of-two N from 16 to 2^20, up to
+# 2^27 elements (1 GiB of complex64 per buffer): the table answers exact
+# (N, batch) keys only, and a shape it does not hold runs the radix-2
+# baseline, one launch per stage (at N = 2^20, B = 2, 7x the four-step's time).
+DENSE_MAX_LOG_ELEMS = 27
+DENSE_LOG_N = range(4, 21)
 # real transforms, default norm: exact-semantic entries at the roofline rows
 # (the LDS kernel's real modes and the four-step around a half-length core
 # have their own best elements, stagger and split)
@@ -190,11 +196,27 @@ def carry_previous_fallbacks(prev: "dict | None", prev_sha: "str | None", table:
     return fallbacks, drops, records
 
 
+def dense_cells():
+    """(N, batch) for every power-of-two batch up to 2^DENSE_MAX_LOG_ELEMS
+    elements, N = 16 .. 2^20."""
+    return [(1 << k, 1 << j) for k in DENSE_LOG_N for j in range(0, DENSE_MAX_LOG_ELEMS - k + 1)]
+
+
+def _unique(cells_):
+    seen, out = set(), []
+    for c in cells_:
+        if c not in seen:
+            seen.add(c)
+            out.append(c)
+    return out
+
+
 def real_cells():
     """(N, batch) of the exact-semantic real entries: the roofline rows'
-    batch, and twice it (the same bytes per launch as the C2C row, which
-    bench.py's real rows use)."""
-    return [(n, b) for n in ROOF_SIZES for b in (max(64, (1 << 25) // n), 2 * max(64, (1 << 25) // n))]
+    batch and twice it (the same bytes per launch as the C2C row, which
+    bench.py's real rows use), then every dense cell."""
+    return _unique([(n, b) for n in ROOF_SIZES for b in (max(64, (1 << 25) // n), 2 * max(64, (1 << 25) // n))]
+                   + dense_cells())
 
 
 def cells(quick: bool = False):
@@ -205,11 +227,7 @@ def cells(quick: bool = False):
     for n in ROOF_SIZES:
         out.append((n, max(64, (1 << 25) // n)))
     out += EXTRA_CELLS
-    seen, uniq = set(), []
-    for c in out:
-        if c not in seen:
-            seen.add(c)
-            uniq.append(c)
+    uniq = _unique(out + dense_cells())
     if quick:
         uniq = [c for c in uniq if c[0] * c[1] <= (1 << 22) or c[1] == 1]
     return uniq
@@ -232,7 +250,9 @@ def real_candidates(n: int, b: int, transform_type: str, space):
                 continue
             if logc == 15 and e != 32:
                 continue
-            if core <= 16 and e != 16:
+            # below 16 points a thread holds at most the whole core: larger
+            # counts than the core repeat the core-sized kernel (16 is the default)
+            if e > core and e != 16:
                 continue
             stags = [s for s in space.lds_stagger
                      if s == 0 or (e >= 16 and logc >= 9 and n * b >= (1 << 24))]
@@ -277,7 +297,7 @@ def candidates(n: int, b: int, direction: str, space):
                 continue
             if e == 32 and logn < 10:
                 continue
-            if n <= 16 and e != 16:
+            if e > n and e != 16:
                 continue
             # the start stagger acts on launches of two or more waves of
             # workgroups with at most four workgroups per CU: 16 or 32
@@ -466,7 +486,7 @@ def main() -> int:
                 x = torch.randn((b, n), dtype=torch.float32, device=dev, generator=gen)
             else:
                 x = torch.randn((b, n // 2 + 1), dtype=torch.complex64, device=dev, generator=gen)
-            inc_name = "fft_dit_batch"
+            inc_name = "fft_dit" if b == 1 else "fft_dit_batch"
             inc_ms = time_runner(inc_name, n, b, 256, {}, x, tt, td)
             row = {"N": n, "batch": b, "direction": "dit", "transform_type": tt, "m0_dit@256": round(inc_ms, 5)}
             timed = []
@@ -486,7 +506,9 @@ def main() -> int:
                          "reason": f"{tt}: challenger {label} beats M0 incumbent m0_dit@256 by "
                                    f"{gain:.1f}% (>= {GUARD_PCT}%)",
                          "block": block, "flow_id": flow_id, "flow_realization": real,
-                         "processing_unit": unit, "params": dict(params, variant="folded"), "executed": name}
+                         "processing_unit": unit, "params": dict(params), "executed": name}
+                if b > 1:
+                    entry["params"]["variant"] = "folded"
                 entries.append(entry)
             print(f"{tt} N={n:>8} B={b:>6}: M0 {inc_ms:.4f} ms, best {best[1] if best else '-'} "
                   f"{best[0] if best else float('nan'):.4f} ms ({gain:+.1f}%) [{time.time() - t_start:.0f}s]",
@@ -502,7 +524,9 @@ def main() -> int:
                                "HIP events; "
                                "cells of 64 MiB and more: each execute after an untimed 256 MiB write; "
                                "forward C2C complex64 (legacy entries, answering every semantic), plus "
-                               "exact-semantic R2C / C2R entries (norm backward) at the roofline rows",
+                               "exact-semantic R2C / C2R entries (norm backward); cells: the reference's "
+                               "config-5 sweep, the roofline rows and every power-of-two batch of every "
+                               "power-of-two N = 16 .. 2^20 up to 2^27 elements",
         "sources": ["kunlunxin-fft_amd/table_builder.py live sweep"],
         "entries": entries, "previous_fallbacks": [],
     }
