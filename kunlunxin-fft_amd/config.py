@@ -111,6 +111,7 @@ class DesignSpace:
     lds_elems: tuple
     lds_max_n: int
     lds_stagger: tuple
+    lds_staged: tuple
     dense_max_n: int
     fourstep_n1: tuple
     fourstep_chunk_rows: tuple
@@ -140,6 +141,9 @@ class DesignSpace:
         stag = lds.get("stagger", [0])
         _require(isinstance(stag, list) and stag and all(isinstance(v, int) and 0 <= v <= 16 for v in stag),
                  "butterfly_space.json: P.lds_fused.stagger must be ints in [0, 16]")
+        staged = lds.get("staged", [0])
+        _require(isinstance(staged, list) and staged and all(v in (0, 1) for v in staged),
+                 "butterfly_space.json: P.lds_fused.staged must be a list of 0 / 1")
         fs = p.get("four_step", {})
         _require(_pow2_list(fs.get("n1")), "butterfly_space.json: P.four_step.n1 must be powers of two")
         ch = fs.get("chunk_rows")
@@ -163,7 +167,7 @@ class DesignSpace:
         return DesignSpace(
             space_id=d["space_id"], target=d["target"], radix=tuple(p["radix"]),
             stage_blocks=tuple(st["blocks"]), lds_elems=tuple(lds["elems"]), lds_max_n=lds["max_n"],
-            lds_stagger=tuple(stag), dense_max_n=dense["max_n"],
+            lds_stagger=tuple(stag), lds_staged=tuple(staged), dense_max_n=dense["max_n"],
             fourstep_n1=tuple(fs["n1"]), fourstep_chunk_rows=tuple(ch), fourstep_min_n=fs["min_n"],
             fourstep_schedule=tuple(sched), fourstep_pass2_order=tuple(order),
             batch_candidates=tuple(b["candidates"]), batch_variants=tuple(variants),

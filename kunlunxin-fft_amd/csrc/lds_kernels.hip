@@ -17,8 +17,11 @@
 // rows W^(k), W^(2k), W^(4k), W^(8k) (k < NS) -- a few coalesced loads per
 // butterfly; the other powers are composed with one complex product each.
 // Pass 0 reads HBM directly and the last pass writes HBM directly --
-// both are unit-stride across lanes -- and the passes in between exchange
-// through LDS.  LDS addresses carry one pad slot per 16 elements and an odd
+// both are unit-stride across the lanes of a transform -- and the passes in
+// between exchange through LDS.  With fewer than 16 threads per transform
+// those runs are shorter than 128 bytes; the staged form (C2C only) instead
+// moves the block's transforms, one contiguous run of memory, through LDS
+// with consecutive lanes on consecutive elements, on the way in and out.  LDS addresses carry one pad slot per 16 elements and an odd
 // per-transform pitch, which spreads the stride-R Stockham writes over banks.
 //
 // Modes fused into the same kernel (src/xpu/entry.py:555-587 semantics):
@@ -123,13 +126,19 @@ __device__ __forceinline__ float2 swap_halves(float2 x) {
     return make_float2(__shfl_xor(x.x, 32), __shfl_xor(x.y, 32));
 }
 
-template <int LOGL, int LOGE, int DIR, int MODE>
+// STAGED (C2C, fewer than 16 threads per transform): the block's TPB
+// transforms are TPB * L consecutive elements; they come in and go out
+// through the transforms' LDS rows, lane-consecutive, instead of straight
+// between HBM and the registers of pass 0 / the last pass.
+template <int LOGL, int LOGE, int DIR, int MODE, bool STAGED = false>
 __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE, MODE>::MIN_WAVES)) void lds_fft_kernel(
     const void* __restrict__ src_v, void* __restrict__ dst_v, const float2* __restrict__ tw,
     const float2* __restrict__ tw_real, int64_t rows, float scale, int stag_wave, int stag_cus, int stag_n) {
     using C = LdsCfg<LOGL, LOGE, MODE>;
     constexpr int L = C::L, E = C::E, T = C::T, P = C::P;
-    constexpr bool NEED_LDS = (P > 1) || (MODE == 1);
+    static_assert(!STAGED || (MODE == 0 && T < 16 && !C::SPLIT && C::TPB * L == C::WG * E),
+                  "the staged form is for C2C transforms of fewer than 16 threads");
+    constexpr bool NEED_LDS = (P > 1) || (MODE == 1) || STAGED;
     static_assert(!(C::SPLIT && MODE == 1 && C::LE != 5 && !C::PAIR),
                   "16-element r2c kernels without lane pairing stitch whole complex values out of LDS");
     __shared__ float2 lds_raw[NEED_LDS ? (C::LDS_FLOATS + 1) / 2 : 1];
@@ -274,6 +283,22 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
                     v[m.value * R0 + q.value] = z;
                 });
             });
+        } else if constexpr (STAGED) {
+            // element k of the block's run belongs to transform k / L; lane
+            // k's loads of one instruction are 64 consecutive elements
+            const float2* src = (const float2*)src_v + (int64_t)blockIdx.x * C::TPB * L;
+            const int64_t here = rows - (int64_t)blockIdx.x * C::TPB;  // transforms of this block that exist
+            static_for<0, E>([&](auto r) {
+                const int k = tid + r.value * C::WG;
+                if ((k >> LOGL) < here) lds[(k >> LOGL) * C::PITCH + pad(k & (L - 1))] = load_nt(src + k);
+            });
+            __syncthreads();
+            const int pj = pad(j);
+            static_for<0, NB0>([&](auto m) {
+                static_for<0, R0>([&](auto q) {
+                    v[m.value * R0 + q.value] = lt[pad_add<m.value * T + q.value * (L / R0)>(pj, j)];
+                });
+            });
         } else {
             // non-temporal: every input element is read exactly once, and
             // keeping it out of L2 and the MALL measured 5-10% faster
@@ -313,7 +338,7 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
         });
         if constexpr ((p < P - 1 || (MODE == 1 && !C::PAIR)) && !C::SPLIT) {
             // every thread has read this pass's inputs (pass 0 of c2r: the partner bins)
-            if constexpr (p > 0 || (MODE == 2 && !C::PAIR)) __syncthreads();
+            if constexpr (p > 0 || (MODE == 2 && !C::PAIR) || STAGED) __syncthreads();
             static_for<0, NB>([&](auto m) {
                 const int b = j + m.value * T;
                 const int base = ((b >> LNS) << (LNS + LR)) + (b & (NS - 1));
@@ -424,6 +449,24 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
             static_for<0, E>([&](auto m) { stitch(j + m.value * T); });
             if (j == 0) stitch(L);
         }
+    } else if constexpr (STAGED) {
+        constexpr int LR = C::logr(P - 1);
+        constexpr int R = 1 << LR;
+        constexpr int NB = E / R;
+        constexpr int NS = L / R;
+        __syncthreads();  // every read of the last pass's operands from LDS is done
+        static_for<0, NB>([&](auto m) {
+            const int b = j + m.value * T;
+            const int pb = pad(b);
+            static_for<0, R>([&](auto q) { lt[pad_add<q.value * NS>(pb, b)] = v[m.value * R + q.value]; });
+        });
+        __syncthreads();
+        float2* dst = (float2*)dst_v + (int64_t)blockIdx.x * C::TPB * L;
+        const int64_t here = rows - (int64_t)blockIdx.x * C::TPB;
+        static_for<0, E>([&](auto r) {
+            const int k = tid + r.value * C::WG;
+            if ((k >> LOGL) < here) dst[k] = cscale(lds[(k >> LOGL) * C::PITCH + pad(k & (L - 1))], scale);
+        });
     } else {
         constexpr int LR = C::logr(P - 1);
         constexpr int R = 1 << LR;
@@ -450,9 +493,10 @@ struct LdsArgs {
     hipStream_t stream;
     int num_cus;  // compute units of the device (start stagger)
     int stagger;  // start stagger, s_sleep(127) units (0 = off)
+    bool staged;  // C2C of fewer than 16 threads per transform: in and out through LDS
 };
 
-template <int LOGL, int LOGE, int DIR, int MODE>
+template <int LOGL, int LOGE, int DIR, int MODE, bool STAGED = false>
 hipError_t launch_one(const LdsArgs& a) {
     using C = LdsCfg<LOGL, LOGE>;
     const int64_t blocks = (a.rows + C::TPB - 1) / C::TPB;
@@ -463,7 +507,8 @@ hipError_t launch_one(const LdsArgs& a) {
         // blocks one wave of the grid holds (occupancy query, once per kernel)
         static const int per_cu = [] {
             int b = 0;
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, lds_fft_kernel<LOGL, LOGE, DIR, MODE>, C::WG, 0) !=
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, lds_fft_kernel<LOGL, LOGE, DIR, MODE, STAGED>, C::WG,
+                                                             0) !=
                 hipSuccess) {
                 (void)hipGetLastError();
                 b = 0;
@@ -474,7 +519,7 @@ hipError_t launch_one(const LdsArgs& a) {
         // only when the launch runs at least two waves of blocks
         if (wave > 0 && blocks >= 2 * wave) wave_blocks = (int)wave, n = a.stagger;
     }
-    lds_fft_kernel<LOGL, LOGE, DIR, MODE><<<(unsigned)blocks, C::WG, 0, a.stream>>>(
+    lds_fft_kernel<LOGL, LOGE, DIR, MODE, STAGED><<<(unsigned)blocks, C::WG, 0, a.stream>>>(
         a.src, a.dst, a.tw, a.tw_real, a.rows, a.scale, wave_blocks, a.num_cus / 8, n);
     mark(a.stream);
     return hipGetLastError();
@@ -482,6 +527,11 @@ hipError_t launch_one(const LdsArgs& a) {
 
 template <int LOGL, int LOGE>
 hipError_t dispatch_mode(int mode, int dir, const LdsArgs& a) {
+    if constexpr (LdsCfg<LOGL, LOGE>::T < 16) {
+        if (mode == 0 && a.staged)
+            return dir < 0 ? launch_one<LOGL, LOGE, -1, 0, true>(a) : launch_one<LOGL, LOGE, 1, 0, true>(a);
+    }
+    if (a.staged) return hipErrorInvalidValue;  // refused at plan creation
     if (mode == 0) return dir < 0 ? launch_one<LOGL, LOGE, -1, 0>(a) : launch_one<LOGL, LOGE, 1, 0>(a);
     if (mode == 1) return launch_one<LOGL, LOGE, -1, 1>(a);
     return launch_one<LOGL, LOGE, 1, 2>(a);
@@ -490,6 +540,7 @@ hipError_t dispatch_mode(int mode, int dir, const LdsArgs& a) {
 // 32 elements per thread (split exchange)
 template <int LOGL>
 hipError_t dispatch_split(int mode, int dir, const LdsArgs& a) {
+    if (a.staged) return hipErrorInvalidValue;  // 32 elements: at least 32 threads per transform
     if (mode == 0) return dir < 0 ? launch_one<LOGL, 5, -1, 0>(a) : launch_one<LOGL, 5, 1, 0>(a);
     if (mode == 1) return launch_one<LOGL, 5, -1, 1>(a);
     if (mode == 2) return launch_one<LOGL, 5, 1, 2>(a);
@@ -536,11 +587,16 @@ int lds_threads_per_block(int log2l, int elems) {
     return t >= 256 ? t : 256;
 }
 
+bool lds_staged_supported(int log2l, int elems) {
+    const int le = ilog2(elems) < log2l ? ilog2(elems) : log2l;
+    return lds_supported(log2l, elems) && elems != 0 && elems != 32 && (log2l - le) < 4;
+}
+
 hipError_t launch_lds(int mode, int dir, int log2l, int elems, const void* src, void* dst,
                       const float2* tw, const float2* tw_real, int64_t rows, float scale,
-                      hipStream_t stream, int num_cus, int stagger) {
+                      hipStream_t stream, int num_cus, int stagger, bool staged) {
     const int loge = ilog2(elems);
-    const LdsArgs a{src, dst, tw, tw_real, rows, scale, stream, num_cus, stagger};
+    const LdsArgs a{src, dst, tw, tw_real, rows, scale, stream, num_cus, stagger, staged};
     switch (log2l) {
         case 0: return dispatch_elems<0>(loge, mode, dir, a);
         case 1: return dispatch_elems<1>(loge, mode, dir, a);

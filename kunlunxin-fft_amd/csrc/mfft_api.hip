@@ -211,7 +211,7 @@ int run_core(const mfft_plan* p, const float2* src, float2* dst, int dir, float 
             break;
         case MFFT_FLOW_LDS_FUSED:
             e = mfft::launch_lds(0, dir, mfft::ilog2((int)p->core_n), p->elems, src, dst, p->tw, nullptr,
-                                 p->batch, scale, stream, p->num_cus, p->stagger);
+                                 p->batch, scale, stream, p->num_cus, p->stagger, p->staged);
             break;
         case MFFT_FLOW_FOUR_STEP:
             e = mfft::launch_fourstep(dir, src, dst, w.f, p, p->batch, scale, stream, &launches);
@@ -384,6 +384,7 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
     if (flow == MFFT_FLOW_AUTO)
         flow = mfft::lds_supported(logc, 0) ? MFFT_FLOW_LDS_FUSED : MFFT_FLOW_FOUR_STEP;
     int block = 256, elems = 0, stagger = 0;
+    bool staged = false;
     int64_t n1 = 0, n2 = 0, chunk = 0;
     int schedule = 0, pass2_rev = 0, fused_lag = 0, fused_take = 0, fused_ring = 0, fused_bpc = 0;
     switch (flow) {
@@ -416,6 +417,15 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
                 return fail(MFFT_ERR_VALUE, "LDS_FUSED start stagger params[1]=%d exceeds %d", prm[1],
                             mfft::kMaxStagger);
             stagger = prm[1];
+            if (prm[2] > 1)
+                return fail(MFFT_ERR_VALUE, "LDS_FUSED staged form params[2] must be 0 or 1, got %d", prm[2]);
+            if (prm[2] && (transform_type != MFFT_C2C || !mfft::lds_staged_supported(logc, elems)))
+                return fail(MFFT_ERR_UNSUPPORTED,
+                            "the staged LDS_FUSED form (params[2] = 1) runs C2C with fewer than 16 threads "
+                            "per transform (core length / elements per thread < 16; got core length %lld, "
+                            "elements %d)",
+                            (long long)core_n, elems);
+            staged = prm[2] != 0;
             break;
         case MFFT_FLOW_FOUR_STEP: {
             int l1, l2;
@@ -574,6 +584,7 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
     p->block = block;
     p->elems = elems;
     p->stagger = stagger;
+    p->staged = staged;
     p->n1 = n1;
     p->n2 = n2;
     p->chunk_rows = chunk;

@@ -111,6 +111,9 @@ def entry_contract_violations(entry: dict, space=None) -> list[str]:
         stg = params.get("stagger", 0)
         if stg not in (0,) + sp.lds_stagger:
             bad.append(f"stagger {stg!r} not in {sp.lds_stagger}")
+        stage = params.get("stage", 0)
+        if stage not in (0,) + sp.lds_staged:
+            bad.append(f"stage {stage!r} not in {sp.lds_staged}")
         if isinstance(n, int) and n > 2 * sp.lds_max_n:
             bad.append(f"N={n} exceeds the LDS kernel's range ({sp.lds_max_n} complex core)")
     if real == "matrix-resident":

@@ -307,6 +307,10 @@ def candidates(n: int, b: int, direction: str, space):
                 params = {"elems": e} if stg == 0 else {"elems": e, "stagger": stg}
                 out.append((f"lds_e{e}" + (f"_s{stg}" if stg else ""), "fft_lds_fused" + sfx, 256, params,
                             ("lds-resident", "stockham-radix16", "lds-stockham-single-pass")))
+            # the staged form: fewer than 16 threads per transform
+            if 1 in space.lds_staged and e != 32 and n // min(e, n) < 16:
+                out.append((f"lds_e{e}_st", "fft_lds_fused" + sfx, 256, {"elems": e, "stage": 1},
+                            ("lds-resident", "stockham-radix16", "lds-stockham-single-pass")))
     if 2 <= n <= space.dense_max_n:
         # the dense-dot matrix-core flow (the reference's M2 dense-dot FFT64)
         name = ("fft_dit_matrix" if direction == "dit" else "fft_dif_matrix") + sfx
