@@ -221,3 +221,27 @@ def test_release_retired_destroys_each_handle_once(monkeypatch):
         t.join()
     assert sorted(destroyed) == sorted("h%d" % i for i in range(100))
     assert sum(counts) == 100 and len(retired) == 0
+
+
+def test_staged_form_maps_only_where_it_exists():
+    """The staged LDS form (params[2] = 1) reaches the C ABI for C2C with
+    fewer than 16 threads per transform; elsewhere the mapping drops it, as
+    the library would refuse it.  The builder offers it exactly there."""
+    lds = native.FLOW_LDS_FUSED
+    assert flow_params("fft_lds_fused_batch", 16, "c2c", 256, {"elems": 4, "stage": 1}) == (lds, (4, 0, 1))
+    assert flow_params("fft_lds_fused_batch", 16, "c2c", 256, {"stage": 1}) == (lds, (0, 0, 1))  # default 16: T = 1
+    assert flow_params("fft_lds_fused_batch", 128, "c2c", 256, {"elems": 16, "stage": 1}) == (lds, (16, 0, 1))
+    assert flow_params("fft_lds_fused_batch", 64, "c2c", 256, {"elems": 4, "stage": 1}) == (lds, (4, 0))  # T = 16
+    assert flow_params("fft_lds_fused_batch", 256, "c2c", 256, {"stage": 1}) == (lds, (0, 0))  # default 16: T = 16
+    assert flow_params("fft_lds_fused_batch", 32, "r2c", 256, {"elems": 4, "stage": 1}) == (lds, (4, 0))
+    assert flow_params("fft_lds_fused_batch", 32, "c2r", 256, {"elems": 4, "stage": 1}) == (lds, (4, 0))
+    sp = DesignSpace.load()
+    for n in (16, 32, 64, 128, 256):
+        staged = [c for c in candidates(n, 4096, "dit", sp) if c[3].get("stage")]
+        want = {e for e in sp.lds_elems if e != 32 and n // min(e, n) < 16}
+        assert {c[3]["elems"] for c in staged} == want, n
+        for label, name, block, params, (real, unit, flow_id) in staged:
+            e = _entry(params, real=real, unit=unit, n=n, b=4096, executed=name)
+            assert not entry_contract_violations(e), (label, entry_contract_violations(e))
+    bad = _entry({"elems": 4, "stage": 2}, n=16, b=4096)
+    assert any("stage" in v for v in entry_contract_violations(bad))
