@@ -126,18 +126,21 @@ __device__ __forceinline__ float2 swap_halves(float2 x) {
     return make_float2(__shfl_xor(x.x, 32), __shfl_xor(x.y, 32));
 }
 
-// STAGED (C2C, fewer than 16 threads per transform): the block's TPB
-// transforms are TPB * L consecutive elements; they come in and go out
-// through the transforms' LDS rows, lane-consecutive, instead of straight
-// between HBM and the registers of pass 0 / the last pass.
+// STAGED (fewer than 16 threads per transform): the block's TPB rows are
+// one contiguous run of memory (L complex values per row in and out of the
+// core; L + 1 bins per row of the R2C output and the C2R input); they come
+// in and go out through LDS, lane-consecutive, instead of straight between
+// HBM and the registers of pass 0 / the last pass or the stitch.
 template <int LOGL, int LOGE, int DIR, int MODE, bool STAGED = false>
 __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE, MODE>::MIN_WAVES)) void lds_fft_kernel(
     const void* __restrict__ src_v, void* __restrict__ dst_v, const float2* __restrict__ tw,
     const float2* __restrict__ tw_real, int64_t rows, float scale, int stag_wave, int stag_cus, int stag_n) {
     using C = LdsCfg<LOGL, LOGE, MODE>;
     constexpr int L = C::L, E = C::E, T = C::T, P = C::P;
-    static_assert(!STAGED || (MODE == 0 && T < 16 && !C::SPLIT && C::TPB * L == C::WG * E),
-                  "the staged form is for C2C transforms of fewer than 16 threads");
+    static_assert(!STAGED || (T < 16 && !C::SPLIT && !C::PAIR && C::TPB * L == C::WG * E),
+                  "the staged form is for transforms of fewer than 16 threads");
+    // rows of L + 1 bins (R2C output, C2R input) of the staged form, flat in LDS
+    static_assert(!STAGED || C::TPB * (L + 1) <= (C::LDS_FLOATS / 2), "staged bin rows exceed the LDS rows");
     constexpr bool NEED_LDS = (P > 1) || (MODE == 1) || STAGED;
     static_assert(!(C::SPLIT && MODE == 1 && C::LE != 5 && !C::PAIR),
                   "16-element r2c kernels without lane pairing stitch whole complex values out of LDS");
@@ -170,7 +173,31 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
     {
         constexpr int R0 = 1 << C::logr(0);
         constexpr int NB0 = E / R0;
-        if constexpr (MODE == 2 && C::PAIR) {
+        if constexpr (STAGED && MODE == 2) {
+            // the block's TPB rows of L + 1 bins, lane-consecutive, into a
+            // flat LDS array; each core input then pairs bin i with bin L - i
+            // out of LDS (bin 0 with bin L, both imaginary parts ignored)
+            const float2* src = (const float2*)src_v + (int64_t)blockIdx.x * C::TPB * (L + 1);
+            const int64_t here = rows - (int64_t)blockIdx.x * C::TPB;
+            static_for<0, E + 1>([&](auto r) {
+                const int k = tid + r.value * C::WG;
+                if (k < C::TPB * (L + 1) && k / (L + 1) < here) lds[k] = load_nt(src + k);
+            });
+            __syncthreads();
+            const float2* xb = lds + tl * (L + 1);
+            static_for<0, NB0>([&](auto m) {
+                static_for<0, R0>([&](auto q) {
+                    const int i = j + m.value * T + q.value * (L / R0);
+                    float2 xk = xb[i];
+                    float2 xj = xb[L - i];
+                    if (i == 0) {
+                        xk.y = 0.0f;
+                        xj.y = 0.0f;
+                    }
+                    v[m.value * R0 + q.value] = c2r_pre_bin(xk, xj, tw_real[i]);
+                });
+            });
+        } else if constexpr (MODE == 2 && C::PAIR) {
             // Each bin is loaded once (non-temporal), v[q] = X[j + T*q]; the
             // mirror of bin j + T*q is the partner lane's v[E-1-q], except for
             // j = T/2 (its own v[E-1-q]) and j = 0 (its own v[E-q], and bin L
@@ -284,8 +311,9 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
                 });
             });
         } else if constexpr (STAGED) {
-            // element k of the block's run belongs to transform k / L; lane
-            // k's loads of one instruction are 64 consecutive elements
+            // C2C, and R2C's real rows viewed as L complex values: element k
+            // of the block's run belongs to row k / L; one load instruction
+            // covers 64 consecutive elements
             const float2* src = (const float2*)src_v + (int64_t)blockIdx.x * C::TPB * L;
             const int64_t here = rows - (int64_t)blockIdx.x * C::TPB;  // transforms of this block that exist
             static_for<0, E>([&](auto r) {
@@ -437,6 +465,27 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
                 else if (k != L / 2) xo[L - k] = r2c_bin(zj, zk, tw_real[L - k], scale, false);
             }
         }
+    } else if constexpr (MODE == 1 && STAGED) {
+        // the stitch of every bin this thread owns into registers, then the
+        // block's TPB rows of L + 1 bins out through a flat LDS array,
+        // lane-consecutive
+        float2 bins[E];
+        static_for<0, E>([&](auto m) {
+            const int k = j + m.value * T;
+            bins[m.value] = r2c_bin(lt[pad(k)], lt[pad((L - k) & (L - 1))], tw_real[k], scale, k == 0);
+        });
+        const float2 last = r2c_bin(lt[pad(0)], lt[pad(0)], tw_real[L], scale, true);
+        __syncthreads();  // every stitch read of the core outputs is done
+        float2* xs = lds + tl * (L + 1);
+        static_for<0, E>([&](auto m) { xs[j + m.value * T] = bins[m.value]; });
+        if (j == 0) xs[L] = last;
+        __syncthreads();
+        float2* xo = (float2*)dst_v + (int64_t)blockIdx.x * C::TPB * (L + 1);
+        const int64_t here = rows - (int64_t)blockIdx.x * C::TPB;
+        static_for<0, E + 1>([&](auto r) {
+            const int k = tid + r.value * C::WG;
+            if (k < C::TPB * (L + 1) && k / (L + 1) < here) xo[k] = lds[k];
+        });
     } else if constexpr (MODE == 1) {
         // r2c stitch out of LDS: bins k in [0, L], X[k] = a - i*w*c
         float2* xo = (float2*)dst_v + row * (L + 1);
@@ -528,8 +577,12 @@ hipError_t launch_one(const LdsArgs& a) {
 template <int LOGL, int LOGE>
 hipError_t dispatch_mode(int mode, int dir, const LdsArgs& a) {
     if constexpr (LdsCfg<LOGL, LOGE>::T < 16) {
-        if (mode == 0 && a.staged)
-            return dir < 0 ? launch_one<LOGL, LOGE, -1, 0, true>(a) : launch_one<LOGL, LOGE, 1, 0, true>(a);
+        if (a.staged) {
+            if (mode == 0)
+                return dir < 0 ? launch_one<LOGL, LOGE, -1, 0, true>(a) : launch_one<LOGL, LOGE, 1, 0, true>(a);
+            if (mode == 1) return launch_one<LOGL, LOGE, -1, 1, true>(a);
+            return launch_one<LOGL, LOGE, 1, 2, true>(a);
+        }
     }
     if (a.staged) return hipErrorInvalidValue;  // refused at plan creation
     if (mode == 0) return dir < 0 ? launch_one<LOGL, LOGE, -1, 0>(a) : launch_one<LOGL, LOGE, 1, 0>(a);

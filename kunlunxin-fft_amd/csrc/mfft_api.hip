@@ -272,7 +272,7 @@ int execute_impl(const mfft_plan* p, const void* in, void* out, const Work& w, v
     if (p->transform_type == MFFT_R2C) {
         if (p->r2c_fused) {
             he = mfft::launch_lds(1, -1, logc, p->elems, in, out, p->tw, p->tw_real, p->batch, p->scale, stream,
-                                  p->num_cus, p->stagger);
+                                  p->num_cus, p->stagger, p->staged);
             return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
         }
         if (p->real4_fused) {
@@ -302,7 +302,7 @@ int execute_impl(const mfft_plan* p, const void* in, void* out, const Work& w, v
     // c2r
     if (p->c2r_fused) {
         he = mfft::launch_lds(2, 1, logc, p->elems, in, out, p->tw, p->tw_real, p->batch, p->scale, stream,
-                              p->num_cus, p->stagger);
+                              p->num_cus, p->stagger, p->staged);
         return he == hipSuccess ? MFFT_OK : hip_fail(he, "kernel launch");
     }
     if (p->real4_fused) {
@@ -419,10 +419,10 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
             stagger = prm[1];
             if (prm[2] > 1)
                 return fail(MFFT_ERR_VALUE, "LDS_FUSED staged form params[2] must be 0 or 1, got %d", prm[2]);
-            if (prm[2] && (transform_type != MFFT_C2C || !mfft::lds_staged_supported(logc, elems)))
+            if (prm[2] && !mfft::lds_staged_supported(logc, elems))
                 return fail(MFFT_ERR_UNSUPPORTED,
-                            "the staged LDS_FUSED form (params[2] = 1) runs C2C with fewer than 16 threads "
-                            "per transform (core length / elements per thread < 16; got core length %lld, "
+                            "the staged LDS_FUSED form (params[2] = 1) runs transforms of fewer than 16 "
+                            "threads (core length / elements per thread < 16; got core length %lld, "
                             "elements %d)",
                             (long long)core_n, elems);
             staged = prm[2] != 0;

@@ -74,13 +74,13 @@ def flow_params(executed: str, n: int, transform_type: str, block, params: dict)
             e = 0
         if logc == 15:
             e = 0
-        # the staged form: C2C with fewer than 16 threads per transform
+        # the staged form: fewer than 16 threads per transform of the core
         # (the elements per thread the library resolves e = 0 to, below 2^15:
         # 16 up to 16 points, 8 up to 64, else 16)
         stage = int(params.get("stage", 0))
         if stage:
             eff = e or (16 if logc <= 4 else 8 if logc <= 6 else 16)
-            if transform_type != "c2c" or eff == 32 or logc - min(eff.bit_length() - 1, logc) >= 4:
+            if eff == 32 or logc - min(eff.bit_length() - 1, logc) >= 4:
                 stage = 0
         if stage:
             return flow, (e, int(params.get("stagger", 0)), 1)

@@ -260,6 +260,10 @@ def real_candidates(n: int, b: int, transform_type: str, space):
                 params = {"elems": e} if stg == 0 else {"elems": e, "stagger": stg}
                 out.append((f"lds_e{e}" + (f"_s{stg}" if stg else ""), "fft_lds_fused" + sfx, 256, params,
                             ("lds-resident", "stockham-radix16", "lds-stockham-single-pass")))
+            # the staged form: fewer than 16 threads per transform of the core
+            if 1 in space.lds_staged and e != 32 and core // min(e, core) < 16:
+                out.append((f"lds_e{e}_st", "fft_lds_fused" + sfx, 256, {"elems": e, "stage": 1},
+                            ("lds-resident", "stockham-radix16", "lds-stockham-single-pass")))
     if 256 <= core and core * 2 >= space.fourstep_min_n:
         for n1 in space.fourstep_n1:
             n2 = core // n1

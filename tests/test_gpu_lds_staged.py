@@ -1,6 +1,8 @@
-"""The LDS kernel's staged C2C form (LDS_FUSED params[2] = 1): for fewer
-than 16 threads per transform, a workgroup's transforms come in and go out
-through LDS with consecutive lanes on consecutive elements.  Only the path
+"""The LDS kernel's staged form (LDS_FUSED params[2] = 1): for fewer than
+16 threads per transform, a workgroup's rows come in and go out through LDS
+with consecutive lanes on consecutive elements (C2C; R2C, whose bin rows
+of N/2 + 1 values leave through a flat LDS array; C2R, whose bin rows come
+in through one and are paired with their mirrors there).  Only the path
 between HBM and the Stockham registers changes: its results must match the
 unstaged kernel's to a few units in the last place (the two instantiations
 may contract products into FMAs differently, which moves the last bit) and
@@ -29,13 +31,47 @@ def staged_cases():
     return out
 
 
-def plan(n, b, elems, stage, td="forward", norm="backward"):
+def plan(n, b, elems, stage, td="forward", norm="backward", tt="c2c"):
     params = {"elems": elems}
     if stage:
         params["stage"] = 1
     return ExecutionPlan(n=n, batch=b, direction="dit", precision="fp32", selection_source="table",
                          reason="test", fallback=False, executed="fft_lds_fused" + ("_batch" if b > 1 else ""),
-                         block=256, params=params, transform_direction=td, norm=norm)
+                         block=256, params=params, transform_type=tt, transform_direction=td, norm=norm)
+
+
+def real_cases():
+    # (N, elems): core N/2 of fewer than 16 threads at `elems` per thread
+    return [(2 * c, e) for c, e in staged_cases()]
+
+
+@pytest.mark.parametrize("n,elems", real_cases(), ids=[f"N{n}-e{e}" for n, e in real_cases()])
+@pytest.mark.parametrize("b", [1, 3, 255, 4099])
+def test_staged_real_equals_unstaged_and_numpy(gpu, n, elems, b):
+    rng = np.random.default_rng(n * 7 + b)
+    r = rng.standard_normal((b, n)).astype(np.float32)
+    rt = torch.from_numpy(r if b > 1 else r[0]).to(gpu)
+    for norm in ("backward", "ortho", "forward"):
+        h = execute_fft_plan(plan(n, b, elems, 1, tt="r2c", norm=norm), rt)
+        h0 = execute_fft_plan(plan(n, b, elems, 0, tt="r2c", norm=norm), rt)
+        d = (h - h0).abs().max().item() / max(h0.abs().max().item(), 1e-30)
+        assert d <= 4e-7, f"r2c N={n} e={elems} B={b} {norm}: staged differs by {d:.2e}"
+        ref = np.fft.rfft(r.astype(np.float64), norm=norm)
+        got = h.cpu().numpy().reshape(b, n // 2 + 1)
+        l2, mx = oracle.rel_l2(got, ref), oracle.max_rel_error(got, ref)
+        assert l2 <= TOL and mx <= TOL, f"r2c N={n} e={elems} B={b} {norm}: rel_l2={l2:.3e} max={mx:.3e}"
+        # C2R of the spectrum, with nonzero DC and Nyquist imaginary parts (ignored)
+        hs = h0.clone()
+        hs[..., 0] += 0.5j
+        hs[..., -1] -= 0.25j
+        y = execute_fft_plan(plan(n, b, elems, 1, td="inverse", tt="c2r", norm=norm), hs)
+        y0 = execute_fft_plan(plan(n, b, elems, 0, td="inverse", tt="c2r", norm=norm), hs)
+        d = (y - y0).abs().max().item() / max(y0.abs().max().item(), 1e-30)
+        assert d <= 4e-7, f"c2r N={n} e={elems} B={b} {norm}: staged differs by {d:.2e}"
+        ref = np.fft.irfft(h0.cpu().numpy().reshape(b, -1).astype(np.complex128), n=n, norm=norm)
+        got = y.cpu().numpy().reshape(b, n)
+        l2, mx = oracle.rel_l2(got, ref), oracle.max_rel_error(got, ref)
+        assert l2 <= TOL and mx <= TOL, f"c2r N={n} e={elems} B={b} {norm}: rel_l2={l2:.3e} max={mx:.3e}"
 
 
 @pytest.mark.parametrize("n,elems", staged_cases(), ids=[f"N{n}-e{e}" for n, e in staged_cases()])
@@ -68,11 +104,12 @@ def test_staged_large_batch_rows_at_the_ends(gpu):
     assert oracle.rel_l2(y[rows].cpu().numpy(), ref) <= TOL
 
 
-@pytest.mark.parametrize("n,elems,tt", [(64, 4, "c2c"), (256, 16, "c2c"), (32, 4, "r2c"), (32, 4, "c2r"),
+@pytest.mark.parametrize("n,elems,tt", [(64, 4, "c2c"), (256, 16, "c2c"), (128, 4, "r2c"), (512, 16, "c2r"),
                                         (2048, 32, "c2c")])
 def test_staged_refused_where_it_does_not_exist(gpu, n, elems, tt):
-    """16 or more threads per transform, or a real transform: the C ABI
-    refuses params[2] = 1 (MFFT_ERR_UNSUPPORTED, ValueError here)."""
+    """16 or more threads per transform of the core, or 32 elements per
+    thread: the C ABI refuses params[2] = 1 (MFFT_ERR_UNSUPPORTED,
+    ValueError here), and params[2] = 2 (MFFT_ERR_VALUE)."""
     td = "inverse" if tt == "c2r" else "forward"
     with pytest.raises(ValueError, match="staged"):
         native.NativePlan(n, 4, tt, td, "backward", native.FLOW_LDS_FUSED, (elems, 0, 1))

@@ -224,8 +224,8 @@ def test_release_retired_destroys_each_handle_once(monkeypatch):
 
 
 def test_staged_form_maps_only_where_it_exists():
-    """The staged LDS form (params[2] = 1) reaches the C ABI for C2C with
-    fewer than 16 threads per transform; elsewhere the mapping drops it, as
+    """The staged LDS form (params[2] = 1) reaches the C ABI for fewer than
+    16 threads per transform of the core; elsewhere the mapping drops it, as
     the library would refuse it.  The builder offers it exactly there."""
     lds = native.FLOW_LDS_FUSED
     assert flow_params("fft_lds_fused_batch", 16, "c2c", 256, {"elems": 4, "stage": 1}) == (lds, (4, 0, 1))
@@ -233,8 +233,10 @@ def test_staged_form_maps_only_where_it_exists():
     assert flow_params("fft_lds_fused_batch", 128, "c2c", 256, {"elems": 16, "stage": 1}) == (lds, (16, 0, 1))
     assert flow_params("fft_lds_fused_batch", 64, "c2c", 256, {"elems": 4, "stage": 1}) == (lds, (4, 0))  # T = 16
     assert flow_params("fft_lds_fused_batch", 256, "c2c", 256, {"stage": 1}) == (lds, (0, 0))  # default 16: T = 16
-    assert flow_params("fft_lds_fused_batch", 32, "r2c", 256, {"elems": 4, "stage": 1}) == (lds, (4, 0))
-    assert flow_params("fft_lds_fused_batch", 32, "c2r", 256, {"elems": 4, "stage": 1}) == (lds, (4, 0))
+    # real transforms: the core of length n/2 decides
+    assert flow_params("fft_lds_fused_batch", 32, "r2c", 256, {"elems": 4, "stage": 1}) == (lds, (4, 0, 1))
+    assert flow_params("fft_lds_fused_batch", 32, "c2r", 256, {"elems": 4, "stage": 1}) == (lds, (4, 0, 1))
+    assert flow_params("fft_lds_fused_batch", 128, "r2c", 256, {"elems": 4, "stage": 1}) == (lds, (4, 0))  # T = 16
     sp = DesignSpace.load()
     for n in (16, 32, 64, 128, 256):
         staged = [c for c in candidates(n, 4096, "dit", sp) if c[3].get("stage")]
