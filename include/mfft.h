@@ -97,11 +97,11 @@ enum {
  *                                    every XCD's CUs start params[1] x 8128
  *                                    clocks late, so that CUs stop loading,
  *                                    computing and storing in lockstep,
- *                        params[2] = staged form (0 or 1; C2C with core
- *                                    length / elements per thread < 16):
- *                                    the workgroup's transforms, one
- *                                    contiguous run, go in and out through
- *                                    LDS with consecutive lanes on
+ *                        params[2] = staged form (0 or 1; core length /
+ *                                    elements per thread < 16, any
+ *                                    transform type): the workgroup's rows,
+ *                                    one contiguous run, go in and out
+ *                                    through LDS with consecutive lanes on
  *                                    consecutive elements
  *   DENSE_MFMA:          no parameters
  *   FOUR_STEP:           params[0] = n1 (column FFT length; n2 = core_n/n1),

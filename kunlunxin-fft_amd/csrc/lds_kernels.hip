@@ -19,9 +19,10 @@
 // Pass 0 reads HBM directly and the last pass writes HBM directly --
 // both are unit-stride across the lanes of a transform -- and the passes in
 // between exchange through LDS.  With fewer than 16 threads per transform
-// those runs are shorter than 128 bytes; the staged form (C2C only) instead
-// moves the block's transforms, one contiguous run of memory, through LDS
-// with consecutive lanes on consecutive elements, on the way in and out.  LDS addresses carry one pad slot per 16 elements and an odd
+// those runs are shorter than 128 bytes (and the bin rows of the real modes
+// are not aligned); the staged form instead moves the block's rows, one
+// contiguous run of memory, through LDS with consecutive lanes on
+// consecutive elements, on the way in and out.  LDS addresses carry one pad slot per 16 elements and an odd
 // per-transform pitch, which spreads the stride-R Stockham writes over banks.
 //
 // Modes fused into the same kernel (src/xpu/entry.py:555-587 semantics):

@@ -18,7 +18,7 @@ struct mfft_plan {
     int block = 256;     // stage flows: threads per block
     int elems = 16;      // LDS_FUSED: elements per thread
     int stagger = 0;     // LDS_FUSED: start stagger of half the first wave, s_sleep(127) units
-    bool staged = false; // LDS_FUSED C2C: transforms in and out through LDS, lane-consecutive
+    bool staged = false; // LDS_FUSED: rows in and out through LDS, lane-consecutive
     int launches = 0;
     int64_t n1 = 0, n2 = 0, chunk_rows = 0;
     int schedule = 0;    // FOUR_STEP: 0 one column group per block, 1 persistent, 2 fused (one launch)
@@ -124,7 +124,7 @@ int lds_threads_per_block(int log2l, int elems);
 hipError_t launch_lds(int mode, int dir, int log2l, int elems, const void* src, void* dst,
                       const float2* tw, const float2* tw_real, int64_t rows, float scale,
                       hipStream_t stream, int num_cus = 0, int stagger = 0, bool staged = false);
-// the staged C2C form exists for these (fewer than 16 threads per transform)
+// the staged form exists for these (fewer than 16 threads per transform)
 bool lds_staged_supported(int log2l, int elems);
 
 // ---- mfma_kernels.hip: dense-dot core on the fp32 matrix cores -----------
