@@ -313,13 +313,16 @@ def fft_dif_radix4_batch(x, block: int = 1024, variant: str = "spread", twiddle=
     return _batched("fft_dif_radix4_batch", x, block, twiddle=twiddle, variant=variant, spread_only=True)
 
 
-def fft_lds_fused(x, elems: int = 0, twiddle=None):
-    """Single-pass LDS-resident Stockham FFT (core length <= 32768)."""
-    return _single("fft_lds_fused", x, None, {"elems": elems}, twiddle=twiddle)
+def fft_lds_fused(x, elems: int = 0, twiddle=None, *, stagger: int = 0, stage: int = 0):
+    """Single-pass LDS-resident Stockham FFT (core length <= 32768); the
+    keywords are the LDS_FUSED flow parameters of include/mfft.h (elements
+    per thread, start stagger, staged form), 0 = the library's default."""
+    return _single("fft_lds_fused", x, None, {"elems": elems, "stagger": stagger, "stage": stage}, twiddle=twiddle)
 
 
-def fft_lds_fused_batch(x, elems: int = 0, twiddle=None):
-    return _batched("fft_lds_fused_batch", x, None, {"elems": elems}, twiddle=twiddle)
+def fft_lds_fused_batch(x, elems: int = 0, twiddle=None, *, stagger: int = 0, stage: int = 0):
+    return _batched("fft_lds_fused_batch", x, None, {"elems": elems, "stagger": stagger, "stage": stage},
+                    twiddle=twiddle)
 
 
 def _four_step_params(n1, chunk_rows, schedule, allow_fused_schedule) -> dict:

@@ -115,3 +115,15 @@ def test_staged_refused_where_it_does_not_exist(gpu, n, elems, tt):
         native.NativePlan(n, 4, tt, td, "backward", native.FLOW_LDS_FUSED, (elems, 0, 1))
     with pytest.raises(ValueError, match="staged"):
         native.NativePlan(16, 4, "c2c", "forward", "backward", native.FLOW_LDS_FUSED, (4, 0, 2))
+
+
+def test_runner_keywords_reach_the_staged_form(gpu):
+    from kunlunxin_fft_amd import runner
+
+    x = torch.randn((1024, 32), dtype=torch.complex64, device=gpu, generator=torch.Generator(gpu).manual_seed(9))
+    ref = np.fft.fft(x.cpu().numpy().astype(np.complex128))
+    for kw in ({"stage": 1}, {"stage": 1, "stagger": 1}, {}):
+        y = runner.fft_lds_fused_batch(x, 4, **kw)
+        assert oracle.rel_l2(y.cpu().numpy(), ref) <= TOL, kw
+    y1 = runner.fft_lds_fused(x[0].contiguous(), 8, stage=1)
+    assert oracle.rel_l2(y1.cpu().numpy(), ref[0]) <= TOL
