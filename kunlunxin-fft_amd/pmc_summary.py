@@ -58,13 +58,22 @@ def _short(name: str) -> str:
 
 
 def _template_args(name: str):
+    """Integer template arguments of a kernel name (``true`` / ``false`` as
+    1 / 0), or None."""
     m = re.search(r"<([^<>]*)>", name)
     if not m:
         return None
-    try:
-        return [int(t.strip()) for t in m.group(1).split(",")]
-    except ValueError:
-        return None
+    out = []
+    for t in m.group(1).split(","):
+        t = t.strip()
+        if t in ("true", "false"):
+            out.append(int(t == "true"))
+            continue
+        try:
+            out.append(int(t))
+        except ValueError:
+            return None
+    return out
 
 
 def per_kernel(d: str, counter: str):
@@ -120,7 +129,7 @@ def real_keys(name: str, grid: int, real_sizes) -> list:
     for s in real_sizes:
         n, b, tt = s["n"], s["batch"], s["transform"]
         core = n // 2
-        if name.startswith("lds_fft_kernel") and t is not None and len(t) == 4 and s["flow"] == "lds-fused":
+        if name.startswith("lds_fft_kernel") and t is not None and len(t) in (4, 5) and s["flow"] == "lds-fused":
             logl, loge, mode = t[0], t[1], t[3]
             if (mode, tt) in ((1, "r2c"), (2, "c2r")) and core == (1 << logl) and (grid << loge) == core * b:
                 keys.append(f"{tt} lds_fft_kernel|N={n}|rows={b}")

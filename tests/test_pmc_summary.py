@@ -156,3 +156,22 @@ def test_execute_rows_sum_every_launch_of_one_execute():
     r = rows[("r2c", n)]
     assert r["launch_keys"] == ["r2c pass 1", "r2c pass 2", "r2c r2c_stitch_kernel"]
     assert r["hbm_bytes"] == 2 * (2 * 8 * (n // 2) * 2 * 32 + real_alg_bytes(n) * 32 // 2 * 3)
+
+
+def test_kernel_names_with_a_boolean_template_argument():
+    """The LDS kernel's names carry its staged flag (true / false) as a fifth
+    template argument; the size matching reads it as 1 / 0."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("_pmc_summary", SCRIPT)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    assert mod._template_args("lds_fft_kernel<10, 4, -1, 0, false>") == [10, 4, -1, 0, 0]
+    assert mod._template_args("lds_fft_kernel<4, 2, -1, 0, true>") == [4, 2, -1, 0, 1]
+    assert mod._template_args("foo<T, 3>") is None
+    sizes = [{"n": 1024, "batch": 32768, "flow": "lds-fused", "split": None}]
+    assert mod.bench_keys("lds_fft_kernel<10, 4, -1, 0, false>", 2097152, sizes) == \
+        ["lds_fft_kernel|N=1024|rows=32768"]
+    real = [{"n": 1024, "batch": 32768, "transform": "r2c", "flow": "lds-fused", "split": None}]
+    assert mod.real_keys("lds_fft_kernel<9, 4, -1, 1, false>", (512 * 32768) // 16, real) == \
+        ["r2c lds_fft_kernel|N=1024|rows=32768"]
