@@ -2,7 +2,7 @@
 
 Each case draws a runner (M0, M5, LDS, four-step), a transform type and
 direction, a norm, N, a ragged batch, and the runner's parameters (threads
-per block, elements per thread, start stagger, n1, chunk rows, schedule, pass-2
+per block, elements per thread, start stagger, staged form, n1, chunk rows, schedule, pass-2
 row order) from their published ranges (N <= 2^20), then checks the GPU result
 to the north-star gate (rel-L2 and peak-normalised worst element <= 1e-5).
 Sizes stay small enough (N * B <= 2^21) that the whole set runs in seconds.
@@ -28,8 +28,10 @@ FLOWS = (("fft_dit", 1, 16), ("fft_dif", 1, 16), ("fft_dit_radix4", 2, 16), ("ff
 
 def _cases(count=400, seed=20261202):
     rng = np.random.default_rng(seed)
+    stage_rng = np.random.default_rng(seed + 1)  # the LDS staged form, drawn apart from the rest
     out = []
     for i in range(count):
+        stage = int(stage_rng.integers(2))
         name, lo, hi = FLOWS[int(rng.integers(len(FLOWS)))]
         tt = ("c2c", "c2c", "r2c", "c2r")[int(rng.integers(4))]
         real = tt != "c2c"
@@ -43,6 +45,8 @@ def _cases(count=400, seed=20261202):
             block = (64, 128, 256, 512, 1024)[int(rng.integers(5))]
         elif name == "fft_lds_fused":
             params = {"elems": (0, 4, 8, 16, 32)[int(rng.integers(5))], "stagger": (0, 0, 1, 3)[int(rng.integers(4))]}
+            if stage:  # taken where fewer than 16 threads hold a transform, dropped elsewhere
+                params["stage"] = 1
         else:
             params = {"n1": (0, 16, 32, 64, 128, 256, 512, 1024)[int(rng.integers(8))],
                       "chunk_rows": (0, 0, 1, 2, 3, 5)[int(rng.integers(6))], "schedule": int(rng.integers(2)),
