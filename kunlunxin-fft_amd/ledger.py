@@ -65,8 +65,7 @@ _FLOW_FAMILY = {
     native.FLOW_DENSE_MFMA: ("dense-mfma", "one hbm read and write; fp32 matrix-core dot"),
 }
 
-MAX_LDS_CORE = 1 << 15       # the single-pass kernel's longest core
-MIN_FOUR_STEP_CORE = 1 << 8  # the four-step's shortest core
+MAX_LDS_CORE = 1 << 15  # the single-pass kernel's longest core
 
 
 def _sync() -> None:
@@ -240,12 +239,6 @@ def _real_ops(transform_type: str, n: int, batch: int, fused: bool, inverse: boo
     return ops
 
 
-def _scale_applies(transform_direction: str, norm: str) -> bool:
-    if norm == "ortho":
-        return True
-    return (norm == "forward") == (transform_direction == "forward") if norm in ("forward", "backward") else False
-
-
 def launch_ledger(plan) -> dict:
     """Analytic launches / HBM bytes / flops of one resolved plan
     (reference ledger.py:163-262).
@@ -293,7 +286,9 @@ def launch_ledger(plan) -> dict:
         gm = core_io + 2 * zrow
     else:
         gm = core_io
-    ops = _real_ops(ttype, n, batch, g["fused_real"], tdir == "inverse", _scale_applies(tdir, norm))
+    from .entry import norm_scale
+
+    ops = _real_ops(ttype, n, batch, g["fused_real"], tdir == "inverse", norm_scale(n, tdir, norm) != 1.0)
     gm += sum(o["in_bytes"] + o["out_bytes"] for o in ops)
     logc = g["logc"]
     flops = 5.0 * core * logc * batch + (10.0 * (core // 2 + 1) * batch if g["real"] else 0.0)
