@@ -38,7 +38,7 @@
  * execute.  `in` and `out` must not overlap; `in` is never written.
  * A plan is immutable after creation.  A plan that needs no workspace
  * (mfft_plan_workspace_size = 0: every LDS_FUSED plan and FOUR_STEP C2C with
- * schedule 0 or 1) can
+ * schedule 0, 1 or 3) can
  * be executed from any number of host threads and streams at once.  Executes
  * of a plan that needs workspace and overlap in time (two streams or two
  * host threads) share the plan's workspace and race: serialise them, give
@@ -119,8 +119,13 @@ enum {
  *                                    the workspace, which stays in that XCD's
  *                                    L2, and its pass 2 on the same XCD
  *                                    (n1, n2 in [128, 512] within 2x; the
- *                                    counters and the ring are workspace),
- *                        params[3] = schedules 0, 1: pass-2 row order: 0 =
+ *                                    counters and the ring are workspace);
+ *                                    3 = narrow: as 0 with four columns per
+ *                                    workgroup and at most 16 elements per
+ *                                    thread, four times the workgroups for
+ *                                    small batches (a real transform's
+ *                                    stitch then runs as its own launch),
+ *                        params[3] = schedules 0, 1, 3: pass-2 row order: 0 =
  *                                    forward; 1 = reverse, so the batch rows
  *                                    pass 1 wrote last (the most likely still
  *                                    in the MALL) are read first; schedule 2:
@@ -197,7 +202,7 @@ int mfft_execute(const mfft_plan* plan, const void* in, void* out, void* stream)
  * for real transforms whose core is not fused into the LDS kernel (one more
  * such buffer) and for the fused FOUR_STEP schedule (its launch counters and
  * its ring of XCDs x slots x core_n complex64); LDS_FUSED and FOUR_STEP C2C
- * with schedules 0 and 1 need none.
+ * with schedules 0, 1 and 3 need none.
  *
  * mfft_plan_create_ex: mfft_plan_create with `flags`; with
  * MFFT_PLAN_CALLER_WORKSPACE the plan allocates only its twiddle tables (and

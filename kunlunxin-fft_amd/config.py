@@ -151,8 +151,8 @@ class DesignSpace:
                  "butterfly_space.json: P.four_step.chunk_rows must be non-negative ints")
         _require(isinstance(fs.get("min_n"), int) and fs["min_n"] > 0, "butterfly_space.json: P.four_step.min_n required")
         sched = fs.get("schedule", [0])
-        _require(isinstance(sched, list) and sched and all(v in (0, 1, 2) for v in sched),
-                 "butterfly_space.json: P.four_step.schedule must be a list of 0/1/2")
+        _require(isinstance(sched, list) and sched and all(v in (0, 1, 2, 3) for v in sched),
+                 "butterfly_space.json: P.four_step.schedule must be a list of 0/1/2/3")
         order = fs.get("pass2_order", [0])
         _require(isinstance(order, list) and order and all(v in (0, 1) for v in order),
                  "butterfly_space.json: P.four_step.pass2_order must be a list of 0/1")

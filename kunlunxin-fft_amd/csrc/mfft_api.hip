@@ -443,8 +443,8 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
             n1 = (int64_t)1 << l1;
             n2 = (int64_t)1 << l2;
             chunk = prm[1] > 0 ? prm[1] : 0;
-            if (prm[2] < 0 || prm[2] > 2)
-                return fail(MFFT_ERR_VALUE, "FOUR_STEP schedule must be 0, 1 or 2, got %d", prm[2]);
+            if (prm[2] < 0 || prm[2] > 3)
+                return fail(MFFT_ERR_VALUE, "FOUR_STEP schedule must be 0, 1, 2 or 3, got %d", prm[2]);
             schedule = prm[2];
             if (schedule != 2 && (prm[3] < 0 || prm[3] > 1))
                 return fail(MFFT_ERR_VALUE, "FOUR_STEP pass-2 row order must be 0 or 1, got %d", prm[3]);
@@ -502,8 +502,8 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
                 break;
             }
             case MFFT_FLOW_FOUR_STEP: {
-                const int e1 = 1 << mfft::fourstep_col_loge(mfft::ilog2((int)n1));
-                const int e2 = 1 << mfft::fourstep_col_loge(mfft::ilog2((int)n2));
+                const int e1 = 1 << mfft::fourstep_col_loge(mfft::ilog2((int)n1), schedule);
+                const int e2 = 1 << mfft::fourstep_col_loge(mfft::ilog2((int)n2), schedule);
                 most(batch * (core_n / (e1 < e2 ? e1 : e2)) + 1024);
                 break;
             }
@@ -620,8 +620,8 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
         const int lc = logc;
         const int l1 = mfft::ilog2((int)n1), l2 = mfft::ilog2((int)n2);
         p->tw_h = (lc + 1) / 2;
-        if (rc == MFFT_OK) rc = put(&p->tw_n1, pass_table(l1, mfft::fourstep_col_loge(l1)));
-        if (rc == MFFT_OK) rc = put(&p->tw_n2, pass_table(l2, mfft::fourstep_col_loge(l2)));
+        if (rc == MFFT_OK) rc = put(&p->tw_n1, pass_table(l1, mfft::fourstep_col_loge(l1, schedule)));
+        if (rc == MFFT_OK) rc = put(&p->tw_n2, pass_table(l2, mfft::fourstep_col_loge(l2, schedule)));
         if (rc == MFFT_OK) rc = put(&p->tw_lo, roots(core_n, (int64_t)1 << p->tw_h, 1));
         if (rc == MFFT_OK) rc = put(&p->tw_hi, roots(core_n, core_n >> p->tw_h, (int64_t)1 << p->tw_h));
     } else if (rc == MFFT_OK && flow == MFFT_FLOW_LDS_FUSED) {

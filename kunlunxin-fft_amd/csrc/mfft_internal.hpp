@@ -149,7 +149,7 @@ constexpr int kFusedHead = kFusedSlots + 1;
 constexpr int kFusedFailMark = 1 << 20;  // added to a pass-1 count by a group that skipped its store
 constexpr int kFusedMaxRing = 64;        // Z slots per XCD
 int fourstep_fused_occupancy(int log2n1, int log2n2);  // resident blocks per CU of the fused kernel
-int fourstep_col_loge(int logl);  // log2 elements per thread of a pass of length 2^logl
+int fourstep_col_loge(int logl, int schedule);  // log2 elements per thread of a pass of length 2^logl
 void fourstep_default_split(int log2n, int* log2n1, int* log2n2);
 // fws: the fused schedule's scratch (counters, then the Z ring), or NULL for
 // the other schedules

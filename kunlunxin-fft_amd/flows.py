@@ -97,7 +97,7 @@ def flow_params(executed: str, n: int, transform_type: str, block, params: dict)
             l2 = core.bit_length() - 1 - l1
             if not (7 <= l1 <= 9 and 7 <= l2 <= 9 and abs(l1 - l2) <= 1):
                 sched = 0  # a real flow's half-length core outside the fused range
-        # params[3]: the pass-2 row order (schedules 0, 1), the queue lag (schedule 2)
+        # params[3]: the pass-2 row order (schedules 0, 1, 3), the queue lag (schedule 2)
         last = int(params.get("lag", 0)) if sched == 2 else int(params.get("pass2_order", 0))
         return flow, (n1, int(params.get("chunk_rows", 0)), sched, last)
     if kind == "block":

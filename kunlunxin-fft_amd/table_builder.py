@@ -8,8 +8,8 @@ design space (config/butterfly_space.json): the radix-4 global-stage flow,
 the dense-dot matrix-core flow (the reference's M2 FFT64 on fp32 MFMA), the
 single-pass LDS kernel at each elements-per-thread setting (and start
 stagger, where it can act), and the four-step at each split, chunking,
-schedule (one column group per workgroup, persistent workgroups, or both
-passes fused per XCD) and pass-2 row order.  The fastest challenger is promoted
+schedule (one column group per workgroup, persistent workgroups, or narrow
+4-column groups for small batches) and pass-2 row order.  The fastest challenger is promoted
 only when it beats the incumbent by at least GUARD_PCT percent (M0 closure);
 otherwise the cell keeps M0.  The table is bound to the device profile hash
 and the live environment fingerprint, so it selects only on the stack it was
@@ -282,6 +282,11 @@ def real_candidates(n: int, b: int, transform_type: str, space):
                         params["pass2_order"] = order
                     out.append((f"fs_n1_{n1}_c{ch}" + ("_r" if order else ""), "fft_four_step" + sfx, 256,
                                 params, ("four-step", "stockham-radix16", "four-step-two-pass")))
+                    # the narrow schedule, with the stitch / pre-twiddle as its own launch
+                    if 3 in space.fourstep_schedule:
+                        out.append((f"fsn_n1_{n1}_c{ch}" + ("_r" if order else ""), "fft_four_step" + sfx, 256,
+                                    dict(params, schedule=3),
+                                    ("four-step", "stockham-radix16", "four-step-two-pass")))
     return out
 
 
@@ -343,7 +348,7 @@ def candidates(n: int, b: int, direction: str, space):
                             params["schedule"] = sched
                         if order:
                             params["pass2_order"] = order
-                        out.append((f"{('fs', 'fsp', 'fsf')[sched]}_n1_{n1}_c{ch}" + ("_r" if order else ""),
+                        out.append((f"{('fs', 'fsp', 'fsf', 'fsn')[sched]}_n1_{n1}_c{ch}" + ("_r" if order else ""),
                                     "fft_four_step" + sfx, 256, params,
                                     ("four-step", "stockham-radix16", "four-step-two-pass")))
     return out

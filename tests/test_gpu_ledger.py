@@ -104,6 +104,8 @@ NATIVE_CASES = [
     ("fft_four_step_batch", 1 << 18, 8, {"schedule": 1, "chunk_rows": 3}, "r2c"),
     ("fft_four_step_batch", 1 << 18, 8, {"schedule": 1, "chunk_rows": 3}, "c2r"),
     ("fft_four_step_batch", 1 << 18, 8, {"schedule": 1}, "c2r"),
+    ("fft_four_step_batch", 1 << 20, 1, {"schedule": 3}, "c2c"),
+    ("fft_four_step_batch", 1 << 18, 8, {"schedule": 3, "chunk_rows": 3}, "r2c"),
     ("fft_dit_batch", 1024, 16, {}, "c2c"),
     ("fft_dif_batch", 4096, 4, {}, "r2c"),
     ("fft_dit_radix4_batch", 2048, 4, {}, "c2c"),

@@ -242,6 +242,45 @@ def test_four_step_persistent(gpu, n, n1, b, chunk):
     check(y, np_ref(x, td, norm), f"persistent four-step N={n} n1={n1} B={b} chunk={chunk} {td}")
 
 
+@pytest.mark.parametrize("n,n1", [(256, 16), (1 << 10, 32), (1 << 10, 64), (1 << 12, 64), (1 << 14, 128),
+                                  (1 << 15, 256), (1 << 16, 256), (1 << 17, 256), (1 << 17, 512),
+                                  (1 << 18, 512), (1 << 19, 512), (1 << 19, 1024), (1 << 20, 1024)])
+@pytest.mark.parametrize("b,chunk,rev", [(1, 0, 0), (5, 0, 1), (7, 3, 0), (64, 0, 0)])
+def test_four_step_narrow(gpu, n, n1, b, chunk, rev):
+    """Schedule 3: 4-column groups with at most 16 elements per thread (the
+    pass tables built for that), over ragged and chunked batches, both row
+    orders of pass 2, both directions."""
+    if n >= (1 << 18):
+        b = min(b, 3)
+    x = seeded_c64(n, b, session=5)
+    td = "inverse" if rev else "forward"
+    norm = "ortho" if chunk == 3 else "backward"
+    plan = mkplan("fft_four_step_batch" if b > 1 else "fft_four_step", n, b, td=td, norm=norm,
+                  params={"n1": n1, "chunk_rows": chunk, "schedule": 3, "pass2_order": rev})
+    y = execute_fft_plan(plan, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    check(y, np_ref(x, td, norm), f"narrow four-step N={n} n1={n1} B={b} chunk={chunk} rev={rev} {td}")
+
+
+@pytest.mark.parametrize("tt", ["r2c", "c2r"])
+@pytest.mark.parametrize("n,b,chunk", [(1 << 17, 1, 0), (1 << 20, 2, 0), (1 << 18, 5, 2), (4096, 3, 0)])
+def test_four_step_narrow_real(gpu, tt, n, b, chunk):
+    """Schedule 3 under a real transform: the half-length core on the narrow
+    passes, the stitch / pre-twiddle as its own launch (chunk by chunk when
+    chunked)."""
+    plan = mkplan("fft_four_step_batch" if b > 1 else "fft_four_step", n, b, tt=tt,
+                  td="inverse" if tt == "c2r" else "forward", params={"chunk_rows": chunk, "schedule": 3})
+    if tt == "r2c":
+        r = seeded_f32(n, b, session=6)
+        y = execute_fft_plan(plan, torch.from_numpy(r).to(gpu)).cpu().numpy()
+        check(y, np.fft.rfft(r.astype(np.float64)), f"narrow r2c N={n} B={b} chunk={chunk}")
+    else:
+        rng = np.random.default_rng(n + b)
+        h = (rng.standard_normal((b, n // 2 + 1)) + 1j * rng.standard_normal((b, n // 2 + 1))).astype(np.complex64)
+        h = h[0] if b == 1 else h
+        y = execute_fft_plan(plan, torch.from_numpy(h).to(gpu)).cpu().numpy()
+        check(y, np.fft.irfft(h.astype(np.complex128), n=n), f"narrow c2r N={n} B={b} chunk={chunk}")
+
+
 FUSED_SPLITS = [(1 << 14, 128), (1 << 15, 128), (1 << 15, 256), (1 << 16, 256), (1 << 17, 256),
                 (1 << 17, 512), (1 << 18, 512)]
 
@@ -322,7 +361,7 @@ def test_four_step_fused_range(gpu):
     p = native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 2))
     assert p.info.n1 == 256 and p.info.launches == 2 and p.sync_overruns() == 0
     with pytest.raises(ValueError, match="schedule"):
-        native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 3))
+        native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 4))
     with pytest.raises(ValueError, match="lag"):
         native.NativePlan(1 << 16, 2, "c2c", "forward", "backward", native.FLOW_FOUR_STEP, (256, 0, 2, 65))
     with pytest.raises(ValueError, match="dequeue"):

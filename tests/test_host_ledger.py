@@ -151,6 +151,9 @@ def test_real_four_step_schedules():
     lg = ledger.launch_ledger(plan("fft_four_step_batch", n, b, {"schedule": 1, "chunk_rows": 16},
                                    transform_type="c2r", transform_direction="inverse"))
     assert (lg["core_launches"], lg["epilogue_launches"]) == (8, 4)
+    # schedule 3 (narrow groups): the stitch as its own launch too
+    lg = ledger.launch_ledger(plan("fft_four_step_batch", n, b, {"schedule": 3}, transform_type="r2c"))
+    assert (lg["core_launches"], lg["epilogue_launches"]) == (2, 1) and lg["schedule"] == 3
     # schedule 1 unchunked: one epilogue launch
     lg = ledger.launch_ledger(plan("fft_four_step_batch", n, b, {"schedule": 1}, transform_type="r2c"))
     assert (lg["core_launches"], lg["epilogue_launches"]) == (2, 1)
