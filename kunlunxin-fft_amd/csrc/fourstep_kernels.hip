@@ -35,11 +35,13 @@ namespace mfft {
 constexpr int col_loge(int logl) { return logl >= 9 ? 5 : (logl >= 8 ? 4 : (logl >= 6 ? 3 : 2)); }
 constexpr int col_logc(int) { return 4; }
 // Schedule 3 (narrow groups, for a batch of one or a few transforms): 4
-// columns per workgroup and at most 16 elements per thread, so a launch
-// has 4x the workgroups and every thread a shorter load-compute-store
-// chain; its 32-byte row runs cost bandwidth that such a launch does not
-// use anyway (N = 2^18-2^20, B = 1: 25-28% less time than schedule 0).
-constexpr int col_loge_narrow(int logl) { return logl >= 9 ? 4 : col_loge(logl); }
+// columns per workgroup and at most 16 elements per thread (8 for passes of
+// 256 and 512 points), so a launch has 4x the workgroups and every thread a
+// shorter load-compute-store chain; its 32-byte row runs cost bandwidth that
+// such a launch does not use anyway (N = 2^18-2^20, B = 1: 25-28% less time
+// than schedule 0).  Measured per pass length: 8 elements beat 16 by 5-7% at
+// 256 and 512 points and lose 2-3% at 1024; 2 columns per workgroup lose.
+constexpr int col_loge_narrow(int logl) { return logl >= 10 ? 4 : (logl >= 8 ? 3 : col_loge(logl)); }
 constexpr int kNarrowLogC = 2;
 int fourstep_col_loge(int logl, int schedule) { return schedule == 3 ? col_loge_narrow(logl) : col_loge(logl); }
 
