@@ -2,8 +2,8 @@
 
 Each case draws a runner (M0, M5, LDS, four-step), a transform type and
 direction, a norm, N, a ragged batch, and the runner's parameters (threads
-per block, elements per thread, start stagger, staged form, n1, chunk rows, schedule, pass-2
-row order) from their published ranges (N <= 2^20), then checks the GPU result
+per block, elements per thread, start stagger, staged form, n1, chunk rows, schedule 0, 1 or 3,
+pass-2 row order) from their published ranges (N <= 2^20), then checks the GPU result
 to the north-star gate (rel-L2 and peak-normalised worst element <= 1e-5).
 Sizes stay small enough (N * B <= 2^21) that the whole set runs in seconds.
 A second set drives the real LDS modes through the C ABI with an explicit
@@ -29,9 +29,11 @@ FLOWS = (("fft_dit", 1, 16), ("fft_dif", 1, 16), ("fft_dit_radix4", 2, 16), ("ff
 def _cases(count=400, seed=20261202):
     rng = np.random.default_rng(seed)
     stage_rng = np.random.default_rng(seed + 1)  # the LDS staged form, drawn apart from the rest
+    narrow_rng = np.random.default_rng(seed + 2)  # the narrow four-step schedule, likewise
     out = []
     for i in range(count):
         stage = int(stage_rng.integers(2))
+        narrow = int(narrow_rng.integers(3)) == 0
         name, lo, hi = FLOWS[int(rng.integers(len(FLOWS)))]
         tt = ("c2c", "c2c", "r2c", "c2r")[int(rng.integers(4))]
         real = tt != "c2c"
@@ -51,6 +53,8 @@ def _cases(count=400, seed=20261202):
             params = {"n1": (0, 16, 32, 64, 128, 256, 512, 1024)[int(rng.integers(8))],
                       "chunk_rows": (0, 0, 1, 2, 3, 5)[int(rng.integers(6))], "schedule": int(rng.integers(2)),
                       "pass2_order": int(rng.integers(2))}
+            if narrow:
+                params["schedule"] = 3
         out.append(pytest.param(i, name, tt, td, norm, 1 << logn, b, block, params,
                                 id=f"{i}-{name}-{tt}-{td}-{norm}-N{1 << logn}-B{b}"))
     return out

@@ -37,6 +37,10 @@ PAIRS = [
     # the fused schedule (params[2] = 2): counters + Z ring in the static buffer
     ((1 << 16, 8, "c2c", "forward", native.FLOW_FOUR_STEP, (256, 0, 2, FUSED_WORD)),
      (1 << 15, 3, "c2c", "inverse", native.FLOW_FOUR_STEP, (128, 0, 2, FUSED_WORD))),
+    # the narrow schedule (params[2] = 3): a real transform's pre-twiddle
+    # runs as its own launch, out of the static buffer
+    ((1 << 18, 2, "c2r", "inverse", native.FLOW_FOUR_STEP, (0, 0, 3)),
+     (1 << 16, 1, "c2r", "inverse", native.FLOW_FOUR_STEP, (0, 0, 3))),
 ]
 
 
@@ -75,6 +79,7 @@ GRAPH_CASES = [
     (4096, 16, "c2c", "forward", native.FLOW_RADIX2_DIT, (256,)),
     (1 << 17, 2, "r2c", "forward", native.FLOW_FOUR_STEP, (256,)),
     (1 << 16, 4, "c2c", "forward", native.FLOW_FOUR_STEP, (256, 0, 2, FUSED_WORD)),
+    (1 << 18, 1, "r2c", "forward", native.FLOW_FOUR_STEP, (0, 0, 3)),
 ]
 
 
