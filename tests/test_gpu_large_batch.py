@@ -32,6 +32,8 @@ CASES = [
     ("fourstep-c2c-chunked-rev", 1 << 20, (1 << 11) + 1, "c2c", "forward", native.FLOW_FOUR_STEP,
      (1024, 1000, 0, 1)),
     ("fourstep-c2c-persistent", 1 << 17, (1 << 14) + 5, "c2c", "forward", native.FLOW_FOUR_STEP, (256, 0, 1, 0)),
+    ("fourstep-c2c-narrow", 1 << 20, (1 << 11) + 1, "c2c", "inverse", native.FLOW_FOUR_STEP, (1024, 0, 3, 1)),
+    ("fourstep-c2r-narrow", 1 << 20, (1 << 12) + 1, "c2r", "inverse", native.FLOW_FOUR_STEP, (512, 0, 3, 0)),
     ("fourstep-r2c", 1 << 20, (1 << 12) + 1, "r2c", "forward", native.FLOW_FOUR_STEP, (1024, 0, 0, 0)),
     ("fourstep-c2r", 1 << 20, (1 << 12) + 1, "c2r", "inverse", native.FLOW_FOUR_STEP, (512, 0, 0, 0)),
     ("radix4-dit", 1 << 16, (1 << 15) + 1, "c2c", "forward", native.FLOW_RADIX4_DIT, ()),
