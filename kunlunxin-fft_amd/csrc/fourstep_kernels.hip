@@ -385,10 +385,10 @@ __device__ __forceinline__ void col_store(const float2 (&v)[C::E], float2* d, fl
                 const int k1 = e & (C::L - 1);
                 if constexpr (MAP == 2) {
                     const int col = pair_col<C::C / 2>(g, h.value * CH + cc, 1 << log_s);
-                    d[((int64_t)col << C::LOG_L) + k1] = lds[cc * C::PITCH + pad(k1)];
+                    store_out<true>(d + ((int64_t)col << C::LOG_L) + k1, lds[cc * C::PITCH + pad(k1)]);
                 } else {
-                    *byte_off(dh + r.value * C::WG, (uint32_t)tid * 8u) =
-                        lds[cc * C::PITCH + pad(MAP == 1 ? pair_k1<C::L, CP>(k1) : k1)];
+                    store_out<true>(byte_off(dh + r.value * C::WG, (uint32_t)tid * 8u),
+                                    lds[cc * C::PITCH + pad(MAP == 1 ? pair_k1<C::L, CP>(k1) : k1)]);
                 }
             });
         });
@@ -400,7 +400,7 @@ __device__ __forceinline__ void col_store(const float2 (&v)[C::E], float2* d, fl
                 float2* a = byte_off(d + ((int64_t)row << log_s), lane);
                 const float2 x = cscale(v[m.value * C::R_LAST + q.value], scale);
                 if constexpr (NTS) store_nt(a, x);
-                else *a = x;
+                else store_out<true>(a, x);
             });
         });
     }
