@@ -399,8 +399,11 @@ __device__ __forceinline__ void col_store(const float2 (&v)[C::E], float2* d, fl
                 const int row = m.value * C::T + q.value * C::NS_LAST;
                 float2* a = byte_off(d + ((int64_t)row << log_s), lane);
                 const float2 x = cscale(v[m.value * C::R_LAST + q.value], scale);
+                // write-through where a row run is a whole 128-byte line (16
+                // columns or more; the narrow groups' 32-byte runs, written
+                // through, took the 2^20-point pass 2 from 7.4 to 9.8 us)
                 if constexpr (NTS) store_nt(a, x);
-                else store_out<true>(a, x);
+                else store_out<(C::C >= 16)>(a, x);
             });
         });
     }

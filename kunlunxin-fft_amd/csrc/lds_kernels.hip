@@ -143,13 +143,17 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
     // rows of L + 1 bins (R2C output, C2R input) of the staged form, flat in LDS
     static_assert(!STAGED || C::TPB * (L + 1) <= (C::LDS_FLOATS / 2), "staged bin rows exceed the LDS rows");
     constexpr bool NEED_LDS = (P > 1) || (MODE == 1) || STAGED;
-    // write-through output stores (store_out) for C2C up to 2^13 points.
-    // Measured over the benchmark's cycles: C2C 2.5% less time in all; at
-    // 2^14 and 2^15 the kernel itself is 2-3% slower with them; C2R's real
-    // rows gain by themselves but the transform after them (R2C, whose bin
-    // rows of L + 1 values are not line-aligned and take partial-line
-    // writes) loses more, so both real modes keep plain stores.
-    constexpr bool WT = MODE == 0 && LOGL <= 13;
+    // write-through output stores (store_out) for C2C up to 2^13 points,
+    // where every store instruction writes whole 128-byte lines: the staged
+    // form, or 16 or more threads per transform (with fewer, the direct
+    // stores are 8-64-byte pieces of lines, and written through one by one
+    // they took N = 16 from 126 to 158 us per 256 MiB).  Measured over the
+    // benchmark's cycles: C2C 2.5% less time in all; at 2^14 and 2^15 the
+    // kernel itself is 2-3% slower with them; C2R's real rows gain by
+    // themselves but the transform after them (R2C, whose bin rows of L + 1
+    // values are not line-aligned and take partial-line writes) loses more,
+    // so both real modes keep plain stores.
+    constexpr bool WT = MODE == 0 && LOGL <= 13 && (STAGED || T >= 16);
     static_assert(!(C::SPLIT && MODE == 1 && C::LE != 5 && !C::PAIR),
                   "16-element r2c kernels without lane pairing stitch whole complex values out of LDS");
     __shared__ float2 lds_raw[NEED_LDS ? (C::LDS_FLOATS + 1) / 2 : 1];
