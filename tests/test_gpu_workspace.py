@@ -134,7 +134,9 @@ def test_caller_workspace_two_streams(gpu):
         assert oracle.rel_l2(y.cpu().numpy(), ref) <= TOL
 
 
-@pytest.mark.parametrize("flow,params,n", [(native.FLOW_LDS_FUSED, (), 4096), (native.FLOW_FOUR_STEP, (256,), 1 << 16)])
+@pytest.mark.parametrize("flow,params,n", [(native.FLOW_LDS_FUSED, (), 4096), (native.FLOW_FOUR_STEP, (256,), 1 << 16),
+                                           (native.FLOW_FOUR_STEP, (0, 0, 1), 1 << 17),
+                                           (native.FLOW_FOUR_STEP, (0, 0, 3), 1 << 18)])
 def test_no_workspace_plan_two_streams(gpu, flow, params, n):
     """A plan that needs no workspace holds nothing an execute writes, so two
     streams may run it at once."""
