@@ -58,10 +58,17 @@ C5_BATCHES = [1, 16, 64, 256]
 ROOF_SIZES = [1 << k for k in range(10, 21)]      # roofline rows: B = max(64, 2^25/N)
 EXTRA_CELLS = [(1 << k, 1) for k in range(15, 21)] + [(1 << 16, 256), (256, 1), (4096, 64)]
 # Every power-of-two batch of every power-of-two N from 16 to 2^20, up to
-# 2^27 elements (1 GiB of complex64 per buffer): the table answers exact
+# 2^30 elements (8 GiB of complex64 per buffer): the table answers exact
 # (N, batch) keys only, and a shape it does not hold runs the radix-2
 # baseline, one launch per stage (at N = 2^20, B = 2, 7x the four-step's time).
-DENSE_MAX_LOG_ELEMS = 27
+DENSE_MAX_LOG_ELEMS = 30
+# Above 2^27 elements a cell times the M0 incumbent and only the PRUNE_KEEP
+# fastest challengers of the same N (and direction or real semantic) at
+# 2^27 elements: every launch there streams whole waves of workgroups, so
+# the ranking of the 2^27 cell holds, and timing every challenger at up to
+# 8 GiB per buffer would take most of an hour.  These cells are built last.
+PRUNE_LOG_ELEMS = 27
+PRUNE_KEEP = 3
 DENSE_LOG_N = range(4, 21)
 # real transforms, default norm: exact-semantic entries at the roofline rows
 # (the LDS kernel's real modes and the four-step around a half-length core
@@ -215,8 +222,53 @@ def real_cells():
     """(N, batch) of the exact-semantic real entries: the roofline rows'
     batch and twice it (the same bytes per launch as the C2C row, which
     bench.py's real rows use), then every dense cell."""
-    return _unique([(n, b) for n in ROOF_SIZES for b in (max(64, (1 << 25) // n), 2 * max(64, (1 << 25) // n))]
-                   + dense_cells())
+    return _large_last(_unique([(n, b) for n in ROOF_SIZES for b in (max(64, (1 << 25) // n),
+                                                                     2 * max(64, (1 << 25) // n))]
+                               + dense_cells()))
+
+
+def _large_last(cells_):
+    """The cells above 2^PRUNE_LOG_ELEMS elements after all the others (their
+    challengers come from the 2^PRUNE_LOG_ELEMS cell of the same N)."""
+    big = lambda c: c[0] * c[1] > (1 << PRUNE_LOG_ELEMS)
+    return [c for c in cells_ if not big(c)] + [c for c in cells_ if big(c)]
+
+
+def pruned(cands, n: int, b: int, key, top: dict):
+    """The challengers to time in cell (n, b): all of them up to
+    2^PRUNE_LOG_ELEMS elements; above, those among the PRUNE_KEEP fastest
+    that top[key] recorded at 2^PRUNE_LOG_ELEMS (all when none is recorded)."""
+    keep = top.get(key)
+    if n * b <= (1 << PRUNE_LOG_ELEMS) or not keep:
+        return list(cands)
+    return [c for c in cands if c[0] in keep]
+
+
+def guard_gain(inc_ms: float, best) -> float:
+    """Percent by which the best challenger beats the M0 incumbent; 100 when
+    the library refuses M0 at this shape (inc_ms infinite), -1 with no
+    challenger."""
+    if best is None or not math.isfinite(best[0]):
+        return -1.0
+    if not math.isfinite(inc_ms):
+        return 100.0
+    return (inc_ms - best[0]) / inc_ms * 100.0
+
+
+def _ms(ms: float):
+    """A timing for the sweep record: rounded, or None for a refused plan."""
+    return round(ms, 5) if math.isfinite(ms) else None
+
+
+def _fmt(ms) -> str:
+    return "refused" if ms is None else f"{ms:.4f}"
+
+
+def record_top(timed, n: int, b: int, key, top: dict) -> None:
+    """At 2^PRUNE_LOG_ELEMS elements, remember the PRUNE_KEEP fastest labels."""
+    ok = [t for t in timed if math.isfinite(t[0])]
+    if n * b == (1 << PRUNE_LOG_ELEMS) and ok:
+        top[key] = [t[1] for t in sorted(ok, key=lambda t: t[0])[:PRUNE_KEEP]]
 
 
 def cells(quick: bool = False):
@@ -227,7 +279,7 @@ def cells(quick: bool = False):
     for n in ROOF_SIZES:
         out.append((n, max(64, (1 << 25) // n)))
     out += EXTRA_CELLS
-    uniq = _unique(out + dense_cells())
+    uniq = _large_last(_unique(out + dense_cells()))
     if quick:
         uniq = [c for c in uniq if c[0] * c[1] <= (1 << 22) or c[1] == 1]
     return uniq
@@ -398,7 +450,13 @@ def main() -> int:
     flush = torch.empty(1 << 26, dtype=torch.float32, device=dev)  # 256 MiB
 
     def time_runner(name, n, b, block, params, x, tt="c2c", td="forward"):
-        np_ = get_native_plan(name, n, b, tt, td, "backward", block, params, 0)
+        try:
+            np_ = get_native_plan(name, n, b, tt, td, "backward", block, params, 0)
+        except ValueError as exc:
+            # a plan the library refuses for this shape (a launch past one
+            # dispatch's 2^32 work-items): not a candidate here
+            print(f"  {name} {params} refused at N={n} B={b} {tt}: {exc}", flush=True)
+            return math.inf
         shape, dt = output_spec(tt, n, b)
         out = torch.empty(shape, dtype=dt, device=dev)
         ws = workspace_for(np_, dev)
@@ -433,9 +491,9 @@ def main() -> int:
         times each, and the lower median of those re-timings decides (one
         noisy median in a launch-bound cell must not pick a kernel that is
         slower on average).  The re-timings are recorded in the sweep row."""
+        timed = sorted((t for t in timed if math.isfinite(t[0])), key=lambda t: t[0])
         if not timed:
             return None
-        timed = sorted(timed, key=lambda t: t[0])
         if len(timed) < 2 or timed[1][0] > timed[0][0] * (1 + CONFIRM_PCT / 100.0):
             return timed[0]
         again = {0: [], 1: []}
@@ -449,6 +507,7 @@ def main() -> int:
         return (med[w],) + tuple(timed[w][1:])
 
     entries, sweep = [], []
+    top = {}  # (n, direction or transform type) -> fastest labels at 2^PRUNE_LOG_ELEMS
     t_start = time.time()
     for (n, b) in cells(args.quick):
         shape = (n,) if b == 1 else (b, n)
@@ -456,15 +515,18 @@ def main() -> int:
         for direction in ("dit", "dif"):
             inc_name = ("fft_dit" if direction == "dit" else "fft_dif") + ("" if b == 1 else "_batch")
             inc_ms = time_runner(inc_name, n, b, 256, {}, x) if n >= 2 else float("inf")
-            row = {"N": n, "batch": b, "direction": direction, f"m0_{direction}@256": round(inc_ms, 5)}
+            row = {"N": n, "batch": b, "direction": direction, f"m0_{direction}@256": _ms(inc_ms)}
             timed = []
-            for label, name, block, params, fam in candidates(n, b, direction, space):
+            for label, name, block, params, fam in pruned(candidates(n, b, direction, space), n, b,
+                                                          (n, direction), top):
                 ms = time_runner(name, n, b, block, params, x)
-                row[label] = round(ms, 5)
+                row[label] = _ms(ms)
                 timed.append((ms, label, name, block, params, fam))
+            record_top(timed, n, b, (n, direction), top)
             best = confirm(timed, n, b, x, row)
             sweep.append(row)
-            gain = (inc_ms - best[0]) / inc_ms * 100.0 if best else -1.0
+            gain = guard_gain(inc_ms, best)
+            inc_ms = inc_ms if math.isfinite(inc_ms) else None
             if best is not None and gain >= GUARD_PCT:
                 ms, label, name, block, params, (real, unit, flow_id) = best
                 entry = {"N": n, "batch": b, "direction": direction, "incumbent_ms": inc_ms,
@@ -488,7 +550,7 @@ def main() -> int:
             if b > 1:
                 entry["params"]["variant"] = "folded"
             entries.append(entry)
-            print(f"N={n:>8} B={b:>6} {direction}: M0 {inc_ms:.4f} ms, best {best[1] if best else '-'} "
+            print(f"N={n:>8} B={b:>6} {direction}: M0 {_fmt(inc_ms)} ms, best {best[1] if best else '-'} "
                   f"{best[0] if best else float('nan'):.4f} ms ({gain:+.1f}%) -> {entry['executed']} "
                   f"[{time.time() - t_start:.0f}s]", flush=True)
         del x
@@ -501,15 +563,17 @@ def main() -> int:
                 x = torch.randn((b, n // 2 + 1), dtype=torch.complex64, device=dev, generator=gen)
             inc_name = "fft_dit" if b == 1 else "fft_dit_batch"
             inc_ms = time_runner(inc_name, n, b, 256, {}, x, tt, td)
-            row = {"N": n, "batch": b, "direction": "dit", "transform_type": tt, "m0_dit@256": round(inc_ms, 5)}
+            row = {"N": n, "batch": b, "direction": "dit", "transform_type": tt, "m0_dit@256": _ms(inc_ms)}
             timed = []
-            for label, name, block, params, fam in real_candidates(n, b, tt, space):
+            for label, name, block, params, fam in pruned(real_candidates(n, b, tt, space), n, b, (n, tt), top):
                 ms = time_runner(name, n, b, block, params, x, tt, td)
-                row[label] = round(ms, 5)
+                row[label] = _ms(ms)
                 timed.append((ms, label, name, block, params, fam))
+            record_top(timed, n, b, (n, tt), top)
             best = confirm(timed, n, b, x, row, tt, td)
             sweep.append(row)
-            gain = (inc_ms - best[0]) / inc_ms * 100.0 if best else -1.0
+            gain = guard_gain(inc_ms, best)
+            inc_ms = inc_ms if math.isfinite(inc_ms) else None
             sem = {"transform_type": tt, "transform_direction": td, "normalization": REAL_NORM}
             if best is not None and gain >= GUARD_PCT:
                 ms, label, name, block, params, (real, unit, flow_id) = best
@@ -523,7 +587,7 @@ def main() -> int:
                 if b > 1:
                     entry["params"]["variant"] = "folded"
                 entries.append(entry)
-            print(f"{tt} N={n:>8} B={b:>6}: M0 {inc_ms:.4f} ms, best {best[1] if best else '-'} "
+            print(f"{tt} N={n:>8} B={b:>6}: M0 {_fmt(inc_ms)} ms, best {best[1] if best else '-'} "
                   f"{best[0] if best else float('nan'):.4f} ms ({gain:+.1f}%) [{time.time() - t_start:.0f}s]",
                   flush=True)
             del x
@@ -539,7 +603,8 @@ def main() -> int:
                                "forward C2C complex64 (legacy entries, answering every semantic), plus "
                                "exact-semantic R2C / C2R entries (norm backward); cells: the reference's "
                                "config-5 sweep, the roofline rows and every power-of-two batch of every "
-                               "power-of-two N = 16 .. 2^20 up to 2^27 elements",
+                               "power-of-two N = 16 .. 2^20 up to 2^30 elements (above 2^27: the M0 "
+                               "incumbent and the 3 fastest challengers of the same N at 2^27)",
         "sources": ["kunlunxin-fft_amd/table_builder.py live sweep"],
         "entries": entries, "previous_fallbacks": [],
     }
