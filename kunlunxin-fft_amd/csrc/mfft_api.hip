@@ -514,9 +514,10 @@ int mfft_plan_create_ex(mfft_plan** out, int64_t n, int64_t batch, int transform
                 most(batch * (core_n >> 1) + block);
         }
         // a real transform whose core does not carry the stitch / pre-twiddle
-        // runs it as its own launch: 256 threads per 512 bins of a row
+        // runs it as its own launch: one thread per mirror pair, core/2 + 1
+        // a row, over the flat batch
         const bool real_fused = flow == MFFT_FLOW_LDS_FUSED || (flow == MFFT_FLOW_FOUR_STEP && schedule == 0);
-        if (real && !real_fused) most(batch * ((((core_n >> 1) + 1 + 255) / 256) * 256));
+        if (real && !real_fused) most(batch * ((core_n >> 1) + 1) + 256);
         if (items > mfft::kMaxLaunchItems)
             return fail(MFFT_ERR_UNSUPPORTED,
                         "batch=%lld of n=%lld: a launch of this flow would run %lld work-items, above the "

@@ -159,15 +159,19 @@ __global__ void bitrev_kernel(const float2* __restrict__ x, float2* __restrict__
 // One thread per mirror pair (k, np-k), k in [0, np/2]: bin np-k takes the
 // same two core outputs with their roles swapped, so every core output is
 // read once (non-temporal: it is not read again).  Pair 0 also writes bin
-// np (both from Z[0]); pair np/2 is one bin.  A block covers 256 pairs of
-// one row (bpr blocks per row), so the row is a per-block quotient.
+// np (both from Z[0]); pair np/2 is one bin.  The pairs of the whole batch
+// are one flat range, np/2 + 1 per row (a launch holds fewer than 2^32, so
+// the row is a 32-bit quotient): short rows share a block instead of each
+// taking one (N = 16: 5 pairs a row, not 256 threads).
 __global__ __launch_bounds__(256) void r2c_stitch_kernel(const float2* __restrict__ z, float2* __restrict__ x,
-                                                         const float2* __restrict__ tw_real, int64_t np, int bpr,
-                                                         float scale) {
-    const int row = (int)(blockIdx.x / (unsigned)bpr);
-    const int64_t k = (int64_t)(blockIdx.x - (unsigned)row * (unsigned)bpr) * 256 + threadIdx.x;
+                                                         const float2* __restrict__ tw_real, int64_t np,
+                                                         uint32_t total, float scale) {
+    const uint32_t g = blockIdx.x * 256u + threadIdx.x;
+    if (g >= total) return;
     const int64_t half = np >> 1;
-    if (k > half) return;
+    const uint32_t pairs = (uint32_t)half + 1u;
+    const uint32_t row = g / pairs;
+    const int64_t k = g - row * pairs;
     const float2* zr = z + (int64_t)row * np;
     float2* xr = x + (int64_t)row * (np + 1);
     const int64_t j = (np - k) & (np - 1);
@@ -182,13 +186,16 @@ __global__ __launch_bounds__(256) void r2c_stitch_kernel(const float2* __restric
 // a = (X[k] + conj X[j])/2, c = (X[k] - conj X[j])/2, j = np-k,
 // w' = exp(+2*pi*i*k/n); imaginary parts of bins 0 and np are ignored.
 // Paired like the stitch: thread k in [0, np/2] reads X[k] and X[np-k] once
-// and writes Z[k] and Z[np-k] (pair 0 only Z[0]; pair np/2 one value).
+// and writes Z[k] and Z[np-k] (pair 0 only Z[0]; pair np/2 one value), over
+// the same flat range of pairs as the stitch.
 __global__ __launch_bounds__(256) void c2r_pre_kernel(const float2* __restrict__ x, float2* __restrict__ z,
-                                                      const float2* __restrict__ tw_real, int64_t np, int bpr) {
-    const int row = (int)(blockIdx.x / (unsigned)bpr);
-    const int64_t k = (int64_t)(blockIdx.x - (unsigned)row * (unsigned)bpr) * 256 + threadIdx.x;
+                                                      const float2* __restrict__ tw_real, int64_t np, uint32_t total) {
+    const uint32_t g = blockIdx.x * 256u + threadIdx.x;
+    if (g >= total) return;
     const int64_t half = np >> 1;
-    if (k > half) return;
+    const uint32_t pairs = (uint32_t)half + 1u;
+    const uint32_t row = g / pairs;
+    const int64_t k = g - row * pairs;
     const float2* xr = x + (int64_t)row * (np + 1);
     float2* zr = z + (int64_t)row * np;
     float2 xk = load_nt(xr + k);
@@ -483,9 +490,11 @@ hipError_t launch_twiddle_transpose(int dir, const float2* s, float2* g, int64_t
 hipError_t launch_r2c_stitch(const float2* z, float2* x, const float2* tw_real, int64_t n,
                              int64_t rows, float scale, hipStream_t stream) {
     const int64_t np = n >> 1;
-    const int bpr = (int)(((np >> 1) + 1 + 255) / 256);  // blocks per row: pairs k in [0, np/2]
-    if (!launch_fits((int64_t)bpr * rows, 256)) return hipErrorInvalidConfiguration;
-    r2c_stitch_kernel<<<(unsigned)(bpr * rows), 256, 0, stream>>>(z, x, tw_real, np, bpr, scale);
+    const int64_t total = rows * ((np >> 1) + 1);  // pairs k in [0, np/2] of every row
+    if (total <= 0) return hipSuccess;
+    if (!launch_fits((total + 255) / 256, 256)) return hipErrorInvalidConfiguration;
+    r2c_stitch_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(z, x, tw_real, np, (uint32_t)total,
+                                                                           scale);
     mark(stream);
     return hipGetLastError();
 }
@@ -493,9 +502,10 @@ hipError_t launch_r2c_stitch(const float2* z, float2* x, const float2* tw_real, 
 hipError_t launch_c2r_pre(const float2* x, float2* z, const float2* tw_real, int64_t n,
                           int64_t rows, hipStream_t stream) {
     const int64_t np = n >> 1;
-    const int bpr = (int)(((np >> 1) + 1 + 255) / 256);
-    if (!launch_fits((int64_t)bpr * rows, 256)) return hipErrorInvalidConfiguration;
-    c2r_pre_kernel<<<(unsigned)(bpr * rows), 256, 0, stream>>>(x, z, tw_real, np, bpr);
+    const int64_t total = rows * ((np >> 1) + 1);
+    if (total <= 0) return hipSuccess;
+    if (!launch_fits((total + 255) / 256, 256)) return hipErrorInvalidConfiguration;
+    c2r_pre_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(x, z, tw_real, np, (uint32_t)total);
     mark(stream);
     return hipGetLastError();
 }

@@ -741,6 +741,32 @@ def test_input_validation_raises_before_launch(gpu):
         fft_dit(torch.ones(12, dtype=torch.complex64, device=gpu))
 
 
+@pytest.mark.parametrize("tt", ["r2c", "c2r"])
+def test_real_fallback_for_a_huge_odd_batch_of_short_rows(gpu, tt):
+    """A batch that is not a power of two runs M0 (the table answers exact
+    keys); its real stitch / pre-twiddle runs one thread per mirror pair over
+    the flat batch, so N = 16 at B = 3 * 2^23 + 1 (past 2^24 rows, where a
+    block per row would need more than one dispatch's 2^32 work-items) plans
+    and matches numpy on the first, a middle and the last rows."""
+    n, b = 16, 3 * (1 << 23) + 1
+    td = "inverse" if tt == "c2r" else "forward"
+    plan = plan_fft("dit", n, batch=b, transform_type=tt, transform_direction=td,
+                    profile_hash=DeviceProfile.load().hash())
+    assert plan.fallback and plan.executed == "fft_dit_batch", plan.reason
+    print(f"huge odd batch {tt}: N={n} B={b}", flush=True)
+    g = torch.Generator(gpu).manual_seed(11)
+    if tt == "r2c":
+        x = torch.randn((b, n), dtype=torch.float32, device=gpu, generator=g)
+    else:
+        x = torch.randn((b, n // 2 + 1), dtype=torch.complex64, device=gpu, generator=g)
+    y = execute_fft_plan(plan, x)
+    rows = [0, 1, b // 2, (1 << 24) - 1, 1 << 24, b - 1]
+    xs = x[rows].cpu().numpy()
+    ref = np.fft.rfft(xs.astype(np.float64)) if tt == "r2c" else np.fft.irfft(xs.astype(np.complex128), n=n)
+    check(y[rows].cpu().numpy(), ref, f"M0 {tt} N={n} B={b}")
+    del x, y
+
+
 def test_native_rejects_oversized_batch(gpu):
     """Plans cover at most 2^40 bytes of complex64 rows (no byte count can
     overflow), and no launch of 2^32 work-items or more (one dispatch's
