@@ -56,8 +56,10 @@ def test_struct_layouts():
     (dict(n=1024, batch=1 << 26, flow=native.FLOW_LDS_FUSED), "dispatch"),
     (dict(n=1 << 20, batch=1 << 17, flow=native.FLOW_FOUR_STEP, params=(1024,)), "dispatch"),
     (dict(n=1 << 14, batch=1 << 23, flow=native.FLOW_DENSE_MFMA), "dispatch"),
-    # the stitch launch, not the 4-point core, is the one that would not fit
-    (dict(n=8, batch=(1 << 24) + 1, transform_type="r2c", flow=native.FLOW_RADIX2_DIT), "dispatch"),
+    # the stitch launch, not the 4-point core, is the one that would not fit:
+    # one thread per mirror pair (3 a row at n = 8) past the limit, while the
+    # radix-2 stages (2 threads a row) still fit
+    (dict(n=8, batch=0x55555556, transform_type="r2c", flow=native.FLOW_RADIX2_DIT), "dispatch"),
 ])
 def test_plan_create_rejects_before_device_work(kwargs, match):
     if not os.path.exists(native.LIB_PATH):
