@@ -123,7 +123,7 @@ def real_keys(name: str, grid: int, real_sizes) -> list:
     bench.py's real-transform leg (``real_per_size``): the LDS kernel's R2C
     (mode 1) and C2R (mode 2) instances, the four-step passes over the
     half-length core, and the standalone stitch / pre-twiddle kernels (one
-    thread per mirror pair, 256-thread blocks per row)."""
+    thread per mirror pair over the flat batch, in 256-thread blocks)."""
     keys = []
     t = _template_args(name)
     for s in real_sizes:
@@ -157,10 +157,10 @@ def real_keys(name: str, grid: int, real_sizes) -> list:
             # around a non-fused core: once per execute, or once per chunk of
             # a chunked four-step core
             want = "r2c" if name.startswith("r2c") else "c2r"
-            bpr = ((core >> 1) + 1 + 255) // 256
+            pairs = (core >> 1) + 1
             rows = s["split"][2] if s.get("split") else b
             for r in sorted({b, rows}):
-                if tt == want and grid == bpr * r * 256:
+                if tt == want and grid == (r * pairs + 255) // 256 * 256:
                     keys.append(f"{tt} {name}|N={n}|rows={r}")
     return keys
 

@@ -83,12 +83,13 @@ def test_stats_labels_real_transform_launches(tmp_path):
     r2c = "void mfft::(anonymous namespace)::lds_fft_kernel<9, 4, -1, 1>(void const*, void*, float)"
     p1 = "void mfft::(anonymous namespace)::fourstep_r2c_pass1_kernel<8, 4, 4>(float2 const*, int)"
     plain = "void mfft::(anonymous namespace)::fourstep_pass_kernel<8, 4, 4, -1, 0>(float2 const*, int)"
-    st = "void mfft::(anonymous namespace)::r2c_stitch_kernel(float2 const*, float2*, float2 const*, long, int, float)"
+    st = ("void mfft::(anonymous namespace)::r2c_stitch_kernel(float2 const*, float2*, float2 const*, long, "
+          "unsigned int, float)")
     n_lds, b_lds = 1024, 32768           # core 512: 2^24 points, 16 per thread
     n_fs, b_fs = 1 << 16, 512            # core 2^15 = 256 x 128
-    bpr = ((n_fs // 4) + 1 + 255) // 256
+    pairs = n_fs // 4 + 1                # one stitch thread per mirror pair of the core, flat over the batch
     rows = [(r2c, (n_lds // 2) * b_lds // 16, 50_000), (p1, (n_fs // 2) * b_fs // 16, 60_000),
-            (st, bpr * b_fs * 256, 53_000), (plain, (n_fs // 2) * b_fs // 16, 61_000)]
+            (st, (pairs * b_fs + 255) // 256 * 256, 53_000), (plain, (n_fs // 2) * b_fs // 16, 61_000)]
     with open(d / "run_kernel_trace.csv", "w", newline="") as f:
         w = csv.writer(f)
         w.writerow(["Kernel_Name", "Start_Timestamp", "End_Timestamp", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z"])
