@@ -526,7 +526,8 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
         const int64_t here = rows - (int64_t)blockIdx.x * C::TPB;
         static_for<0, E>([&](auto r) {
             const int k = tid + r.value * C::WG;
-            if ((k >> LOGL) < here) store_out<WT>(dst + k, cscale(lds[(k >> LOGL) * C::PITCH + pad(k & (L - 1))], scale));
+            if ((k >> LOGL) < here)
+                store_out<WT>(dst + k, cscale(lds[(k >> LOGL) * C::PITCH + pad(k & (L - 1))], scale));
         });
     } else {
         constexpr int LR = C::logr(P - 1);
@@ -537,7 +538,9 @@ __global__ __launch_bounds__((LdsCfg<LOGL, LOGE, MODE>::WG), (LdsCfg<LOGL, LOGE,
         if (active) {
             static_for<0, NB>([&](auto m) {
                 const int b = j + m.value * T;
-                static_for<0, R>([&](auto q) { store_out<WT>(dst + b + q.value * NS, cscale(v[m.value * R + q.value], scale)); });
+                static_for<0, R>([&](auto q) {
+                    store_out<WT>(dst + b + q.value * NS, cscale(v[m.value * R + q.value], scale));
+                });
             });
         }
     }
