@@ -9,17 +9,24 @@ the dense-dot matrix-core flow (the reference's M2 FFT64 on fp32 MFMA), the
 single-pass LDS kernel at each elements-per-thread setting (and start
 stagger, where it can act), and the four-step at each split, chunking,
 schedule (one column group per workgroup, persistent workgroups, or narrow
-4-column groups for small batches) and pass-2 row order.  The fastest challenger is promoted
-only when it beats the incumbent by at least GUARD_PCT percent (M0 closure);
-otherwise the cell keeps M0.  The table is bound to the device profile hash
-and the live environment fingerprint, so it selects only on the stack it was
-measured on.
+4-column groups for small batches) and pass-2 row order.  The fastest
+challenger is promoted only when it beats the incumbent by at least
+GUARD_PCT percent (M0 closure); otherwise the cell keeps M0.  The table is
+bound to the device profile hash and the live environment fingerprint, so it
+selects only on the stack it was measured on.
 
-The roofline rows (N = 2^10..2^20, B = max(64, 2^25/N), and twice that
-batch, where a real launch moves the C2C row's bytes) are also measured for
-R2C forward and C2R inverse with the default norm, against the M0 real flow,
-and stored as exact-semantic entries: the real modes of the LDS kernel and
-the four-step around a half-length core have their own best settings.
+The cells are the reference's config-5 sweep, the roofline rows and every
+power-of-two batch of every power-of-two N = 16..2^20 up to 2^30 elements.
+Above 2^27 elements a cell times the M0 incumbent and the PRUNE_KEEP fastest
+challengers of the same N at 2^27 only (these cells run last).  A plan the
+library refuses at a shape (past one dispatch's 2^32 work-items) is no
+candidate, and where the refused plan is M0 the best challenger is promoted.
+
+The same cells, and the roofline rows at twice their batch (where a real
+launch moves the C2C row's bytes), are also measured for R2C forward and C2R
+inverse with the default norm, against the M0 real flow, and stored as
+exact-semantic entries: the real modes of the LDS kernel and the four-step
+around a half-length core have their own best settings.
 
 A rebuild never silently regresses a cell the deployed table won: every
 cell whose decision changed is re-timed against the previous decision,
