@@ -271,6 +271,28 @@ def test_shipped_table_loads_and_binds_this_profile():
     assert t["precision"] == "fp32"
 
 
+M0_NAMES = {"fft_dit", "fft_dit_batch", "fft_dif", "fft_dif_batch"}
+
+
+def test_shipped_table_covers_the_grid():
+    """Every power-of-two batch of every power-of-two N = 16 .. 2^20 up to
+    2^30 elements has a C2C entry for both decompositions and an exact R2C
+    and C2R entry, each a promoted challenger (no cell of the grid keeps M0,
+    so no power-of-two batch of these N runs the radix-2 baseline)."""
+    t = load_table()
+    have = {}
+    for e in t["entries"]:
+        key = (e["N"], e["batch"], e["direction"], e.get("transform_type", "c2c"))
+        assert key not in have, key
+        have[key] = e["executed"]
+    for k in range(4, 21):
+        for j in range(0, 31 - k):
+            n, b = 1 << k, 1 << j
+            for key in ((n, b, "dit", "c2c"), (n, b, "dif", "c2c"), (n, b, "dit", "r2c"), (n, b, "dit", "c2r")):
+                assert key in have, key
+                assert have[key] not in M0_NAMES, (key, have[key])
+
+
 def test_select_abstains_without_profile():
     s = select("dit", 2048, table=_table([_entry()]), env_hash=ENV)
     assert not s.selected and "profile_hash is required" in s.reason
