@@ -110,6 +110,26 @@ def load_composition_table(path: str = TABLE_PATH):
     return table
 
 
+_DEFAULT: dict = {}  # path -> ((mtime_ns, size), table or None) for plan-time lookups
+
+
+def _default_composition_table(path: str = TABLE_PATH):
+    """load_composition_table(path), re-read only when the file's modification
+    time or size changes (planning queries it on every call); the returned
+    dict is shared and is only read."""
+    try:
+        st = os.stat(path)
+    except OSError:
+        return load_composition_table(path)  # None, or the loader's error
+    stamp = (st.st_mtime_ns, st.st_size)
+    hit = _DEFAULT.get(path)
+    if hit is not None and hit[0] == stamp:
+        return hit[1]
+    table = load_composition_table(path)
+    _DEFAULT[path] = (stamp, table)
+    return table
+
+
 CORES_PATH = os.path.join(CONFIG_DIR, "external_cores.json")
 EXTERNAL_CORES_PATH = CORES_PATH  # the reference's name
 CLASSIFICATIONS = ("local-core", "materialized-external-subtransform", "full-transform-only", "boundary",
@@ -162,7 +182,7 @@ def composition_select(direction: str, n: int, batch: int = 1, precision: str = 
     if (transform_type, transform_direction, normalization) != ("c2c", "forward", "backward"):
         return None
     if table is None:
-        table = load_composition_table()
+        table = _default_composition_table()
         if table is None:
             return None
     if precision != table.get("precision"):

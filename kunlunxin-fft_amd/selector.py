@@ -197,10 +197,38 @@ def is_previous_fallback(table: dict, entry: dict) -> bool:
     return any(entry is e for e in (table.get("previous_fallbacks") or ()))
 
 
+def _cell_index(table: dict) -> tuple:
+    """(fallbacks, entries): the previous-fallback cells by (N, batch,
+    direction, semantic key), first of each kept, and the entries by (N,
+    batch, direction), in table order."""
+    fb, ent = {}, {}
+    for e in table.get("previous_fallbacks") or ():
+        fb.setdefault((e["N"], e["batch"], e["direction"], semantic_key_of(e)), e)
+    for e in table.get("entries", ()):
+        ent.setdefault((e["N"], e["batch"], e["direction"]), []).append(e)
+    return fb, ent
+
+
 def find_entry(table: dict, n: int, batch: int, direction: str, transform_type: str = "c2c",
                transform_direction: str = "forward", normalization: str = "backward"):
     """previous-fallback cell > exact semantic entry > legacy entry > None."""
     want = (transform_type, transform_direction, normalization)
+    idx = _INDEX.get(id(table))
+    if idx is not None and idx[0] is table:
+        # the package's shared table (default_table): indexed once per file
+        # version, the same answer as the scan below
+        fb, ent = idx[1]
+        hit = fb.get((n, batch, direction, want))
+        if hit is not None:
+            return hit
+        legacy = None
+        for e in ent.get((n, batch, direction), ()):
+            sk = semantic_key_of(e)
+            if sk == want:
+                return e
+            if sk is None and legacy is None:
+                legacy = e
+        return legacy
     for e in table.get("previous_fallbacks") or ():
         if (e["N"], e["batch"], e["direction"]) == (n, batch, direction) and semantic_key_of(e) == want:
             return e
@@ -288,6 +316,7 @@ def load_table(path: str = TABLE_PATH) -> dict:
 
 
 _DEFAULT: dict = {}  # path -> ((mtime_ns, size), validated table) for plan-time lookups
+_INDEX: dict = {}  # id(table) -> (table, _cell_index(table)) for the tables default_table shares
 
 
 def default_table(path: str = TABLE_PATH) -> dict:
@@ -304,7 +333,11 @@ def default_table(path: str = TABLE_PATH) -> dict:
     if hit is not None and hit[0] == stamp:
         return hit[1]
     table = load_table(path)
+    old = _DEFAULT.get(path)
+    if old is not None:
+        _INDEX.pop(id(old[1]), None)
     _DEFAULT[path] = (stamp, table)
+    _INDEX[id(table)] = (table, _cell_index(table))
     return table
 
 

@@ -271,6 +271,26 @@ def test_shipped_table_loads_and_binds_this_profile():
     assert t["precision"] == "fp32"
 
 
+def test_indexed_lookup_equals_the_scan():
+    """find_entry on the package's shared table (indexed once per file
+    version) answers exactly as the scan over an unindexed copy, for every
+    cell and semantic, previous-fallback cells included."""
+    import copy
+
+    from kunlunxin_fft_amd.selector import default_table, find_entry
+
+    shared = default_table()
+    plain = copy.deepcopy(shared)
+    sems = [("c2c", "forward", "backward"), ("c2c", "inverse", "ortho"), ("r2c", "forward", "backward"),
+            ("c2r", "inverse", "backward"), ("r2c", "forward", "ortho")]
+    cells = {(e["N"], e["batch"], e["direction"]) for e in shared["entries"] + shared.get("previous_fallbacks", [])}
+    cells |= {(3000, 1, "dit"), (1024, 3, "dit")}
+    for n, b, d in sorted(cells):
+        for sem in sems:
+            got, want = find_entry(shared, n, b, d, *sem), find_entry(plain, n, b, d, *sem)
+            assert (got is None) == (want is None) and (got is None or got == want), (n, b, d, sem)
+
+
 M0_NAMES = {"fft_dit", "fft_dit_batch", "fft_dif", "fft_dif_batch"}
 
 
@@ -469,3 +489,37 @@ def test_default_table_is_read_once_per_file_version(tmp_path):
     path.write_text("{}")
     with pytest.raises(ConfigError):
         selector.default_table(str(path))
+
+
+def test_composition_table_is_read_once_per_file_version(tmp_path):
+    """composition_select reuses the validated composition table until the
+    file changes, and the new version's entries then answer (an index of the
+    shared selector table follows its file version too)."""
+    import json
+    import os
+
+    from kunlunxin_fft_amd import composition, selector
+
+    path = tmp_path / "c.json"
+    path.write_text(open(composition.TABLE_PATH).read())
+    a = composition._default_composition_table(str(path))
+    assert composition._default_composition_table(str(path)) is a
+    assert composition.load_composition_table(str(path)) is not a
+    t = json.loads(path.read_text())
+    t["measurements"] = t["measurements"][:2]
+    path.write_text(json.dumps(t))
+    os.utime(path, ns=(1, 1))
+    b = composition._default_composition_table(str(path))
+    assert b is not a and len(b["measurements"]) == 2
+    assert composition._default_composition_table(str(tmp_path / "missing.json")) is None
+    # the selector's index is dropped with the table version it belonged to
+    sp = tmp_path / "t.json"
+    sp.write_text(open(selector.TABLE_PATH).read())
+    old = selector.default_table(str(sp))
+    assert id(old) in selector._INDEX
+    t = json.loads(sp.read_text())
+    t["entries"] = t["entries"][:3]
+    sp.write_text(json.dumps(t))
+    os.utime(sp, ns=(2, 2))
+    new = selector.default_table(str(sp))
+    assert selector._INDEX.get(id(old), (None,))[0] is not old and selector._INDEX[id(new)][0] is new
