@@ -16,9 +16,9 @@ bound to the device profile hash and the live environment fingerprint, so it
 selects only on the stack it was measured on.
 
 The cells are the reference's config-5 sweep, the roofline rows and every
-power-of-two batch of every power-of-two N = 16..2^20 up to 2^30 elements.
-Above 2^27 elements a cell times the M0 incumbent and the PRUNE_KEEP fastest
-challengers of the same N at 2^27 only (these cells run last).  A plan the
+power-of-two batch of every power-of-two N = 16..2^20 up to 2^32 elements.
+Above 2^27 elements a cell times the PRUNE_KEEP fastest challengers of the
+same N at 2^27 only, and the M0 incumbent 3 times (these cells run last).  A plan the
 library refuses at a shape (past one dispatch's 2^32 work-items) is no
 candidate, and where the refused plan is M0 the best challenger is promoted.
 
@@ -65,15 +65,16 @@ C5_BATCHES = [1, 16, 64, 256]
 ROOF_SIZES = [1 << k for k in range(10, 21)]      # roofline rows: B = max(64, 2^25/N)
 EXTRA_CELLS = [(1 << k, 1) for k in range(15, 21)] + [(1 << 16, 256), (256, 1), (4096, 64)]
 # Every power-of-two batch of every power-of-two N from 16 to 2^20, up to
-# 2^30 elements (8 GiB of complex64 per buffer): the table answers exact
+# 2^32 elements (32 GiB of complex64 per buffer): the table answers exact
 # (N, batch) keys only, and a shape it does not hold runs the radix-2
 # baseline, one launch per stage (at N = 2^20, B = 2, 7x the four-step's time).
-DENSE_MAX_LOG_ELEMS = 30
-# Above 2^27 elements a cell times the M0 incumbent and only the PRUNE_KEEP
-# fastest challengers of the same N (and direction or real semantic) at
-# 2^27 elements: every launch there streams whole waves of workgroups, so
-# the ranking of the 2^27 cell holds, and timing every challenger at up to
-# 8 GiB per buffer would take most of an hour.  These cells are built last.
+DENSE_MAX_LOG_ELEMS = 32
+# Above 2^27 elements a cell times only the PRUNE_KEEP fastest challengers of
+# the same N (and direction or real semantic) at 2^27 elements, and the M0
+# incumbent 3 times after one warm-up (it is several times slower there, far
+# outside the 2% guard): every launch streams whole waves of workgroups, so
+# the ranking of the 2^27 cell holds, and timing everything at up to 32 GiB
+# per buffer would take hours.  These cells are built last.
 PRUNE_LOG_ELEMS = 27
 PRUNE_KEEP = 3
 DENSE_LOG_N = range(4, 21)
@@ -456,7 +457,7 @@ def main() -> int:
     # timed back to back: they live in the MALL in any use.
     flush = torch.empty(1 << 26, dtype=torch.float32, device=dev)  # 256 MiB
 
-    def time_runner(name, n, b, block, params, x, tt="c2c", td="forward"):
+    def time_runner(name, n, b, block, params, x, tt="c2c", td="forward", few=False):
         try:
             np_ = get_native_plan(name, n, b, tt, td, "backward", block, params, 0)
         except ValueError as exc:
@@ -472,12 +473,13 @@ def main() -> int:
         def execute():
             np_.execute_ws(x.data_ptr(), out.data_ptr(), wp, np_.ws_bytes, stream.cuda_stream)
 
-        for _ in range(3):
+        for _ in range(1 if few else 3):
             execute()
         res = []
         if n * b * (8 if tt == "c2c" else 4) >= (64 << 20):
-            for _ in range(args.rounds):
-                for _ in range(max(3, args.reps // 4)):
+            # few: the M0 incumbent of a pruned cell, 3 timings
+            for _ in range(1 if few else args.rounds):
+                for _ in range(3 if few else max(3, args.reps // 4)):
                     flush.fill_(1.0)
                     s = torch.cuda.Event(enable_timing=True)
                     e = torch.cuda.Event(enable_timing=True)
@@ -521,7 +523,8 @@ def main() -> int:
         x = torch.randn(shape, dtype=torch.complex64, device=dev, generator=gen)
         for direction in ("dit", "dif"):
             inc_name = ("fft_dit" if direction == "dit" else "fft_dif") + ("" if b == 1 else "_batch")
-            inc_ms = time_runner(inc_name, n, b, 256, {}, x) if n >= 2 else float("inf")
+            inc_ms = (time_runner(inc_name, n, b, 256, {}, x, few=n * b > (1 << PRUNE_LOG_ELEMS))
+                      if n >= 2 else float("inf"))
             row = {"N": n, "batch": b, "direction": direction, f"m0_{direction}@256": _ms(inc_ms)}
             timed = []
             for label, name, block, params, fam in pruned(candidates(n, b, direction, space), n, b,
@@ -569,7 +572,7 @@ def main() -> int:
             else:
                 x = torch.randn((b, n // 2 + 1), dtype=torch.complex64, device=dev, generator=gen)
             inc_name = "fft_dit" if b == 1 else "fft_dit_batch"
-            inc_ms = time_runner(inc_name, n, b, 256, {}, x, tt, td)
+            inc_ms = time_runner(inc_name, n, b, 256, {}, x, tt, td, few=n * b > (1 << PRUNE_LOG_ELEMS))
             row = {"N": n, "batch": b, "direction": "dit", "transform_type": tt, "m0_dit@256": _ms(inc_ms)}
             timed = []
             for label, name, block, params, fam in pruned(real_candidates(n, b, tt, space), n, b, (n, tt), top):
@@ -610,8 +613,8 @@ def main() -> int:
                                "forward C2C complex64 (legacy entries, answering every semantic), plus "
                                "exact-semantic R2C / C2R entries (norm backward); cells: the reference's "
                                "config-5 sweep, the roofline rows and every power-of-two batch of every "
-                               "power-of-two N = 16 .. 2^20 up to 2^30 elements (above 2^27: the M0 "
-                               "incumbent and the 3 fastest challengers of the same N at 2^27)",
+                               "power-of-two N = 16 .. 2^20 up to 2^32 elements (above 2^27: the 3 fastest "
+                               "challengers of the same N at 2^27, and M0 timed 3 times)",
         "sources": ["kunlunxin-fft_amd/table_builder.py live sweep"],
         "entries": entries, "previous_fallbacks": [],
     }

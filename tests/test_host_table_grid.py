@@ -1,5 +1,5 @@
 """The table builder's cell grid (no GPU): every power-of-two batch of every
-power-of-two N = 16 .. 2^20 up to 2^30 elements, the cells above 2^27
+power-of-two N = 16 .. 2^20 up to 2^32 elements, the cells above 2^27
 elements built after all the others, and there only the three fastest
 challengers of the same N at 2^27 elements timed (with the M0 incumbent)."""
 import pytest
@@ -8,13 +8,13 @@ from kunlunxin_fft_amd import table_builder as tb
 from kunlunxin_fft_amd.config import DesignSpace
 
 
-def test_grid_covers_every_power_of_two_batch_up_to_2_30_elements():
+def test_grid_covers_every_power_of_two_batch_up_to_2_32_elements():
     for cells in (tb.cells(), tb.real_cells()):
         have = set(cells)
         for k in range(4, 21):
-            for j in range(0, 31 - k):
+            for j in range(0, 33 - k):
                 assert (1 << k, 1 << j) in have, (k, j)
-        assert max(n * b for n, b in cells) == 1 << 30
+        assert max(n * b for n, b in cells) == 1 << 32
         assert len(cells) == len(have)  # no cell twice
 
 
