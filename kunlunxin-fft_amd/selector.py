@@ -198,15 +198,42 @@ def is_previous_fallback(table: dict, entry: dict) -> bool:
 
 
 def _cell_index(table: dict) -> tuple:
-    """(fallbacks, entries): the previous-fallback cells by (N, batch,
-    direction, semantic key), first of each kept, and the entries by (N,
-    batch, direction), in table order."""
-    fb, ent = {}, {}
+    """(fallbacks, entries, batches): the previous-fallback cells by (N,
+    batch, direction, semantic key), first of each kept; the entries by (N,
+    batch, direction), in table order; the sorted batches of the entries by
+    (N, direction)."""
+    fb, ent, bat = {}, {}, {}
     for e in table.get("previous_fallbacks") or ():
         fb.setdefault((e["N"], e["batch"], e["direction"], semantic_key_of(e)), e)
     for e in table.get("entries", ()):
         ent.setdefault((e["N"], e["batch"], e["direction"]), []).append(e)
-    return fb, ent
+        bat.setdefault((e["N"], e["direction"]), set()).add(e["batch"])
+    return fb, ent, {k: sorted(v) for k, v in bat.items()}
+
+
+def _table_batches(table: dict, n: int, direction: str) -> list:
+    """Sorted batches the table holds entries for at (N, direction)."""
+    idx = _INDEX.get(id(table))
+    if idx is not None and idx[0] is table:
+        return idx[1][2].get((n, direction), [])
+    return sorted({e["batch"] for e in table.get("entries", ()) if (e["N"], e["direction"]) == (n, direction)})
+
+
+def rounded_batch(table: dict, n: int, batch: int, direction: str, transform_type: str = "c2c",
+                  transform_direction: str = "forward", normalization: str = "backward"):
+    """The table batch whose measured decision a batch with no exact key
+    takes: the smallest table batch at or above it (the next power of two,
+    on a grid of powers of two), or past the table's largest batch of this N
+    that largest one; None when no batch of this N, direction and semantic
+    has an entry."""
+    sem = (transform_type, transform_direction, normalization)
+    # batched entries only for a batch above 1 (their runners are the batch forms)
+    have = [b for b in _table_batches(table, n, direction)
+            if (b > 1 or batch == 1) and find_entry(table, n, b, direction, *sem) is not None]
+    if not have:
+        return None
+    above = [b for b in have if b >= batch]
+    return above[0] if above else have[-1]
 
 
 def find_entry(table: dict, n: int, batch: int, direction: str, transform_type: str = "c2c",
@@ -217,7 +244,7 @@ def find_entry(table: dict, n: int, batch: int, direction: str, transform_type: 
     if idx is not None and idx[0] is table:
         # the package's shared table (default_table): indexed once per file
         # version, the same answer as the scan below
-        fb, ent = idx[1]
+        fb, ent = idx[1][0], idx[1][1]
         hit = fb.get((n, batch, direction, want))
         if hit is not None:
             return hit
@@ -410,6 +437,13 @@ def select(direction: str, n: int, batch: int = 1, precision: str = "fp32",
         return no(f"environment hash {cur} != table {bound} (device/runtime changed since "
                   "the table was built); re-measure before selecting")
     e = find_entry(table, n, batch, direction, *sem)
+    rounded = None
+    if e is None and batch > 1:
+        # no exact key (a batch that is not a power of two, or past the grid):
+        # the measured decision of the nearest table batch of this N
+        rounded = rounded_batch(table, n, batch, direction, *sem)
+        if rounded is not None:
+            e = find_entry(table, n, rounded, direction, *sem)
     if e is None:
         return no(f"no measured entry for N={n} batch={batch} direction={direction} "
                   f"semantic={transform_type}/{transform_direction}/{normalization}; fall back to M0")
@@ -419,6 +453,10 @@ def select(direction: str, n: int, batch: int = 1, precision: str = "fp32",
     else:
         tier = "semantic" if semantic_key_of(e) is not None else "legacy"
         reason = e.get("reason", "measured confirmation winner")
+    if rounded is not None:
+        reason = (f"no entry for batch={batch}; the measured decision of batch={rounded} ({tier} entry) "
+                  f"applies: {reason}")
+        tier = "batch-rounded"
     return Selection(
         n=n, direction=direction, batch=batch, precision=precision, source="table", reason=reason,
         transform_type=transform_type, transform_direction=transform_direction,

@@ -742,17 +742,15 @@ def test_input_validation_raises_before_launch(gpu):
 
 
 @pytest.mark.parametrize("tt", ["r2c", "c2r"])
-def test_real_fallback_for_a_huge_odd_batch_of_short_rows(gpu, tt):
-    """A batch that is not a power of two runs M0 (the table answers exact
-    keys); its real stitch / pre-twiddle runs one thread per mirror pair over
-    the flat batch, so N = 16 at B = 3 * 2^23 + 1 (past 2^24 rows, where a
-    block per row would need more than one dispatch's 2^32 work-items) plans
-    and matches numpy on the first, a middle and the last rows."""
+def test_real_m0_for_a_huge_odd_batch_of_short_rows(gpu, tt):
+    """M0 (the closed fallback) on real rows: its stitch / pre-twiddle runs
+    one thread per mirror pair over the flat batch, so N = 16 at
+    B = 3 * 2^23 + 1 (past 2^24 rows, where a block per row would need more
+    than one dispatch's 2^32 work-items) plans and matches numpy on the
+    first, a middle and the last rows."""
     n, b = 16, 3 * (1 << 23) + 1
     td = "inverse" if tt == "c2r" else "forward"
-    plan = plan_fft("dit", n, batch=b, transform_type=tt, transform_direction=td,
-                    profile_hash=DeviceProfile.load().hash())
-    assert plan.fallback and plan.executed == "fft_dit_batch", plan.reason
+    plan = mkplan("fft_dit_batch", n, b, tt=tt, td=td)
     print(f"huge odd batch {tt}: N={n} B={b}", flush=True)
     g = torch.Generator(gpu).manual_seed(11)
     if tt == "r2c":
@@ -764,6 +762,49 @@ def test_real_fallback_for_a_huge_odd_batch_of_short_rows(gpu, tt):
     xs = x[rows].cpu().numpy()
     ref = np.fft.rfft(xs.astype(np.float64)) if tt == "r2c" else np.fft.irfft(xs.astype(np.complex128), n=n)
     check(y[rows].cpu().numpy(), ref, f"M0 {tt} N={n} B={b}")
+    del x, y
+
+
+ROUND_CASES = [(16, 3, "c2c"), (1024, 100, "c2c"), (1024, 1000, "r2c"), (4096, 100, "c2r"), (1 << 15, 5, "c2c"),
+               (1 << 16, 7, "r2c"), (1 << 18, 3, "c2r"), (1 << 20, 3, "c2c"), (256, 70000, "c2c"),
+               (1 << 20, 5000, "c2c")]
+
+
+@pytest.mark.parametrize("n,b,tt", ROUND_CASES, ids=[f"N{n}-B{b}-{tt}" for n, b, tt in ROUND_CASES])
+def test_batch_without_exact_key_runs_the_rounded_decision(gpu, n, b, tt):
+    """plan_fft for a batch the table holds no key for (not a power of two,
+    or past its 2^32-element grid: N = 2^20, B = 5000) takes the decision of
+    the next power-of-two batch of the same N and semantic (or the largest
+    one), and runs it correctly on the ragged batch: the first, a middle and
+    the last rows against numpy."""
+    from kunlunxin_fft_amd.selector import default_table, find_entry, rounded_batch
+
+    td = "inverse" if tt == "c2r" else "forward"
+    prof = DeviceProfile.load().hash()
+    plan = plan_fft("dit", n, batch=b, transform_type=tt, transform_direction=td, profile_hash=prof)
+    t = default_table()
+    rb = rounded_batch(t, n, b, "dit", tt, td, "backward")
+    e = find_entry(t, n, rb, "dit", tt, td, "backward")
+    assert not plan.fallback and plan.selection_source == "table" and f"batch={rb}" in plan.reason, plan.reason
+    assert plan.executed == e["executed"]
+    print(f"rounded batch: N={n} B={b} {tt} -> table batch {rb} ({plan.executed})", flush=True)
+    g = torch.Generator(gpu).manual_seed(n + b)
+    if tt == "r2c":
+        x = torch.randn((b, n), dtype=torch.float32, device=gpu, generator=g)
+    elif tt == "c2r":
+        x = torch.randn((b, n // 2 + 1), dtype=torch.complex64, device=gpu, generator=g)
+    else:
+        x = torch.randn((b, n), dtype=torch.complex64, device=gpu, generator=g)
+    y = execute_fft_plan(plan, x)
+    rows = sorted({0, b // 2, b - 1})
+    h = x[rows].cpu().numpy()
+    if tt == "r2c":
+        ref = np.fft.rfft(h.astype(np.float64))
+    elif tt == "c2r":
+        ref = np.fft.irfft(h.astype(np.complex128), n=n)
+    else:
+        ref = np.fft.fft(h.astype(np.complex128))
+    check(y[rows].cpu().numpy(), ref, f"rounded N={n} B={b} {tt}")
     del x, y
 
 

@@ -129,6 +129,62 @@ def test_plan_falls_back_on_unknown_n():
     assert "no measured entry" in plan.reason
 
 
+def test_plan_rounds_a_batch_without_exact_key():
+    """A batch with no exact key (not a power of two, or past the table's
+    grid) takes the measured decision of the smallest table batch at or
+    above it, or past the largest batch of this N, the largest: entry tier
+    batch-rounded, source table, the rounding in the reason.  Batch 1
+    entries never answer a batch above 1; unknown N, a profile or
+    environment mismatch still abstain."""
+    t = _table([_entry(2048, 1, "dit", executed="fft_lds_fused", params={"elems": 8}),
+                _entry(2048, 64, "dit", executed="fft_lds_fused_batch", params={"elems": 16}),
+                _entry(2048, 128, "dit", executed="fft_four_step_batch", real="four-step",
+                       params={"n1": 64})])
+    for batch, want, rounded in ((100, "fft_four_step_batch", 128), (65, "fft_four_step_batch", 128),
+                                 (3, "fft_lds_fused_batch", 64), (63, "fft_lds_fused_batch", 64),
+                                 (1000, "fft_four_step_batch", 128), (256, "fft_four_step_batch", 128)):
+        sel = select("dit", 2048, batch=batch, profile_hash=PROF, table=t, env_hash=ENV)
+        assert sel.source == "table" and sel.entry_tier == "batch-rounded", (batch, sel.reason)
+        assert sel.executed == want and f"batch={rounded}" in sel.reason, (batch, sel.reason)
+        plan = plan_fft("dit", 2048, batch=batch, profile_hash=PROF, table=t, env_hash=ENV)
+        assert not plan.fallback and plan.executed == want and plan.batch == batch
+    # exact keys answer as before
+    assert select("dit", 2048, batch=64, profile_hash=PROF, table=t, env_hash=ENV).entry_tier == "legacy"
+    # no entry of this N, or a binding mismatch: abstain
+    assert plan_fft("dit", 4096, batch=100, profile_hash=PROF, table=t, env_hash=ENV).fallback
+    assert plan_fft("dit", 2048, batch=100, profile_hash="f" * 16, table=t, env_hash=ENV).fallback
+    assert plan_fft("dit", 2048, batch=100, profile_hash=PROF, table=t, env_hash="0" * 16).fallback
+    # the other decomposition has no entries here
+    assert plan_fft("dif", 2048, batch=100, profile_hash=PROF, table=t, env_hash=ENV).fallback
+    # only a batch-1 entry: a batch above 1 abstains
+    only1 = _table([_entry(2048, 1, "dit", executed="fft_lds_fused")])
+    assert plan_fft("dit", 2048, batch=5, profile_hash=PROF, table=only1, env_hash=ENV).fallback
+
+
+def test_rounding_on_the_shipped_table_matches_the_next_power_of_two():
+    """On the shipped table (indexed), an odd batch takes the next power of
+    two's entry for every semantic, and a batch past 2^32 elements the
+    largest batch's."""
+    from kunlunxin_fft_amd.selector import default_table, find_entry, rounded_batch
+
+    t = default_table()
+    for n in (16, 1024, 1 << 15, 1 << 20):
+        for batch in (3, 100, 1000):
+            for sem in (("c2c", "forward", "backward"), ("r2c", "forward", "backward"),
+                        ("c2r", "inverse", "backward")):
+                up = 1 << (batch - 1).bit_length()
+                if n * up > (1 << 32):
+                    continue
+                assert rounded_batch(t, n, batch, "dit", *sem) == up
+                sel = select("dit", n, batch=batch, profile_hash=t["profile_hash"], table=t,
+                             env_hash=t["env_hash"], transform_type=sem[0], transform_direction=sem[1])
+                e = find_entry(t, n, up, "dit", *sem)
+                assert sel.entry_tier == "batch-rounded" and sel.executed == e["executed"]
+                assert {k: v for k, v in sel.params.items()} == (e.get("params") or {})
+    biggest = (1 << 32) // (1 << 20)
+    assert rounded_batch(t, 1 << 20, 3 * biggest, "dit") == biggest
+
+
 def test_plan_falls_back_on_missing_profile():
     plan = plan_fft("dit", 2048, profile_hash=None, table=_table([_entry()]), env_hash=ENV)
     assert plan.fallback and plan.executed == "fft_dit"
