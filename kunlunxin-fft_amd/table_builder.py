@@ -211,10 +211,10 @@ def carry_previous_fallbacks(prev: "dict | None", prev_sha: "str | None", table:
     return fallbacks, drops, records
 
 
-def dense_cells():
-    """(N, batch) for every power-of-two batch up to 2^DENSE_MAX_LOG_ELEMS
+def dense_cells(max_log_elems: int = DENSE_MAX_LOG_ELEMS):
+    """(N, batch) for every power-of-two batch up to 2^max_log_elems
     elements, N = 16 .. 2^20."""
-    return [(1 << k, 1 << j) for k in DENSE_LOG_N for j in range(0, DENSE_MAX_LOG_ELEMS - k + 1)]
+    return [(1 << k, 1 << j) for k in DENSE_LOG_N for j in range(0, max_log_elems - k + 1)]
 
 
 def _unique(cells_):
@@ -226,13 +226,13 @@ def _unique(cells_):
     return out
 
 
-def real_cells():
+def real_cells(max_log_elems: int = DENSE_MAX_LOG_ELEMS):
     """(N, batch) of the exact-semantic real entries: the roofline rows'
     batch and twice it (the same bytes per launch as the C2C row, which
     bench.py's real rows use), then every dense cell."""
     return _large_last(_unique([(n, b) for n in ROOF_SIZES for b in (max(64, (1 << 25) // n),
                                                                      2 * max(64, (1 << 25) // n))]
-                               + dense_cells()))
+                               + dense_cells(max_log_elems)))
 
 
 def _large_last(cells_):
@@ -279,7 +279,7 @@ def record_top(timed, n: int, b: int, key, top: dict) -> None:
         top[key] = [t[1] for t in sorted(ok, key=lambda t: t[0])[:PRUNE_KEEP]]
 
 
-def cells(quick: bool = False):
+def cells(quick: bool = False, max_log_elems: int = DENSE_MAX_LOG_ELEMS):
     out = []
     for n in C5_SIZES:
         for b in C5_BATCHES:
@@ -287,7 +287,7 @@ def cells(quick: bool = False):
     for n in ROOF_SIZES:
         out.append((n, max(64, (1 << 25) // n)))
     out += EXTRA_CELLS
-    uniq = _large_last(_unique(out + dense_cells()))
+    uniq = _large_last(_unique(out + dense_cells(max_log_elems)))
     if quick:
         uniq = [c for c in uniq if c[0] * c[1] <= (1 << 22) or c[1] == 1]
     return uniq
@@ -418,6 +418,9 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--out", required=True)
     ap.add_argument("--quick", action="store_true")
+    ap.add_argument("--max-log-elems", type=int, default=DENSE_MAX_LOG_ELEMS,
+                    help="largest cell of the dense grid, log2 of N x batch (default %(default)s; a smaller "
+                         "grid builds faster, and batches past it take its largest batch's decision)")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--rounds", type=int, default=3)
     ap.add_argument("--previous", default=None,
@@ -518,7 +521,7 @@ def main() -> int:
     entries, sweep = [], []
     top = {}  # (n, direction or transform type) -> fastest labels at 2^PRUNE_LOG_ELEMS
     t_start = time.time()
-    for (n, b) in cells(args.quick):
+    for (n, b) in cells(args.quick, args.max_log_elems):
         shape = (n,) if b == 1 else (b, n)
         x = torch.randn(shape, dtype=torch.complex64, device=dev, generator=gen)
         for direction in ("dit", "dif"):
@@ -565,7 +568,7 @@ def main() -> int:
                   f"[{time.time() - t_start:.0f}s]", flush=True)
         del x
     # ---- real transforms at the roofline rows: exact-semantic entries
-    for n, b in ([] if args.quick else real_cells()):
+    for n, b in ([] if args.quick else real_cells(args.max_log_elems)):
         for tt, td in REAL_SEMANTICS:
             if tt == "r2c":
                 x = torch.randn((b, n), dtype=torch.float32, device=dev, generator=gen)

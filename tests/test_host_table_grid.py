@@ -72,3 +72,14 @@ def test_refused_plans_are_not_candidates():
     top = {}
     tb.record_top([(inf, "a"), (1.0, "b")], 16, (1 << 27) // 16, (16, "r2c"), top)
     assert top == {(16, "r2c"): ["b"]}
+
+
+def test_max_log_elems_bounds_the_grid():
+    """--max-log-elems 24: the dense grid stops at 2^24 elements (the config
+    sweep and roofline rows stay), for both the C2C and the real cells."""
+    for cells in (tb.cells(max_log_elems=24), tb.real_cells(max_log_elems=24)):
+        dense = {(n, b) for n, b in cells}
+        assert all((1 << k, 1 << j) in dense for k in range(4, 21) for j in range(0, 25 - k))
+        # past 2^24 only the roofline rows (real: at twice the batch, 2^27 at N = 2^20)
+        assert all(n * b <= 1 << 24 or n in tb.ROOF_SIZES for n, b in cells)
+        assert max(n * b for n, b in cells) <= 1 << 27
