@@ -360,7 +360,9 @@ __device__ __forceinline__ int pair_k1(int pos) { return pair_col<CP>(pos / (2 *
 // MAP 2 (C2R pass 1): lane column c is column pair_col(g, c, 2^log_s) (d = Z).
 // NTS (KIND 1): non-temporal stores, for output that nothing in this launch
 // reads again (it then does not displace lines the launch still uses).
-template <class C, int KIND, int MAP = 0, bool NTS = false, int CP = 8>
+// WT: write-through stores (store_out) of whole lines; off for the fused
+// schedule's Z ring, which is meant to stay in the XCD's L2.
+template <class C, int KIND, int MAP = 0, bool NTS = false, int CP = 8, bool WT = true>
 __device__ __forceinline__ void col_store(const float2 (&v)[C::E], float2* d, float2* lds, int tid, int c, int j,
                                           int log_s, float scale, int g = 0) {
     if constexpr (KIND == 0) {
@@ -385,10 +387,10 @@ __device__ __forceinline__ void col_store(const float2 (&v)[C::E], float2* d, fl
                 const int k1 = e & (C::L - 1);
                 if constexpr (MAP == 2) {
                     const int col = pair_col<C::C / 2>(g, h.value * CH + cc, 1 << log_s);
-                    store_out<true>(d + ((int64_t)col << C::LOG_L) + k1, lds[cc * C::PITCH + pad(k1)]);
+                    store_out<WT>(d + ((int64_t)col << C::LOG_L) + k1, lds[cc * C::PITCH + pad(k1)]);
                 } else {
-                    store_out<true>(byte_off(dh + r.value * C::WG, (uint32_t)tid * 8u),
-                                    lds[cc * C::PITCH + pad(MAP == 1 ? pair_k1<C::L, CP>(k1) : k1)]);
+                    store_out<WT>(byte_off(dh + r.value * C::WG, (uint32_t)tid * 8u),
+                                  lds[cc * C::PITCH + pad(MAP == 1 ? pair_k1<C::L, CP>(k1) : k1)]);
                 }
             });
         });
@@ -403,7 +405,7 @@ __device__ __forceinline__ void col_store(const float2 (&v)[C::E], float2* d, fl
                 // columns or more; the narrow groups' 32-byte runs, written
                 // through, took the 2^20-point pass 2 from 7.4 to 9.8 us)
                 if constexpr (NTS) store_nt(a, x);
-                else store_out<(C::C >= 16)>(a, x);
+                else store_out<(WT && C::C >= 16)>(a, x);
             });
         });
     }
@@ -858,7 +860,7 @@ __global__ __launch_bounds__((ColCfg<LL1, LE1, LC1>::WG)) void fourstep_fused_ke
                 __syncthreads();
                 ok = 1 - __builtin_amdgcn_readfirstlane(fail_s);
             }
-            if (ok) col_store<A, 0>(v, zr + ((int64_t)c0 << LL1), lds, tl, c, j, LL2, 1.0f);
+            if (ok) col_store<A, 0, 0, false, 8, false>(v, zr + ((int64_t)c0 << LL1), lds, tl, c, j, LL2, 1.0f);
             __builtin_amdgcn_s_waitcnt(0);  // this thread's Z stores have reached L2
             __syncthreads();
             if (lead) atomicAdd(done1 + t, one * (ok ? 1 : 1 + kFusedFailMark));
