@@ -252,6 +252,8 @@ def plan_fft(direction: str, n: int, batch: int = 1, precision: str = "fp32",
     params = dict(sel.params or {})
     if sel.entry_tier == "previous-fallback":
         params["previous_fallback"] = True
+    if sel.entry_tier == "batch-rounded":
+        params["table_batch"] = sel.table_batch  # the measured batch whose decision this plan runs
     if params.get("real_flow"):
         from .semantic import family_allows
 

@@ -293,6 +293,7 @@ class Selection:
     incumbent_ms: float | None = None
     challenger_ms: float | None = None
     executed: str | None = None
+    table_batch: int | None = None  # entry tier batch-rounded: the table batch whose decision applies
 
     @property
     def selected(self) -> bool:
@@ -463,5 +464,5 @@ def select(direction: str, n: int, batch: int = 1, precision: str = "fp32",
         normalization=normalization, entry_tier=tier, block=e["block"], flow_id=e["flow_id"],
         flow_realization=e["flow_realization"], processing_unit=e["processing_unit"],
         params=dict(e.get("params") or {}), incumbent_ms=e.get("incumbent_ms"),
-        challenger_ms=e.get("challenger_ms"), executed=e.get("executed"),
+        challenger_ms=e.get("challenger_ms"), executed=e.get("executed"), table_batch=rounded,
     )

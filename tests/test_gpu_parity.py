@@ -786,7 +786,7 @@ def test_batch_without_exact_key_runs_the_rounded_decision(gpu, n, b, tt):
     rb = rounded_batch(t, n, b, "dit", tt, td, "backward")
     e = find_entry(t, n, rb, "dit", tt, td, "backward")
     assert not plan.fallback and plan.selection_source == "table" and f"batch={rb}" in plan.reason, plan.reason
-    assert plan.executed == e["executed"]
+    assert plan.executed == e["executed"] and plan.params["table_batch"] == rb
     print(f"rounded batch: N={n} B={b} {tt} -> table batch {rb} ({plan.executed})", flush=True)
     g = torch.Generator(gpu).manual_seed(n + b)
     if tt == "r2c":

@@ -148,8 +148,10 @@ def test_plan_rounds_a_batch_without_exact_key():
         assert sel.executed == want and f"batch={rounded}" in sel.reason, (batch, sel.reason)
         plan = plan_fft("dit", 2048, batch=batch, profile_hash=PROF, table=t, env_hash=ENV)
         assert not plan.fallback and plan.executed == want and plan.batch == batch
-    # exact keys answer as before
+        assert plan.params["table_batch"] == rounded == sel.table_batch
+    # exact keys answer as before, with no rounding marker
     assert select("dit", 2048, batch=64, profile_hash=PROF, table=t, env_hash=ENV).entry_tier == "legacy"
+    assert "table_batch" not in plan_fft("dit", 2048, batch=64, profile_hash=PROF, table=t, env_hash=ENV).params
     # no entry of this N, or a binding mismatch: abstain
     assert plan_fft("dit", 4096, batch=100, profile_hash=PROF, table=t, env_hash=ENV).fallback
     assert plan_fft("dit", 2048, batch=100, profile_hash="f" * 16, table=t, env_hash=ENV).fallback
